@@ -1,0 +1,240 @@
+"""Decode-attention throughput on the packed TurboQuant KV cache (MI355X).
+
+Workload (Qwen3-8B geometry): q fp16 [8, 32, 128],
+8 sequences x 32768 cached tokens, 8 KV heads, head_dim 128, 16-token pages
+assigned by a seeded random permutation of a 16384-page pool, split-KV + LSE
+merge.  One step = one decode-attention call (partials kernel + combine
+kernel) over the resident cache.  Also measured: the write kernel on
+configs[1] (8192 tokens x 8 heads, K and V, outlier channels, permuted slots).
+
+Prints ONE JSON line.  value = algorithmic bytes per step / step time, where
+algorithmic bytes = codes + norms of every (token, kv head, K|V) + page-table
+entries + q + o (285,409,280 B at this shape).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_decode_workload(torch, batch=8, seq_len=32768, hq=32, hkv=8, hd=128, seed=3):
+    """Device-resident cfg-3 workload; K/V written by the HIP write kernel."""
+    from turboquant_amd import ops
+    from turboquant_amd.geometry import choose_splits, entry_bytes, hadamard_signs
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    pd = hd
+    _, _, ebs = entry_bytes(hd)
+    pages_per_seq = seq_len // 16
+    nb = batch * pages_per_seq
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    bt = perm.view(batch, pages_per_seq).to(dev)
+    cache = torch.zeros((2, nb, 16, hkv, ebs), dtype=torch.uint8, device=dev)
+    signs = hadamard_signs(pd, dev)
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    chunk = 8192
+    t_all = torch.arange(seq_len, device=dev, dtype=torch.int32)
+    for b in range(batch):
+        for t0 in range(0, seq_len, chunk):
+            t = t_all[t0:t0 + chunk]
+            slots = (bt[b, t // 16] * 16 + t % 16).to(torch.int32)
+            k = torch.randn((len(t), hkv, hd), generator=gd, device=dev).half()
+            v = torch.randn((len(t), hkv, hd), generator=gd, device=dev).half()
+            ops.quantize_write_kv_cache(cache, k, v, signs, slots, hd, pd)
+    q = torch.randn((batch, hq, pd), generator=gd, device=dev).half()
+    seq = torch.full((batch,), seq_len, dtype=torch.int32, device=dev)
+    indices = bt.reshape(-1).contiguous()
+    indptr = (torch.arange(batch + 1, dtype=torch.int32, device=dev) * pages_per_seq)
+    splits, cs = choose_splits(batch, seq_len, hkv)
+    torch.cuda.synchronize()
+    return dict(cache=cache, q=q, seq=seq, indices=indices, indptr=indptr, bt=bt, signs=signs,
+                splits=splits, cs=cs, nb=nb, ebs=ebs, pd=pd, hd=hd, hq=hq, hkv=hkv,
+                batch=batch, seq_len=seq_len)
+
+
+def alg_bytes(w):
+    per = w["pd"] // 2 + 2 * (w["pd"] // 64)
+    b, L = w["batch"], w["seq_len"]
+    return b * L * w["hkv"] * 2 * per + b * math.ceil(L / 16) * 4 + 2 * b * w["hq"] * w["pd"] * 2
+
+
+def time_launches(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps  # ms
+
+
+def cpu_baseline(torch, w, budget_s=12.0):
+    """The C oracle (dequantize-then-attend, OpenMP) on the host cores, on a
+    bounded sample: whole sequences of the same workload, repeated until
+    `budget_s` of CPU time is spent; reported in the same GB/s unit."""
+    import numpy as np
+
+    import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    cache = w["cache"].cpu().numpy()
+    q = w["q"].cpu().numpy()
+    bt = w["bt"].cpu().numpy()
+    signs = w["signs"].cpu().numpy()
+    nseq = 2
+    per = w["pd"] // 2 + 2 * (w["pd"] // 64)
+    L = w["seq_len"]
+    sample_bytes = nseq * L * w["hkv"] * 2 * per + nseq * (L // 16) * 4 + 2 * nseq * w["hq"] * w["pd"] * 2
+    ip = np.arange(nseq + 1, dtype=np.int32) * bt.shape[1]
+    times = []
+    t_start = time.time()
+    while True:
+        t0 = time.perf_counter()
+        oracle.decode(q[:nseq], cache, bt[:nseq].reshape(-1), ip,
+                      np.full(nseq, L, np.int32), w["hkv"], w["pd"], 1.0 / math.sqrt(w["hd"]),
+                      signs)
+        times.append(time.perf_counter() - t0)
+        if time.time() - t_start > budget_s or len(times) >= 20:
+            break
+    med = statistics.median(times)
+    return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{nseq} of 8 sequences x {L} tokens (same cache, q, page table), "
+                      f"{len(times)} runs, median {med * 1e3:.1f} ms; oracle/tq_oracle.c "
+                      f"fp64-accumulated dequantize-then-attend, OpenMP {threads} threads"}
+
+
+def bench_write(torch, steps, warmup):
+    from tests import workloads as W
+    from turboquant_amd import ops
+    from turboquant_amd.geometry import hadamard_signs
+    dev = torch.device("cuda:0")
+    c = W.cfg2()
+    shape, pd = W.cache_bytes(c["num_blocks"], 8, 128)
+    cache = torch.zeros(shape, dtype=torch.uint8, device=dev)
+    k = torch.from_numpy(c["k"]).to(dev)
+    v = torch.from_numpy(c["v"]).to(dev)
+    slots = torch.from_numpy(c["slots"]).to(dev)
+    signs = hadamard_signs(pd, dev)
+    ms = time_launches(torch, lambda: ops.quantize_write_kv_cache(cache, k, v, signs, slots,
+                                                                  128, pd), steps, warmup)
+    nbytes = W.algorithmic_write_bytes(8192, 8, 128)
+    return {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "alg_bytes": nbytes, "config": "8192 tok x 8 heads x 128, K+V fp16, outliers x20, "
+                                           "permuted slots (configs[1])"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--splits", type=int, default=0, help="override num_splits")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build's path runs on a single MI355X; "
+              f"--gpus {args.gpus} is not supported (sharding is described in DESIGN.md).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from turboquant_amd import _lib, ops
+    _lib.load()
+    log("building cfg-3 cache on the GPU (write kernel)")
+    w = make_decode_workload(torch)
+    if args.splits:
+        w["splits"] = args.splits
+        w["cs"] = -(-w["seq_len"] // args.splits) + 15 & ~15
+    b, hq, pd, S = w["batch"], w["hq"], w["pd"], w["splits"]
+    dev = w["q"].device
+    o = torch.empty((b, hq, pd), dtype=torch.float16, device=dev)
+    po = torch.empty((b * S, hq, pd), dtype=torch.float32, device=dev)
+    pl = torch.empty((b * S, hq), dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(w["hd"])
+    lib = _lib.load()
+    cache = w["cache"]
+    kbase = cache.data_ptr()
+    vbase = kbase + cache[0].numel()
+
+    def step():
+        ops.decode_paged_splitkv(w["q"], cache, w["indices"], w["indptr"], w["seq"], w["hkv"],
+                                 w["hd"], pd, scale, w["signs"], o, po, pl, S, w["cs"])
+
+    def partials_only():
+        rc = lib.tq_decode_partials(w["q"].data_ptr(), hq * pd, pd, kbase, vbase,
+                                    w["indices"].data_ptr(), w["indptr"].data_ptr(),
+                                    w["seq"].data_ptr(), b, hq, w["hkv"], pd, 16, w["ebs"],
+                                    w["nb"], scale, w["signs"].data_ptr(), S, w["cs"],
+                                    po.data_ptr(), pl.data_ptr(),
+                                    torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "tq_decode_partials")
+
+    log(f"timing decode: splits={S} chunk={w['cs']} steps={args.steps} warmup={args.warmup}")
+    ms = time_launches(torch, step, args.steps, args.warmup)
+    nbytes = alg_bytes(w)
+    value = nbytes / (ms * 1e-3) / 1e9
+    log(f"decode step {ms * 1e3:.1f} us -> {value:.0f} GB/s")
+    ms_k = time_launches(torch, partials_only, args.steps, args.warmup)
+    achieved = nbytes / (ms_k * 1e-3) / 1e9
+    log(f"partials kernel {ms_k * 1e3:.1f} us -> {achieved:.0f} GB/s")
+    layout_bytes = b * w["seq_len"] * w["hkv"] * 2 * w["ebs"]
+    wr = bench_write(torch, args.steps, args.warmup)
+    log(f"write kernel {wr['us']} us -> {wr['GB/s']} GB/s")
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle) ...")
+        cpu = cpu_baseline(torch, w)
+        log(f"CPU baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": "decode-attn GB/s & % HBM peak, Qwen3-8B shape B=8 L=32k",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 codes -> f16 MFMA, f32 accumulate",
+        "data": "synthetic (seeded torch RNG, N(0,1) q/K/V, random page permutation)",
+        "config": {"workload": "decode attention, configs[2]: Qwen3-8B geometry 32q/8kv/hd128, "
+                               "B=8, 32768 cached tokens/seq, 16-token pages, split-KV + LSE merge",
+                   "batch": b, "seq_len": w["seq_len"], "num_qo_heads": hq,
+                   "num_kv_heads": w["hkv"], "head_dim": w["hd"], "page_size": 16,
+                   "num_splits": S, "kv_chunk_size": w["cs"], "parallelism": "single GPU"},
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "layout_GB/s": round(layout_bytes / (ms * 1e-3) / 1e9, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "decode_partials_kernel<128>",
+                     "kernel_us": round(ms_k * 1e3, 2), "alg_bytes": nbytes},
+        "cpu_baseline": cpu,
+        "write_kernel": wr,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

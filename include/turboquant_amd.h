@@ -1,0 +1,130 @@
+/*
+ * turboquant_amd.h -- C ABI of the MI355X (gfx950) TurboQuant quantized
+ * paged-KV hot path.  Plain pointers and sizes only; every device pointer is
+ * HIP device memory owned by the caller, every launch goes on `stream`, no
+ * call allocates or synchronises.
+ *
+ * Cache layout (fixed by the vLLM page-size hook of the reference,
+ * turboquant/vllm_backend_fused.py:56-86):
+ *   kv_cache uint8 [2, num_blocks, block_size, num_kv_heads, ebs]
+ *   pd = next_pow2(head_dim) in {64,128,256}, qbytes = pd/2,
+ *   ebs = (qbytes + 2*(pd/64) + 15) & ~15  (48 / 80 / 144 bytes)
+ *   entry bytes [0, qbytes): 4-bit codes, dim 2k in the high nibble of byte k
+ *   entry bytes [qbytes, qbytes + 2*pd/64): fp16 norm repeated pd/64 times
+ *   the K slab is kv_cache[0], the V slab kv_cache[1].
+ *
+ * Return value: 0 on success, -22 (-EINVAL) for bad arguments, otherwise the
+ * hipError_t of the launch.  tq_last_error() returns a message for the last
+ * non-zero return on the calling thread.
+ */
+#ifndef TURBOQUANT_AMD_H
+#define TURBOQUANT_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* tq_stream_t; /* == hipStream_t */
+
+enum tq_dtype { TQ_F32 = 0, TQ_F16 = 1, TQ_BF16 = 2 };
+
+/*
+ * Quantize K and V rows and scatter them into the paged cache.
+ *
+ * Replaces turboquant_write::quantize_write_kv_cache
+ * (reference csrc/src/quantize_write_binding.cu:207-269, kernel
+ * csrc/include/turboquant/quantize_write_kernel.cuh:332-431), which the
+ * backend calls from TurboQuantFusedImpl._write_to_cache
+ * (turboquant/vllm_backend_fused.py:293-305).
+ *
+ * key/value: element (t, h, d) at base + t*stride_tok + h*stride_head + d, in
+ * `in_dtype` (the reference takes fp32 after .float(); fp16 -> fp32 is exact,
+ * so fp16 input gives the same bytes).  slot_mapping int32 [num_tokens]:
+ * slot < 0 or slot >= num_blocks*block_size is skipped (the reference skips
+ * negative slots).  signs fp32 [padded_dim] of +-1.  Bytes written per entry:
+ * codes + norms; pad bytes are not touched.
+ */
+int tq_quantize_write_kv_cache(void* k_slab, void* v_slab,
+                               const void* key, const void* value, int32_t in_dtype,
+                               int64_t k_stride_tok, int64_t k_stride_head,
+                               int64_t v_stride_tok, int64_t v_stride_head,
+                               const float* signs, const int32_t* slot_mapping,
+                               int64_t num_tokens, int32_t num_kv_heads,
+                               int32_t head_dim, int32_t padded_dim,
+                               int32_t block_size, int32_t ebs, int64_t num_blocks,
+                               tq_stream_t stream);
+
+/*
+ * Split-KV GQA decode attention over the packed paged cache, one query token
+ * per sequence: partials kernel + LSE merge with the inverse rotation.
+ *
+ * Replaces turboquant_v5::decode_v5_from_cache_paged_splitkv_ws
+ * (reference csrc/src/decode_v5_tc_binding.cu:754-874: the v5 kernel
+ * csrc/include/flashinfer_decode_turboquant_v5_tc.cuh:106-795 and
+ * SplitKVCombineKernel csrc/include/flashinfer_decode_turboquant_combine.cuh:18-79),
+ * called by TurboQuantFusedImpl.forward (turboquant/vllm_backend_fused.py:422-435).
+ *
+ * q: fp16, element (b, h, d) at q + b*q_stride_b + h*q_stride_h + d, d < pd
+ *    (head_dim < pd must be zero padded, as the reference backend does).
+ * Sequence b's token t is page indices[indptr[b] + t/block_size], entry
+ * t % block_size, for t < seq_lens[b]; block_size % 16 == 0.  Split s of
+ * sequence b covers tokens [s*kv_chunk_size, min((s+1)*kv_chunk_size, seq_len)).
+ * Pages outside [0, num_blocks) are treated as empty.
+ * partition_o: fp32 [batch*num_splits, num_qo_heads, pd] and
+ * partition_lse: fp32 [batch*num_splits, num_qo_heads] are workspace.
+ * o: fp16 [batch, num_qo_heads, pd] contiguous, the attention output in the
+ * original (unrotated) domain.  signs == NULL disables the rotation.
+ * num_qo_heads / num_kv_heads must be an integer <= 16.
+ */
+int tq_decode_paged_splitkv(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                            const uint8_t* k_slab, const uint8_t* v_slab,
+                            const int32_t* indices, const int32_t* indptr,
+                            const int32_t* seq_lens, int32_t batch,
+                            int32_t num_qo_heads, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t padded_dim,
+                            int32_t block_size, int32_t ebs, int64_t num_blocks,
+                            float sm_scale, const float* signs,
+                            int32_t num_splits, int32_t kv_chunk_size,
+                            float* partition_o, float* partition_lse, void* o,
+                            tq_stream_t stream);
+
+/*
+ * The first kernel of tq_decode_paged_splitkv alone (the reference's v5 split
+ * kernel, v5_tc.cuh:106-795): writes partition_o (normalised, rotated domain)
+ * and partition_lse (natural log; -inf for an empty split).
+ */
+int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                       const uint8_t* k_slab, const uint8_t* v_slab,
+                       const int32_t* indices, const int32_t* indptr,
+                       const int32_t* seq_lens, int32_t batch,
+                       int32_t num_qo_heads, int32_t num_kv_heads,
+                       int32_t padded_dim, int32_t block_size, int32_t ebs,
+                       int64_t num_blocks, float sm_scale, const float* signs,
+                       int32_t num_splits, int32_t kv_chunk_size,
+                       float* partition_o, float* partition_lse, tq_stream_t stream);
+
+/*
+ * The second kernel alone: LSE merge of the splits of each sequence, inverse
+ * rotation (s * FWHT(o) / sqrt(pd)) and the fp16 store into o.  Replaces
+ * SplitKVCombineKernel (combine.cuh:18-79) plus the per-split inverse FWHT of
+ * v5_tc.cuh:712-765.  Splits with lse == -inf are skipped; a sequence with
+ * no tokens gets zeros.
+ */
+int tq_combine_splits(const float* partition_o, const float* partition_lse,
+                      int32_t batch, int32_t num_splits, int32_t num_qo_heads,
+                      int32_t padded_dim, const float* signs, void* o,
+                      tq_stream_t stream);
+
+/* Message for the last non-zero return of a tq_* call on this thread. */
+const char* tq_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int32_t tq_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TURBOQUANT_AMD_H */

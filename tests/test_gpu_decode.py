@@ -1,0 +1,110 @@
+"""GPU parity of the split-KV decode against the fp32/fp64 dequantize-then-attend
+oracle (max-abs 2e-3 / rel 1e-2), at the BASELINE shapes and edge cases."""
+import numpy as np
+import pytest
+import torch
+
+from tests import gpu_cases as G
+from tests import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(case, what, **kw):
+    cache, pd = G.build_cache(case)
+    got, qp, scale = G.run_decode(case, cache, pd, **kw)
+    ref = G.oracle_decode(case, cache.cpu().numpy(), qp, pd, scale, signs=kw.get("signs", True))
+    G.assert_close(got, ref, what)
+    return got, ref
+
+
+def test_cfg1_decode():
+    print("case: cfg1 decode B=1 L=1024 32/8/128", flush=True)
+    c = W.cfg1()
+    c["block_table"] = c["block_table"]
+    _check(c, "cfg1")
+
+
+def test_cfg3_decode_full_size():
+    print("case: cfg3 decode B=8 L=32768 32/8/128 random page permutation", flush=True)
+    _check(W.cfg3(), "cfg3")
+
+
+@pytest.mark.parametrize("hd", [128, 64, 256])
+def test_cfg4_ragged(hd):
+    batch = {128: 16, 64: 8, 256: 8}[hd]
+    print(f"case: cfg4 ragged hd={hd} B={batch} Student-t K", flush=True)
+    _check(W.cfg4(batch=batch, hd=hd), f"cfg4 hd{hd}")
+
+
+@pytest.mark.parametrize("splits,chunk", [(1, None), (3, None), (7, 100), (64, 16), (40, 37)])
+def test_split_invariance(splits, chunk):
+    """Any split layout (including chunks that are not page multiples) gives
+    the same attention within tolerance."""
+    print(f"case: split invariance splits={splits} chunk={chunk}", flush=True)
+    c = W.decode_case(21, 3, [1000, 37, 2048], 32, 8, 128)
+    _check(c, f"splits={splits}", num_splits=splits, chunk=chunk)
+
+
+def test_edge_lengths_and_gqa():
+    """seq_len 0, 1, 15, 16, 17 and a partial last page; GQA ratios 1, 2, 8, 16."""
+    for hq, hkv in ((8, 8), (16, 8), (16, 2), (16, 1)):
+        print(f"case: edge lengths hq={hq} hkv={hkv}", flush=True)
+        c = W.decode_case(31 + hq, 6, [0, 1, 15, 16, 17, 333], hq, hkv, 128)
+        got, ref = _check(c, f"edges {hq}/{hkv}", num_splits=4, chunk=96)
+        assert np.all(got[0] == 0)  # empty sequence -> zeros
+
+
+def test_no_rotation_signs_none():
+    print("case: signs=None", flush=True)
+    c = W.decode_case(41, 2, [500, 77], 32, 8, 128)
+    _check(c, "no rotation", signs=False)
+
+
+def test_out_of_range_page_is_empty():
+    """A page id outside the cache contributes nothing (instead of faulting)."""
+    print("case: out of range page", flush=True)
+    c = W.decode_case(51, 1, [64], 32, 8, 128)
+    cache, pd = G.build_cache(c)
+    c2 = dict(c)
+    bt = c["block_table"].copy()
+    bt[0, 3] = 1 << 20  # last 16 tokens point outside the pool
+    c2["block_table"] = bt
+    got, qp, scale = G.run_decode(c2, cache, pd, num_splits=2, chunk=32)
+    c3 = dict(c)
+    c3["seq_lens"] = np.array([48], np.int32)
+    ref = G.oracle_decode(c3, cache.cpu().numpy(), qp, pd, scale)
+    G.assert_close(got, ref, "oob page")
+
+
+def test_graph_replay_matches_eager():
+    """The op captured in a HIP graph: every replay equals the eager result."""
+    print("case: graph replay", flush=True)
+    from turboquant_amd import ops
+    from turboquant_amd.geometry import hadamard_signs
+    c = W.decode_case(61, 4, [700, 1300, 64, 2000], 32, 8, 128)
+    cache, pd = G.build_cache(c)
+    eager, qp, scale = G.run_decode(c, cache, pd, num_splits=5, chunk=416)
+    dev = G.DEV
+    qt = torch.from_numpy(qp).to(dev)
+    bt = torch.from_numpy(c["block_table"]).to(dev)
+    ind = bt.reshape(-1).contiguous()
+    ip = torch.arange(5, dtype=torch.int32, device=dev) * bt.shape[1]
+    sl = torch.from_numpy(c["seq_lens"]).to(dev)
+    o = torch.empty((4, 32, pd), dtype=torch.float16, device=dev)
+    po = torch.empty((20, 32, pd), dtype=torch.float32, device=dev)
+    pl = torch.empty((20, 32), dtype=torch.float32, device=dev)
+    s = hadamard_signs(pd, dev)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        ops.decode_paged_splitkv(qt, cache, ind, ip, sl, 8, 128, pd, scale, s, o, po, pl, 5, 416)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        ops.decode_paged_splitkv(qt, cache, ind, ip, sl, 8, 128, pd, scale, s, o, po, pl, 5, 416)
+    for i in range(4):
+        o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(o.float().cpu().numpy(), eager), f"replay {i}"

@@ -1,0 +1,125 @@
+"""GPU parity of the write kernel against the C oracle: bit-exact cache bytes."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import workloads as W
+from turboquant_amd import ops
+from turboquant_amd.geometry import hadamard_signs
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_cache(shape, k, v, slots, hd, pd, fill=0):
+    cache = np.full(shape, fill, np.uint8)
+    oracle.write_kv_cache(cache, k, v, hadamard_signs(pd).numpy(), slots, hd, pd)
+    return cache
+
+
+def _gpu_cache(shape, k, v, slots, hd, pd, fill=0, dtype=torch.float16):
+    dev = torch.device("cuda:0")
+    cache = torch.full(shape, fill, dtype=torch.uint8, device=dev)
+    kt = torch.from_numpy(k).to(dev).to(dtype)
+    vt = torch.from_numpy(v).to(dev).to(dtype)
+    ops.quantize_write_kv_cache(cache, kt, vt, hadamard_signs(pd, dev),
+                                torch.from_numpy(slots).to(dev), hd, pd)
+    torch.cuda.synchronize()
+    return cache.cpu().numpy()
+
+
+def _diff_report(a, b):
+    bad = np.argwhere(a != b)
+    return f"{len(bad)} bytes differ, first {bad[:5].tolist()}"
+
+
+def test_cfg2_write_bit_exact():
+    print("case: cfg2 write 8192x8x128 outliers x20, permuted slots", flush=True)
+    c = W.cfg2()
+    shape, pd = W.cache_bytes(c["num_blocks"], 8, 128)
+    ref = _oracle_cache(shape, c["k"], c["v"], c["slots"], 128, pd, fill=0xA5)
+    got = _gpu_cache(shape, c["k"], c["v"], c["slots"], 128, pd, fill=0xA5)
+    assert np.array_equal(ref, got), _diff_report(ref, got)
+    # pad bytes untouched
+    assert (got[..., 68:] == 0xA5).all()
+
+
+@pytest.mark.parametrize("hd", [64, 96, 256])
+def test_write_other_head_dims(hd):
+    print(f"case: write hd={hd}", flush=True)
+    rng = np.random.default_rng(10 + hd)
+    n, h, nb = 300, 4, 32
+    k, v = W.write_inputs(rng, n, h, hd, k_dist="t3")
+    slots = rng.permutation(nb * 16)[:n].astype(np.int32)
+    shape, pd = W.cache_bytes(nb, h, hd)
+    ref = _oracle_cache(shape, k, v, slots, hd, pd)
+    got = _gpu_cache(shape, k, v, slots, hd, pd)
+    assert np.array_equal(ref, got), _diff_report(ref, got)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_write_input_dtypes(dtype):
+    """fp32 (the reference's own input dtype) and bf16 rows give the oracle's bytes
+    for the same fp16-representable values."""
+    print(f"case: write dtype={dtype}", flush=True)
+    rng = np.random.default_rng(5)
+    n, h, hd, nb = 200, 8, 128, 16
+    k, v = W.write_inputs(rng, n, h, hd)
+    if dtype == torch.bfloat16:  # values exactly representable in both
+        k = torch.from_numpy(k).to(torch.bfloat16).to(torch.float16).numpy()
+        v = torch.from_numpy(v).to(torch.bfloat16).to(torch.float16).numpy()
+    slots = np.arange(n, dtype=np.int32)
+    shape, pd = W.cache_bytes(nb, h, hd)
+    ref = _oracle_cache(shape, k, v, slots, hd, pd)
+    got = _gpu_cache(shape, k, v, slots, hd, pd, dtype=dtype)
+    assert np.array_equal(ref, got), _diff_report(ref, got)
+
+
+def test_write_skips_negative_and_out_of_range_slots():
+    print("case: write negative/oob slots", flush=True)
+    rng = np.random.default_rng(6)
+    n, h, hd, nb = 64, 8, 128, 4
+    k, v = W.write_inputs(rng, n, h, hd)
+    slots = np.arange(n, dtype=np.int32)
+    slots[::3] = -1
+    slots[1] = nb * 16 + 5  # beyond the cache
+    shape, pd = W.cache_bytes(nb, h, hd)
+    ref = _oracle_cache(shape, k, v, slots, hd, pd, fill=0x11)
+    got = _gpu_cache(shape, k, v, slots, hd, pd, fill=0x11)
+    assert np.array_equal(ref, got), _diff_report(ref, got)
+    flat = got[0].reshape(nb * 16, h, -1)
+    assert (flat[0] == 0x11).all() and (flat[3] == 0x11).all()
+
+
+def test_write_strided_rows_and_zero_rows():
+    """key/value as strided views of a fused qkv buffer; all-zero rows map to 0x88."""
+    print("case: write strided + zero rows", flush=True)
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(7)
+    n, h, hd, nb = 48, 8, 128, 4
+    qkv = rng.standard_normal((n, (32 + 2 * h) * hd)).astype(np.float16)
+    qkv[5] = 0
+    k = qkv[:, 32 * hd:(32 + h) * hd].reshape(n, h, hd)
+    v = qkv[:, (32 + h) * hd:].reshape(n, h, hd)
+    slots = np.arange(n, dtype=np.int32)
+    shape, pd = W.cache_bytes(nb, h, hd)
+    ref = _oracle_cache(shape, np.ascontiguousarray(k), np.ascontiguousarray(v), slots, hd, pd)
+    t = torch.from_numpy(qkv).to(dev)
+    kt = t[:, 32 * hd:(32 + h) * hd].view(n, h, hd)
+    vt = t[:, (32 + h) * hd:].view(n, h, hd)
+    cache = torch.zeros(shape, dtype=torch.uint8, device=dev)
+    ops.quantize_write_kv_cache(cache, kt, vt, hadamard_signs(pd, dev),
+                                torch.from_numpy(slots).to(dev), hd, pd)
+    got = cache.cpu().numpy()
+    assert np.array_equal(ref, got), _diff_report(ref, got)
+    row5 = got[0].reshape(nb * 16, h, -1)[5]
+    assert (row5[:, :64] == 0x88).all() and (row5[:, 64:68] == 0).all()
+
+
+def test_write_empty_is_noop():
+    dev = torch.device("cuda:0")
+    cache = torch.zeros((2, 1, 16, 8, 80), dtype=torch.uint8, device=dev)
+    e = torch.zeros((0, 8, 128), dtype=torch.float16, device=dev)
+    ops.quantize_write_kv_cache(cache, e, e, hadamard_signs(128, dev),
+                                torch.zeros(0, dtype=torch.int32, device=dev), 128, 128)
+    assert int(cache.sum()) == 0

@@ -1,0 +1,591 @@
+// tq_decode.hip -- split-KV GQA decode attention over the packed paged cache.
+//
+// Semantics: dequantize-then-attend of the reference
+// (turboquant/triton_decode_ref.py:89-131, :264-299) computed in the rotated
+// domain as the reference's v5 kernel does
+// (csrc/include/flashinfer_decode_turboquant_v5_tc.cuh:106-795): q is rotated
+// once, q' = fp16(FWHT(s*q)/sqrt(pd)); K^ = codebook[code]*norm/sqrt(pd);
+// softmax(q'.K^ * sm_scale) V^ per split, LSE merge across splits
+// (flashinfer_decode_turboquant_combine.cuh:18-79), then the inverse rotation
+// o = s * FWHT(o')/sqrt(pd), applied once per (sequence, head) after the merge.
+//
+// gfx950 design (not the reference's):
+//  * One workgroup per (sequence, split, group of G kv heads), one wave64 per
+//    kv head; all G heads of a token share 80-byte neighbours in the same
+//    cache lines, so a workgroup consumes whole lines.
+//  * A 16-token tile is one MFMA block.  QK^T: v_mfma_f32_16x16x32_f16 with
+//    A = dequantized K (row = token, lane l loads 16 B of token l%16 with one
+//    dwordx4), B = q' (column = q head; GQA heads padded to 16).  The C layout
+//    (row 4*(l/16)+r = token, column l%16 = head) is exactly the B layout of
+//    the PV product v_mfma_f32_16x16x16_f16 (A = V^T: row = dim slot l%16,
+//    k = tokens 4*(l/16)..+3), so probabilities never leave registers.
+//  * 4-bit -> fp16 dequant without memory lookups: the codebook is odd
+//    (c[15-i] = -c[i]); codes are folded to (sign, 3-bit magnitude) with
+//    bit tricks on 8 nibbles at once, magnitudes come from two v_perm_b32
+//    byte tables (high and low byte of the fp16 value), the sign is OR-ed into
+//    the high byte, and v_perm interleaves the bytes into packed fp16 pairs.
+//  * The K norm scales the score; the V norm and 1/sqrt(pd) fold into the
+//    fp16 probability, so dequantized operands are raw codebook values.
+//  * Online softmax in the exp2 domain with a lazy rescale (the running max
+//    only moves when a tile exceeds it by more than 2^3), bounding p <= 8.
+#include <math.h>
+
+#include "tq_common.h"
+
+namespace tq {
+
+namespace {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// fp16 bit patterns of the positive centroids c[8+m], m = 0..7:
+// 0x301c 0x3636 0x3941 0x3b8a 0x3d06 0x3e79 0x4024 0x4177, split into a
+// high-byte table and a low-byte table of 8 bytes each (2 dwords, m = byte).
+constexpr uint32_t kHi0 = 0x3b393630u, kHi1 = 0x41403e3du;
+constexpr uint32_t kLo0 = 0x8a41361cu, kLo1 = 0x77247906u;
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  // byte i of the result = byte sel_i of the 8-byte value {hi:lo} (lo = bytes 0-3)
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Dequantize 8 codes (one dword, byte k = code[2k] << 4 | code[2k+1]) to 8
+// fp16 codebook values, as 4 packed pairs:
+//   x[0] = (byte0 low, byte1 low)   x[1] = (byte2 low, byte3 low)
+//   x[2] = (byte0 high, byte1 high) x[3] = (byte2 high, byte3 high)
+// i.e. element order {1,3,5,7,0,2,4,6} of the 8 dims the dword holds.
+__device__ __forceinline__ void dq8(uint32_t D, uint32_t* x) {
+  // fold: nibble n -> (neg flag in bit 3, magnitude index m in bits 0-2) with
+  // c[n] = (n >= 8) ? M[n-8] : -M[7-n]
+  const uint32_t a = D & 0x88888888u;
+  const uint32_t F = ~D ^ (a - (a >> 3));
+  const uint32_t SL = F & 0x07070707u;
+  const uint32_t SH = (F >> 4) & 0x07070707u;
+  const uint32_t hL = perm(kHi1, kHi0, SL) | ((F << 4) & 0x80808080u);
+  const uint32_t lL = perm(kLo1, kLo0, SL);
+  const uint32_t hH = perm(kHi1, kHi0, SH) | (F & 0x80808080u);
+  const uint32_t lH = perm(kLo1, kLo0, SH);
+  x[0] = perm(hL, lL, 0x05010400u);
+  x[1] = perm(hL, lL, 0x07030602u);
+  x[2] = perm(hH, lH, 0x05010400u);
+  x[3] = perm(hH, lH, 0x07030602u);
+}
+
+__device__ __forceinline__ half8_t as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u32x4 u = {a, b, c, d};
+  return __builtin_bit_cast(half8_t, u);
+}
+__device__ __forceinline__ half4_t as_half4(uint32_t a, uint32_t b) {
+  u32x2 u = {a, b};
+  return __builtin_bit_cast(half4_t, u);
+}
+
+// broadcast lane r of each quad (DPP quad_perm, no LDS)
+template <int R>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, R * 0x55, 0xf, 0xf, false);
+}
+
+__device__ __forceinline__ float h2f(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+struct DecodeParams {
+  const _Float16* q;
+  int64_t q_sb, q_sh;
+  const uint8_t* ks;
+  const uint8_t* vs;
+  const int32_t* indices;
+  const int32_t* indptr;
+  const int32_t* seq_lens;
+  const float* signs;
+  float* po;
+  float* plse;
+  int64_t num_blocks;
+  int B, Hq, Hkv, ratio, block_size, ebs, S, cs, G, HG;
+  float qk_scale;     // sm_scale * log2(e) / sqrt(pd)
+  float inv_sqrt_pd;  // 1/sqrt(pd)
+};
+
+template <int PD>
+struct Tile {
+  static constexpr int KD = PD / 32;            // K dwords per lane = QK MFMAs
+  static constexpr int VB = PD / 32;            // V bytes per lane per token
+  static constexpr int VW = VB >= 4 ? VB / 4 : 1;  // V dwords per lane per token
+  uint32_t k[KD];
+  uint32_t v[4][VW];
+  uint32_t nk, nv;
+};
+
+template <int PD>
+__device__ __forceinline__ void load_tile(const DecodeParams& p, int b, int kvh, int tile,
+                                          int lane, bool& ok, Tile<PD>& t) {
+  constexpr int KB = PD / 8;
+  constexpr int VB = PD / 32;
+  const int T = tile * kTile;
+  int page = p.indices[p.indptr[b] + T / p.block_size];
+  page = __builtin_amdgcn_readfirstlane(page);
+  ok = page >= 0 && (int64_t)page < p.num_blocks;
+  if (!ok) {
+#pragma unroll
+    for (int i = 0; i < Tile<PD>::KD; i++) t.k[i] = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int i = 0; i < Tile<PD>::VW; i++) t.v[j][i] = 0;
+    t.nk = t.nv = 0;
+    return;
+  }
+  const int64_t tokstride = (int64_t)p.Hkv * p.ebs;
+  const int64_t rowbase =
+      ((int64_t)page * p.block_size + (T % p.block_size)) * tokstride + (int64_t)kvh * p.ebs;
+  const int q4 = lane >> 4, n = lane & 15;
+  // K: token n, bytes [q4*KB, (q4+1)*KB)
+  const uint8_t* kp = p.ks + rowbase + n * tokstride + q4 * KB;
+  if constexpr (PD == 64) {
+    u32x2 w = *reinterpret_cast<const u32x2*>(kp);
+    t.k[0] = w[0]; t.k[1] = w[1];
+  } else if constexpr (PD == 128) {
+    u32x4 w = *reinterpret_cast<const u32x4*>(kp);
+#pragma unroll
+    for (int i = 0; i < 4; i++) t.k[i] = w[i];
+  } else {
+    u32x4 w0 = *reinterpret_cast<const u32x4*>(kp);
+    u32x4 w1 = *reinterpret_cast<const u32x4*>(kp + 16);
+#pragma unroll
+    for (int i = 0; i < 4; i++) { t.k[i] = w0[i]; t.k[4 + i] = w1[i]; }
+  }
+  // V: tokens 4*q4 + j, bytes [n*VB, (n+1)*VB)
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint8_t* vp = p.vs + rowbase + (4 * q4 + j) * tokstride + n * VB;
+    if constexpr (PD == 64) {
+      t.v[j][0] = *reinterpret_cast<const uint16_t*>(vp);
+    } else if constexpr (PD == 128) {
+      t.v[j][0] = *reinterpret_cast<const uint32_t*>(vp);
+    } else {
+      u32x2 w = *reinterpret_cast<const u32x2*>(vp);
+      t.v[j][0] = w[0]; t.v[j][1] = w[1];
+    }
+  }
+  // norms of token 4*q4 + (lane & 3), broadcast within the quad later
+  const int64_t noff = rowbase + (4 * q4 + (lane & 3)) * tokstride + PD / 2;
+  t.nk = *reinterpret_cast<const uint16_t*>(p.ks + noff);
+  t.nv = *reinterpret_cast<const uint16_t*>(p.vs + noff);
+}
+
+// 4x4 byte transpose: E_k byte j = byte k of D_j
+__device__ __forceinline__ void transpose4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
+                                           uint32_t* e) {
+  const uint32_t a01 = perm(d1, d0, 0x05010400u), b01 = perm(d1, d0, 0x07030602u);
+  const uint32_t a23 = perm(d3, d2, 0x05010400u), b23 = perm(d3, d2, 0x07030602u);
+  e[0] = perm(a23, a01, 0x05040100u);
+  e[1] = perm(a23, a01, 0x07060302u);
+  e[2] = perm(b23, b01, 0x05040100u);
+  e[3] = perm(b23, b01, 0x07060302u);
+}
+
+template <int PD>
+__global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
+  constexpr int KD = PD / 32;
+  constexpr int VB = PD / 32;
+  constexpr int NO = PD / 16;  // PV MFMAs = dim slots per lane
+  extern __shared__ float smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int q4 = lane >> 4, n = lane & 15;
+  int bid = blockIdx.x;
+  const int hg = bid % p.HG;
+  bid /= p.HG;
+  const int s = bid % p.S;
+  const int b = bid / p.S;
+  const int kvh = hg * p.G + w;
+  const int ratio = p.ratio;
+
+  // ---- q' = fp16(FWHT(s*q)/sqrt(pd)) for this wave's `ratio` heads, in LDS
+  float* qs = smem + (size_t)w * ratio * PD;
+  for (int i = lane; i < ratio * PD; i += 64) {
+    const int r = i / PD, d = i - r * PD;
+    float x = (float)p.q[b * p.q_sb + (int64_t)(kvh * ratio + r) * p.q_sh + d];
+    if (p.signs) x = x * p.signs[d];
+    qs[i] = x;
+  }
+  __syncthreads();
+  if (p.signs) {
+    for (int h = 1; h < PD; h <<= 1) {
+      for (int i = lane; i < ratio * PD / 2; i += 64) {
+        const int r = i / (PD / 2), j = i - r * (PD / 2);
+        const int lo = r * PD + (j / h) * 2 * h + (j % h);
+        const float a = qs[lo], c = qs[lo + h];
+        qs[lo] = a + c;
+        qs[lo + h] = a - c;
+      }
+      __syncthreads();
+    }
+  }
+  const float qsc = p.signs ? p.inv_sqrt_pd : 1.0f;
+  // B operand of the QK MFMA: column n = q head, 8 dims of quarter q4 per MFMA
+  half8_t qop[KD];
+  {
+    constexpr int ord[8] = {1, 3, 5, 7, 0, 2, 4, 6};
+#pragma unroll
+    for (int c = 0; c < KD; c++) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int d = q4 * (PD / 4) + 8 * c + ord[e];
+        qop[c][e] = (n < ratio) ? (_Float16)(qs[n * PD + d] * qsc) : (_Float16)0.0f;
+      }
+    }
+  }
+
+  float4_t O[NO];
+#pragma unroll
+  for (int i = 0; i < NO; i++) O[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY;
+  float lsum = 0.f;
+
+  const int L = p.seq_lens[b];
+  const int c0 = s * p.cs;
+  const int c1 = min(c0 + p.cs, L);
+  if (c0 < c1) {
+    const int tile0 = c0 / kTile, tile1 = (c1 - 1) / kTile;
+    Tile<PD> cur, nxt;
+    bool ok_cur, ok_nxt = false;
+    load_tile<PD>(p, b, kvh, tile0, lane, ok_cur, cur);
+    for (int tile = tile0; tile <= tile1; tile++) {
+      if (tile < tile1) load_tile<PD>(p, b, kvh, tile + 1, lane, ok_nxt, nxt);
+
+      // ---- scores S[t = 4*q4 + r][h = n]
+      float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < KD; c++) {
+        uint32_t x[4];
+        dq8(cur.k[c], x);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(x[0], x[1], x[2], x[3]), qop[c],
+                                                     acc, 0, 0, 0);
+      }
+      const float nk[4] = {h2f(quad_bcast<0>(cur.nk)), h2f(quad_bcast<1>(cur.nk)),
+                           h2f(quad_bcast<2>(cur.nk)), h2f(quad_bcast<3>(cur.nk))};
+      const float nv[4] = {h2f(quad_bcast<0>(cur.nv)), h2f(quad_bcast<1>(cur.nv)),
+                           h2f(quad_bcast<2>(cur.nv)), h2f(quad_bcast<3>(cur.nv))};
+      const int tbase = tile * kTile + 4 * q4;
+      float sc[4];
+      bool valid[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int t = tbase + r;
+        valid[r] = ok_cur && t >= c0 && t < c1;
+        sc[r] = valid[r] ? acc[r] * nk[r] * p.qk_scale : -INFINITY;
+      }
+      float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float m_new = fmaxf(m, tmax);
+      const bool need = (n < ratio) && (m_new > m + 3.0f);
+      if (__any(need)) {
+        const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+#pragma unroll
+        for (int i = 0; i < NO; i++) O[i] *= alpha;
+        lsum *= alpha;
+        m = m_new;
+      }
+      float pr[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        pr[r] = valid[r] ? __builtin_amdgcn_exp2f(sc[r] - m) : 0.0f;
+        lsum += pr[r];
+      }
+      half4_t pv;
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        pv[r] = valid[r] ? (_Float16)(pr[r] * nv[r] * p.inv_sqrt_pd) : (_Float16)0.0f;
+
+      // ---- O[h][dim slot] += V^T P^T
+      uint32_t e[VB];
+      if constexpr (PD == 64) {
+        const uint32_t p01 = cur.v[0][0] | (cur.v[1][0] << 16);
+        const uint32_t p23 = cur.v[2][0] | (cur.v[3][0] << 16);
+        e[0] = perm(p23, p01, 0x06040200u);
+        e[1] = perm(p23, p01, 0x07050301u);
+      } else if constexpr (PD == 128) {
+        transpose4(cur.v[0][0], cur.v[1][0], cur.v[2][0], cur.v[3][0], e);
+      } else {
+        transpose4(cur.v[0][0], cur.v[1][0], cur.v[2][0], cur.v[3][0], e);
+        transpose4(cur.v[0][1], cur.v[1][1], cur.v[2][1], cur.v[3][1], e + 4);
+      }
+#pragma unroll
+      for (int k = 0; k < VB; k++) {
+        uint32_t x[4];
+        dq8(e[k], x);
+        O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_half4(x[0], x[1]), pv,
+                                                             O[2 * k + 1], 0, 0, 0);
+        O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_half4(x[2], x[3]), pv, O[2 * k],
+                                                         0, 0, 0);
+      }
+      if (tile < tile1) {
+        cur = nxt;
+        ok_cur = ok_nxt;
+      }
+    }
+  }
+
+  // ---- finish: O[i][r] = o[h = n][dim (4*q4 + r)*NO + i]
+  float lt = lsum + __shfl_xor(lsum, 16);
+  lt = lt + __shfl_xor(lt, 32);
+  if (n < ratio) {
+    const float inv = lt > 0.f ? 1.0f / lt : 0.0f;
+    const int64_t row = ((int64_t)b * p.S + s) * p.Hq + kvh * ratio + n;
+    float* out = p.po + row * PD + q4 * (PD / 4);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+#pragma unroll
+      for (int i = 0; i < NO; i += 4) {
+        float4_t v = {O[i][r] * inv, O[i + 1][r] * inv, O[i + 2][r] * inv, O[i + 3][r] * inv};
+        *reinterpret_cast<float4_t*>(out + r * NO + i) = v;
+      }
+    }
+    if (q4 == 0)
+      p.plse[row] = lt > 0.f ? (m + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
+  }
+}
+
+template <int PD>
+__global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ po,
+                                                     const float* __restrict__ plse, int S,
+                                                     int Hq, const float* __restrict__ signs,
+                                                     float inv_sqrt_pd, _Float16* __restrict__ o) {
+  constexpr int V = PD / 64;
+  const int lane = threadIdx.x;
+  const int b = blockIdx.x / Hq, h = blockIdx.x % Hq;
+  float mx = -INFINITY;
+  for (int s = 0; s < S; s++) mx = fmaxf(mx, plse[((int64_t)b * S + s) * Hq + h]);
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; i++) acc[i] = 0.f;
+  if (mx > -INFINITY) {
+    float den = 0.f;
+    for (int s = 0; s < S; s++) {
+      const int64_t row = ((int64_t)b * S + s) * Hq + h;
+      const float l = plse[row];
+      if (!(l > -INFINITY)) continue;
+      const float wgt = __expf(l - mx);
+      den += wgt;
+      const float* src = po + row * PD + lane * V;
+#pragma unroll
+      for (int i = 0; i < V; i++) acc[i] += wgt * src[i];
+    }
+    const float inv = 1.0f / den;
+#pragma unroll
+    for (int i = 0; i < V; i++) acc[i] *= inv;
+    if (signs) {
+#pragma unroll
+      for (int hh = 1; hh < V; hh <<= 1)
+#pragma unroll
+        for (int i = 0; i < V; i += 2 * hh)
+#pragma unroll
+          for (int k = 0; k < hh; k++) {
+            const float a = acc[i + k], c = acc[i + k + hh];
+            acc[i + k] = a + c;
+            acc[i + k + hh] = a - c;
+          }
+#pragma unroll
+      for (int delta = 1; delta < 64; delta <<= 1)
+#pragma unroll
+        for (int i = 0; i < V; i++) {
+          const float partner = __shfl_xor(acc[i], delta);
+          acc[i] = (lane & delta) ? (partner - acc[i]) : (acc[i] + partner);
+        }
+#pragma unroll
+      for (int i = 0; i < V; i++) acc[i] = acc[i] * inv_sqrt_pd * signs[lane * V + i];
+    }
+  }
+  _Float16* dst = o + ((int64_t)b * Hq + h) * PD + lane * V;
+#pragma unroll
+  for (int i = 0; i < V; i++) dst[i] = (_Float16)acc[i];
+}
+
+int check_geometry(int pd, int hq, int hkv, int bs, int ebs, const char* who) {
+  if (pd != 64 && pd != 128 && pd != 256) {
+    set_error("%s: padded_dim must be 64, 128 or 256, got %d", who, pd);
+    return kEinval;
+  }
+  if (hkv <= 0 || hq <= 0 || hq % hkv != 0 || hq / hkv > 16) {
+    set_error("%s: num_qo_heads %d / num_kv_heads %d must be an integer <= 16", who, hq, hkv);
+    return kEinval;
+  }
+  if (bs <= 0 || bs % kTile != 0) {
+    set_error("%s: block_size %d must be a positive multiple of 16", who, bs);
+    return kEinval;
+  }
+  if (ebs % 16 != 0 || ebs < pd / 2 + 2 * (pd / 64)) {
+    set_error("%s: ebs %d must be a multiple of 16 and >= %d", who, ebs, pd / 2 + 2 * (pd / 64));
+    return kEinval;
+  }
+  return 0;
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                  const uint8_t* k_slab, const uint8_t* v_slab,
+                                  const int32_t* indices, const int32_t* indptr,
+                                  const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                  int32_t num_kv_heads, int32_t padded_dim, int32_t block_size,
+                                  int32_t ebs, int64_t num_blocks, float sm_scale,
+                                  const float* signs, int32_t num_splits, int32_t kv_chunk_size,
+                                  float* partition_o, float* partition_lse, tq_stream_t stream) {
+  using namespace tq;
+  int rc = check_geometry(padded_dim, num_qo_heads, num_kv_heads, block_size, ebs, "decode");
+  if (rc) return rc;
+  if (batch < 0 || num_splits < 1 || kv_chunk_size < 1) {
+    set_error("decode: batch %d, num_splits %d, kv_chunk_size %d out of range", batch,
+              num_splits, kv_chunk_size);
+    return kEinval;
+  }
+  if (batch == 0) return 0;
+  if (!q || !k_slab || !v_slab || !indices || !indptr || !seq_lens || !partition_o ||
+      !partition_lse) {
+    set_error("decode: null pointer");
+    return kEinval;
+  }
+  if ((uintptr_t)k_slab % 16 || (uintptr_t)v_slab % 16 || (uintptr_t)partition_o % 16) {
+    set_error("decode: cache slabs and partition_o must be 16-byte aligned");
+    return kEinval;
+  }
+  const int pd = padded_dim;
+  const int ratio = num_qo_heads / num_kv_heads;
+  int G = 1;
+  for (int g = 8; g >= 1; g--)
+    if (num_kv_heads % g == 0 && g * ratio * pd <= 16384) {
+      G = g;
+      break;
+    }
+  DecodeParams p;
+  p.q = static_cast<const _Float16*>(q);
+  p.q_sb = q_stride_b;
+  p.q_sh = q_stride_h;
+  p.ks = k_slab;
+  p.vs = v_slab;
+  p.indices = indices;
+  p.indptr = indptr;
+  p.seq_lens = seq_lens;
+  p.signs = signs;
+  p.po = partition_o;
+  p.plse = partition_lse;
+  p.num_blocks = num_blocks;
+  p.B = batch;
+  p.Hq = num_qo_heads;
+  p.Hkv = num_kv_heads;
+  p.ratio = ratio;
+  p.block_size = block_size;
+  p.ebs = ebs;
+  p.S = num_splits;
+  p.cs = kv_chunk_size;
+  p.G = G;
+  p.HG = num_kv_heads / G;
+  p.inv_sqrt_pd = 1.0f / sqrtf((float)pd);
+  p.qk_scale = sm_scale * 1.4426950408889634f * p.inv_sqrt_pd;
+  const int64_t blocks = (int64_t)batch * num_splits * p.HG;
+  if (blocks > 0x7fffffffLL) {
+    set_error("decode: grid too large");
+    return kEinval;
+  }
+  const size_t lds = (size_t)G * ratio * pd * sizeof(float);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)blocks), block(64 * G);
+  switch (pd) {
+    case 64:
+      hipLaunchKernelGGL(decode_partials_kernel<64>, grid, block, lds, st, p);
+      break;
+    case 128:
+      hipLaunchKernelGGL(decode_partials_kernel<128>, grid, block, lds, st, p);
+      break;
+    default:
+      hipLaunchKernelGGL(decode_partials_kernel<256>, grid, block, lds, st, p);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("decode: launch failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return 0;
+}
+
+extern "C" int tq_combine_splits(const float* partition_o, const float* partition_lse,
+                                 int32_t batch, int32_t num_splits, int32_t num_qo_heads,
+                                 int32_t padded_dim, const float* signs, void* o,
+                                 tq_stream_t stream) {
+  using namespace tq;
+  const int pd = padded_dim;
+  if (pd != 64 && pd != 128 && pd != 256) {
+    set_error("combine: padded_dim must be 64, 128 or 256, got %d", pd);
+    return kEinval;
+  }
+  if (batch < 0 || num_splits < 1 || num_qo_heads < 1) {
+    set_error("combine: bad sizes");
+    return kEinval;
+  }
+  if (batch == 0) return 0;
+  if (!partition_o || !partition_lse || !o) {
+    set_error("combine: null pointer");
+    return kEinval;
+  }
+  const int64_t blocks = (int64_t)batch * num_qo_heads;
+  if (blocks > 0x7fffffffLL) {
+    set_error("combine: grid too large");
+    return kEinval;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const float isq = 1.0f / sqrtf((float)pd);
+  _Float16* out = static_cast<_Float16*>(o);
+  dim3 grid((unsigned)blocks), block(64);
+  switch (pd) {
+    case 64:
+      hipLaunchKernelGGL(combine_kernel<64>, grid, block, 0, st, partition_o, partition_lse,
+                         num_splits, num_qo_heads, signs, isq, out);
+      break;
+    case 128:
+      hipLaunchKernelGGL(combine_kernel<128>, grid, block, 0, st, partition_o, partition_lse,
+                         num_splits, num_qo_heads, signs, isq, out);
+      break;
+    default:
+      hipLaunchKernelGGL(combine_kernel<256>, grid, block, 0, st, partition_o, partition_lse,
+                         num_splits, num_qo_heads, signs, isq, out);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("combine: launch failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return 0;
+}
+
+extern "C" int tq_decode_paged_splitkv(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                       const uint8_t* k_slab, const uint8_t* v_slab,
+                                       const int32_t* indices, const int32_t* indptr,
+                                       const int32_t* seq_lens, int32_t batch,
+                                       int32_t num_qo_heads, int32_t num_kv_heads,
+                                       int32_t head_dim, int32_t padded_dim, int32_t block_size,
+                                       int32_t ebs, int64_t num_blocks, float sm_scale,
+                                       const float* signs, int32_t num_splits,
+                                       int32_t kv_chunk_size, float* partition_o,
+                                       float* partition_lse, void* o, tq_stream_t stream) {
+  using namespace tq;
+  if (head_dim <= 0 || head_dim > padded_dim) {
+    set_error("decode: head_dim %d exceeds padded_dim %d", head_dim, padded_dim);
+    return kEinval;
+  }
+  int rc = tq_decode_partials(q, q_stride_b, q_stride_h, k_slab, v_slab, indices, indptr,
+                              seq_lens, batch, num_qo_heads, num_kv_heads, padded_dim,
+                              block_size, ebs, num_blocks, sm_scale, signs, num_splits,
+                              kv_chunk_size, partition_o, partition_lse, stream);
+  if (rc) return rc;
+  return tq_combine_splits(partition_o, partition_lse, batch, num_splits, num_qo_heads,
+                           padded_dim, signs, o, stream);
+}

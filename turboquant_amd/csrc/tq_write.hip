@@ -1,0 +1,294 @@
+// tq_write.hip -- quantize-and-scatter of K/V rows into the packed paged cache.
+//
+// Same numbers as the reference scatter kernel
+// (csrc/include/turboquant/quantize_write_kernel.cuh:332-431): every vector is
+// handled by 32 lanes holding VEC = pd/32 consecutive dims each, so the
+// fp32 sum of squares, its reduction tree, sqrt, reciprocal, sign flip,
+// FWHT butterflies and the 1/sqrt(pd) scale happen in the same order and
+// give the same bits.  MI355X layout: a wave64 carries two vectors (one per
+// 32-lane half), a 256-thread workgroup carries 8 consecutive (token, head)
+// vectors, so the 8 heads of one token (8 x ebs contiguous bytes) are
+// written by one workgroup.  One launch covers K and V.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "tq_common.h"
+
+namespace tq {
+
+namespace {
+
+// Load VEC consecutive input elements as fp32 (exact for fp16/bf16).
+template <int VEC>
+__device__ __forceinline__ void load_row(const void* base, int64_t off, int dtype,
+                                         int d0, int head_dim, bool vec_ok, float* x) {
+  if (dtype == TQ_F16) {
+    const _Float16* p = reinterpret_cast<const _Float16*>(base) + off + d0;
+    if (vec_ok) {
+      if constexpr (VEC == 2) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        h2 v = *reinterpret_cast<const h2*>(p);
+        x[0] = (float)v[0]; x[1] = (float)v[1];
+      } else if constexpr (VEC == 4) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        h4 v = *reinterpret_cast<const h4*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; i++) x[i] = (float)v[i];
+      } else {
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        h8 v = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+        for (int i = 0; i < 8; i++) x[i] = (float)v[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; i++) x[i] = (d0 + i < head_dim) ? (float)p[i] : 0.0f;
+    }
+  } else if (dtype == TQ_BF16) {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(base) + off + d0;
+#pragma unroll
+    for (int i = 0; i < VEC; i++)
+      x[i] = (d0 + i < head_dim) ? __uint_as_float((uint32_t)p[i] << 16) : 0.0f;
+  } else {
+    const float* p = reinterpret_cast<const float*>(base) + off + d0;
+#pragma unroll
+    for (int i = 0; i < VEC; i++) x[i] = (d0 + i < head_dim) ? p[i] : 0.0f;
+  }
+}
+
+// code = #{j : v >= b_j} over the 15 boundaries b_j = boundary_j * scale.
+// The boundaries are symmetric with b_7 = 0, so for v >= 0 (this includes
+// -0.0, as in the reference's `val >= b[mid]`) the code is 8 + #{k : v >= B_k},
+// and for v < 0 or NaN it is 7 - #{k : |v| > B_k}, B_k = b_{7+k}.  On positive
+// floats "a > B" is "bits(a) - 1 >= bits(B)" as integers, so one integer
+// compare chain serves both sides.  Same result as the binary search of
+// quantize_write_kernel.cuh:34-46 for every fp32 input.
+__device__ __forceinline__ uint32_t bucketize(float v, const int32_t* bbits) {
+  const bool pos = v >= 0.0f;
+  int32_t a = (int32_t)(__float_as_uint(v) & 0x7fffffffu) - (pos ? 0 : 1);
+  uint32_t k = 0;
+#pragma unroll
+  for (int j = 0; j < 7; j++) k += (a >= bbits[j]) ? 1u : 0u;
+  return pos ? 8u + k : 7u - k;
+}
+
+template <int PD, bool VEC_OK>
+__global__ __launch_bounds__(256) void write_kernel(
+    uint8_t* __restrict__ k_slab, uint8_t* __restrict__ v_slab,
+    const void* __restrict__ key, const void* __restrict__ value, int dtype,
+    int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh,
+    const float* __restrict__ signs, const int32_t* __restrict__ slots,
+    int64_t num_tokens, int H, int head_dim, int block_size, int ebs, int64_t nslots,
+    float scale) {
+#pragma clang fp contract(off)
+  constexpr int VEC = PD / 32;
+  const int lane = threadIdx.x & 31;
+  const int64_t per_kv = num_tokens * H;
+  const int64_t g = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (g >= 2 * per_kv) return;
+  const int kv = g >= per_kv ? 1 : 0;
+  const int64_t rem = g - kv * per_kv;
+  const int64_t t = rem / H;
+  const int h = (int)(rem - t * H);
+  const int32_t slot = slots[t];
+  if (slot < 0 || (int64_t)slot >= nslots) return;  // whole 32-lane group leaves together
+
+  float v[VEC];
+  const int d0 = lane * VEC;
+  if (kv == 0)
+    load_row<VEC>(key, t * k_st + h * k_sh, dtype, d0, head_dim, VEC_OK, v);
+  else
+    load_row<VEC>(value, t * v_st + h * v_sh, dtype, d0, head_dim, VEC_OK, v);
+
+  // 1. per-lane sum of squares, FMA-accumulated in dim order
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VEC; i++) ss = __builtin_fmaf(v[i], v[i], ss);
+  // 2. 32-lane butterfly; every lane ends with the bits lane 0 of the
+  //    reference's shfl_down tree (16,8,4,2,1) holds
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) ss = ss + __shfl_xor(ss, off, 32);
+  // 3. IEEE sqrt and reciprocal
+  const float l2 = __builtin_sqrtf(ss);
+  const float inv = (l2 > 1e-8f) ? (1.0f / l2) : 0.0f;
+  // 4. normalise, flip signs
+#pragma unroll
+  for (int i = 0; i < VEC; i++) v[i] = v[i] * inv;
+#pragma unroll
+  for (int i = 0; i < VEC; i++) v[i] = v[i] * signs[d0 + i];
+  // 5. FWHT: in-lane stages, then cross-lane stages
+#pragma unroll
+  for (int hh = 1; hh < VEC; hh <<= 1) {
+#pragma unroll
+    for (int i = 0; i < VEC; i += 2 * hh) {
+#pragma unroll
+      for (int k = 0; k < hh; k++) {
+        float a = v[i + k], b = v[i + k + hh];
+        v[i + k] = a + b;
+        v[i + k + hh] = a - b;
+      }
+    }
+  }
+#pragma unroll
+  for (int delta = 1; delta < 32; delta <<= 1) {
+#pragma unroll
+    for (int i = 0; i < VEC; i++) {
+      float partner = __shfl_xor(v[i], delta, 32);
+      v[i] = (lane & delta) ? (partner - v[i]) : (v[i] + partner);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VEC; i++) v[i] = v[i] * scale;
+
+  // 6. bucketize against b_j * scale (fp32 products, as the reference forms them)
+  int32_t bbits[7];
+#pragma unroll
+  for (int j = 0; j < 7; j++) bbits[j] = (int32_t)__float_as_uint(boundary_pos(j + 1) * scale);
+
+  uint8_t* entry = (kv == 0 ? k_slab : v_slab) +
+                   ((int64_t)slot * H + h) * (int64_t)ebs;  // slot*H == (block*bs+entry)*H
+  // 7. pack: byte k = code[2k] << 4 | code[2k+1]
+  uint32_t packed = 0;
+#pragma unroll
+  for (int i = 0; i < VEC; i += 2) {
+    uint32_t c0 = bucketize(v[i], bbits), c1 = bucketize(v[i + 1], bbits);
+    packed |= ((c0 << 4) | c1) << (4 * i);  // byte i/2
+  }
+  uint8_t* dst = entry + lane * (VEC / 2);
+  if constexpr (VEC == 2) {
+    *dst = (uint8_t)packed;
+  } else if constexpr (VEC == 4) {
+    *reinterpret_cast<uint16_t*>(dst) = (uint16_t)packed;
+  } else {
+    *reinterpret_cast<uint32_t*>(dst) = packed;
+  }
+  // 8. fp16(l2), round to nearest even, repeated pd/64 times after the codes
+  if (lane == 0) {
+    _Float16 nh = (_Float16)l2;
+    uint32_t nb = (uint32_t)__builtin_bit_cast(uint16_t, nh);
+    uint8_t* np = entry + PD / 2;
+    if constexpr (PD == 64) {
+      *reinterpret_cast<uint16_t*>(np) = (uint16_t)nb;
+    } else if constexpr (PD == 128) {
+      *reinterpret_cast<uint32_t*>(np) = nb | (nb << 16);
+    } else {
+      uint2 w;
+      w.x = nb | (nb << 16);
+      w.y = w.x;
+      *reinterpret_cast<uint2*>(np) = w;
+    }
+  }
+}
+
+template <int PD>
+hipError_t launch_write(bool vec_ok, dim3 grid, hipStream_t stream, uint8_t* ks, uint8_t* vs,
+                        const void* key, const void* value, int dtype, int64_t k_st,
+                        int64_t k_sh, int64_t v_st, int64_t v_sh, const float* signs,
+                        const int32_t* slots, int64_t n, int H, int hd, int bs, int ebs,
+                        int64_t nslots, float scale) {
+  if (vec_ok)
+    hipLaunchKernelGGL((write_kernel<PD, true>), grid, dim3(256), 0, stream, ks, vs, key, value,
+                       dtype, k_st, k_sh, v_st, v_sh, signs, slots, n, H, hd, bs, ebs, nslots,
+                       scale);
+  else
+    hipLaunchKernelGGL((write_kernel<PD, false>), grid, dim3(256), 0, stream, ks, vs, key, value,
+                       dtype, k_st, k_sh, v_st, v_sh, signs, slots, n, H, hd, bs, ebs, nslots,
+                       scale);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+thread_local char g_err[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+}  // namespace tq
+
+extern "C" const char* tq_last_error(void) { return tq::g_err; }
+extern "C" int32_t tq_abi_version(void) { return 1; }
+
+extern "C" int tq_quantize_write_kv_cache(void* k_slab, void* v_slab, const void* key,
+                                          const void* value, int32_t in_dtype,
+                                          int64_t k_stride_tok, int64_t k_stride_head,
+                                          int64_t v_stride_tok, int64_t v_stride_head,
+                                          const float* signs, const int32_t* slot_mapping,
+                                          int64_t num_tokens, int32_t num_kv_heads,
+                                          int32_t head_dim, int32_t padded_dim,
+                                          int32_t block_size, int32_t ebs, int64_t num_blocks,
+                                          tq_stream_t stream) {
+  using namespace tq;
+  const int pd = padded_dim;
+  if (pd != 64 && pd != 128 && pd != 256) {
+    set_error("quantize_write: padded_dim must be 64, 128 or 256, got %d", pd);
+    return kEinval;
+  }
+  if (head_dim <= 0 || head_dim > pd || (pd > 64 && 2 * head_dim <= pd)) {
+    set_error("quantize_write: head_dim %d does not pad to %d", head_dim, pd);
+    return kEinval;
+  }
+  if (ebs % 16 != 0 || ebs < pd / 2 + 2 * (pd / 64)) {
+    set_error("quantize_write: ebs %d must be a multiple of 16 and >= %d", ebs,
+              pd / 2 + 2 * (pd / 64));
+    return kEinval;
+  }
+  if (in_dtype != TQ_F32 && in_dtype != TQ_F16 && in_dtype != TQ_BF16) {
+    set_error("quantize_write: unsupported input dtype %d", in_dtype);
+    return kEinval;
+  }
+  if (num_kv_heads <= 0 || block_size <= 0 || num_tokens < 0 || num_blocks < 0) {
+    set_error("quantize_write: bad sizes");
+    return kEinval;
+  }
+  if (num_tokens == 0) return 0;
+  if (!k_slab || !v_slab || !key || !value || !signs || !slot_mapping) {
+    set_error("quantize_write: null pointer");
+    return kEinval;
+  }
+  const int vec = pd / 32;
+  const int esz = in_dtype == TQ_F32 ? 4 : 2;
+  // vector loads need the full row, and every row start aligned to VEC elements
+  bool vec_ok = in_dtype == TQ_F16 && head_dim == pd &&
+                (k_stride_tok % vec == 0) && (k_stride_head % vec == 0) &&
+                (v_stride_tok % vec == 0) && (v_stride_head % vec == 0) &&
+                ((uintptr_t)key % (vec * esz) == 0) && ((uintptr_t)value % (vec * esz) == 0);
+  const int64_t vectors = 2 * num_tokens * (int64_t)num_kv_heads;
+  const int64_t blocks = (vectors + 7) / 8;
+  if (blocks > 0x7fffffffLL) {
+    set_error("quantize_write: too many tokens");
+    return kEinval;
+  }
+  const float scale = 1.0f / sqrtf((float)pd);
+  const int64_t nslots = num_blocks * (int64_t)block_size;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)blocks);
+  uint8_t* ks = static_cast<uint8_t*>(k_slab);
+  uint8_t* vs = static_cast<uint8_t*>(v_slab);
+  hipError_t e;
+  switch (pd) {
+    case 64:
+      e = launch_write<64>(vec_ok, grid, s, ks, vs, key, value, in_dtype, k_stride_tok,
+                           k_stride_head, v_stride_tok, v_stride_head, signs, slot_mapping,
+                           num_tokens, num_kv_heads, head_dim, block_size, ebs, nslots, scale);
+      break;
+    case 128:
+      e = launch_write<128>(vec_ok, grid, s, ks, vs, key, value, in_dtype, k_stride_tok,
+                            k_stride_head, v_stride_tok, v_stride_head, signs, slot_mapping,
+                            num_tokens, num_kv_heads, head_dim, block_size, ebs, nslots, scale);
+      break;
+    default:
+      e = launch_write<256>(vec_ok, grid, s, ks, vs, key, value, in_dtype, k_stride_tok,
+                            k_stride_head, v_stride_tok, v_stride_head, signs, slot_mapping,
+                            num_tokens, num_kv_heads, head_dim, block_size, ebs, nslots, scale);
+  }
+  if (e != hipSuccess) {
+    set_error("quantize_write: launch failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return 0;
+}

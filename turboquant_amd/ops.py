@@ -1,0 +1,185 @@
+"""torch-facing ops over the C ABI, registered under the reference's op names.
+
+* ``torch.ops.turboquant_write.quantize_write_kv_cache`` — schema of
+  csrc/src/quantize_write_binding.cu:285-286 (reference).
+* ``torch.ops.turboquant_v5.decode_v5_from_cache_paged_splitkv_ws`` — schema of
+  csrc/src/decode_v5_tc_binding.cu:966-973 (reference).
+
+Both launch on the current torch stream, allocate nothing and never sync, so
+they can be captured in a HIP graph.  They have a CUDA (= HIP on ROCm) kernel
+only: CPU tensors raise.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .geometry import entry_bytes
+
+_DTYPES = {torch.float32: _lib.TQ_F32, torch.float16: _lib.TQ_F16, torch.bfloat16: _lib.TQ_BF16}
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError("TurboQuant ops run on the GPU only; got a CPU tensor")
+
+
+def quantize_write_kv_cache(kv_cache: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                            signs: torch.Tensor, slot_mapping: torch.Tensor, head_dim: int,
+                            padded_dim: int) -> None:
+    """Quantize K/V [num_tokens, H, head_dim] and scatter into kv_cache in place.
+
+    kv_cache: uint8-addressable [2, num_blocks, block_size, H, ebs].  Mirrors
+    quantize_write_kv_cache (quantize_write_binding.cu:207-269) including its
+    checks; key/value may be fp32 (as the reference requires), fp16 or bf16.
+    """
+    _require_gpu(kv_cache, key, value, signs, slot_mapping)
+    if kv_cache.dim() != 5 or kv_cache.size(0) != 2:
+        raise RuntimeError("kv_cache leading dim must be 2 (K,V)")
+    if slot_mapping.dtype != torch.int32:
+        raise RuntimeError("slot_mapping must be int32")
+    if key.dtype not in _DTYPES or value.dtype != key.dtype:
+        raise RuntimeError(f"key/value must share a float dtype, got {key.dtype}/{value.dtype}")
+    if key.dim() != 3 or value.shape != key.shape:
+        raise RuntimeError("key/value must be [num_tokens, num_heads, head_dim]")
+    if key.stride(-1) != 1 or value.stride(-1) != 1:
+        raise RuntimeError("key/value last dim must be contiguous")
+    ebs = kv_cache.size(-1) * kv_cache.element_size()
+    if ebs % 16 != 0:
+        raise RuntimeError(f"kv_cache.size(-1) must be 16-byte aligned, got {ebs}")
+    if not kv_cache.is_contiguous():
+        raise RuntimeError("kv_cache must be contiguous")
+    if signs.dtype != torch.float32 or signs.numel() < padded_dim:
+        raise RuntimeError("signs must be fp32 [padded_dim]")
+    num_tokens = min(key.size(0), slot_mapping.numel())
+    if num_tokens == 0:
+        return
+    _, nb, bs, h, _ = kv_cache.shape
+    if key.size(1) != h:
+        raise RuntimeError(f"key has {key.size(1)} heads, cache has {h}")
+    lib = _lib.load()
+    base = kv_cache.data_ptr()
+    slab = nb * bs * h * ebs
+    with torch.cuda.device(kv_cache.device):
+        rc = lib.tq_quantize_write_kv_cache(
+            base, base + slab, key.data_ptr(), value.data_ptr(), _DTYPES[key.dtype],
+            key.stride(0), key.stride(1), value.stride(0), value.stride(1),
+            signs.data_ptr(), slot_mapping.data_ptr(), num_tokens, h, int(head_dim),
+            int(padded_dim), bs, ebs, nb, _stream_ptr(kv_cache.device))
+    _lib.check(rc, "quantize_write_kv_cache")
+
+
+def decode_paged_splitkv(q: torch.Tensor, kv_cache: torch.Tensor, indices: torch.Tensor,
+                         indptr: torch.Tensor, seq_lens: torch.Tensor, num_kv_heads: int,
+                         head_dim: int, padded_dim: int, sm_scale: float,
+                         signs: torch.Tensor | None, o: torch.Tensor, partition_o: torch.Tensor,
+                         partition_lse: torch.Tensor, num_splits: int,
+                         kv_chunk_size: int) -> torch.Tensor:
+    """Split-KV decode: q fp16 [B, Hq, pd] -> o fp16 [B, Hq, pd] (returned)."""
+    _require_gpu(q, kv_cache, indices, indptr, seq_lens, o, partition_o, partition_lse)
+    if q.dtype != torch.float16 or q.dim() != 3 or q.size(2) != padded_dim or q.stride(2) != 1:
+        raise RuntimeError("q must be fp16 [B, Hq, padded_dim] with a contiguous last dim")
+    b, hq, pd = q.shape
+    for t, name in ((indices, "indices"), (indptr, "indptr"), (seq_lens, "seq_lens")):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise RuntimeError(f"{name} must be a contiguous int32 tensor")
+    if seq_lens.numel() < b or indptr.numel() < b:
+        raise RuntimeError("seq_lens / indptr shorter than the batch")
+    if tuple(o.shape) != (b, hq, pd) or o.dtype != torch.float16 or not o.is_contiguous():
+        raise RuntimeError("o_ws shape mismatch")
+    if (partition_o.dtype != torch.float32 or partition_o.numel() < b * num_splits * hq * pd
+            or not partition_o.is_contiguous()):
+        raise RuntimeError("partition_o_ws shape/dtype mismatch")
+    if (partition_lse.dtype != torch.float32 or partition_lse.numel() < b * num_splits * hq
+            or not partition_lse.is_contiguous()):
+        raise RuntimeError("partition_lse_ws shape/dtype mismatch")
+    if kv_cache.dim() != 5 or kv_cache.size(0) != 2 or not kv_cache.is_contiguous():
+        raise RuntimeError("kv_cache must be contiguous [2, num_blocks, block_size, H, ebs]")
+    _, nb, bs, hk, _ = kv_cache.shape
+    if hk != num_kv_heads:
+        raise RuntimeError(f"kv_cache has {hk} kv heads, num_kv_heads={num_kv_heads}")
+    ebs = kv_cache.size(-1) * kv_cache.element_size()
+    sp = 0
+    if signs is not None and signs.numel() > 0:
+        if signs.dtype != torch.float32 or signs.numel() < pd:
+            raise RuntimeError("hadamard_signs must be fp32 [padded_dim]")
+        _require_gpu(signs)
+        sp = signs.data_ptr()
+    lib = _lib.load()
+    base = kv_cache.data_ptr()
+    slab = nb * bs * hk * ebs
+    with torch.cuda.device(q.device):
+        rc = lib.tq_decode_paged_splitkv(
+            q.data_ptr(), q.stride(0), q.stride(1), base, base + slab, indices.data_ptr(),
+            indptr.data_ptr(), seq_lens.data_ptr(), b, hq, int(num_kv_heads), int(head_dim),
+            int(padded_dim), bs, ebs, nb, float(sm_scale), sp, int(num_splits),
+            int(kv_chunk_size), partition_o.data_ptr(), partition_lse.data_ptr(), o.data_ptr(),
+            _stream_ptr(q.device))
+    _lib.check(rc, "decode_paged_splitkv")
+    return o
+
+
+# --------------------------------------------------------------------------
+# torch.library registration under the reference's namespaces and schemas
+# --------------------------------------------------------------------------
+_registered = False
+_libs = []
+
+
+def _reference_paged_splitkv(q, kv_cache, indices, indptr, last_page_len, seq_lens,
+                             num_kv_heads, page_size, head_dim, padded_dim, sm_scale,
+                             hadamard_signs, qbytes, nbytes, o_ws, max_len, partition_o_ws,
+                             partition_lse_ws, request_indices, kv_tile_indices, split_indptr,
+                             kv_chunk_size_t, num_splits):
+    """Argument adapter for decode_v5_from_cache_paged_splitkv_ws.
+
+    The chunk size is recomputed on the host as ceil(max_len / num_splits),
+    the value the reference backend stores in kv_chunk_size_t
+    (vllm_backend_fused.py:210-213), so no device tensor is read.
+    request_indices / kv_tile_indices / split_indptr are implied by
+    (batch, num_splits); last_page_len and nbytes are unused, as in the
+    reference op.
+    """
+    if int(padded_dim) != q.size(-1):
+        raise RuntimeError("padded_dim does not match q")
+    exp_q, _, _ = entry_bytes(int(head_dim))
+    if int(qbytes) != exp_q:
+        raise RuntimeError(f"qbytes {qbytes} does not match head_dim {head_dim}")
+    if int(max_len) <= 0:
+        raise RuntimeError("max_len must be positive")
+    if int(num_splits) < 1:
+        raise RuntimeError("num_splits must be >= 1")
+    cs = -(-int(max_len) // int(num_splits))
+    return decode_paged_splitkv(q, kv_cache, indices, indptr, seq_lens, int(num_kv_heads),
+                                int(head_dim), int(padded_dim), float(sm_scale), hadamard_signs,
+                                o_ws, partition_o_ws, partition_lse_ws, int(num_splits), cs)
+
+
+def register_ops() -> None:
+    """Define turboquant_write::* and turboquant_v5::* with the reference
+    schemas and bind the HIP implementations to the CUDA dispatch key."""
+    global _registered
+    if _registered:
+        return
+    from torch.library import Library
+    w = Library("turboquant_write", "DEF")
+    w.define("quantize_write_kv_cache(Tensor(a!) kv_cache, Tensor key, Tensor value, "
+             "Tensor signs, Tensor slot_mapping, int head_dim, int padded_dim) -> ()")
+    w.impl("quantize_write_kv_cache", quantize_write_kv_cache, "CUDA")
+    d = Library("turboquant_v5", "DEF")
+    d.define("decode_v5_from_cache_paged_splitkv_ws(Tensor q, Tensor kv_cache, "
+             "Tensor indices, Tensor indptr, Tensor last_page_len, Tensor seq_lens, "
+             "int num_kv_heads, int page_size, int head_dim, int padded_dim, "
+             "float sm_scale, Tensor hadamard_signs, int qbytes, int nbytes, "
+             "Tensor o_ws, int max_len, "
+             "Tensor partition_o_ws, Tensor partition_lse_ws, "
+             "Tensor request_indices, Tensor kv_tile_indices, "
+             "Tensor split_indptr, Tensor kv_chunk_size_t, int num_splits) -> Tensor")
+    d.impl("decode_v5_from_cache_paged_splitkv_ws", _reference_paged_splitkv, "CUDA")
+    _libs.extend([w, d])
+    _registered = True

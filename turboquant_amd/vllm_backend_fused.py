@@ -1,0 +1,319 @@
+"""TurboQuant vLLM attention backend on the MI355X HIP kernels.
+
+Drop-in for reference turboquant/vllm_backend_fused.py:32-468: same classes,
+static/class methods, constructor and forward signatures, cache shape and
+page-size hook; the kernels behind them are libtq_hip.so.
+
+    LLM(..., attention_backend="CUSTOM", kv_cache_dtype="fp8")
+
+fp8 selects a 1-byte allocation that this backend views as packed 4-bit codes
+plus fp16 norms, [2, num_blocks, block_size, num_kv_heads, ebs].
+
+vLLM is imported lazily-optional: when it is absent (unit tests, the CPU
+container) minimal stand-in base classes keep the module importable so the
+backend can be driven with a metadata object carrying the fields vLLM's
+FlashAttentionMetadata provides (max_query_len, num_actual_tokens,
+block_table, seq_lens, query_start_loc, slot_mapping).
+"""
+from __future__ import annotations
+
+import math
+import sys
+import traceback
+
+import torch
+import torch.nn.functional as F
+
+from .geometry import (QUANT_BYTES_PER_CHUNK, TILE_DIMS, choose_splits, entry_bytes,
+                       hadamard_signs, padded_dim)
+
+try:  # pragma: no cover - exercised only where vLLM is installed
+    from vllm.v1.attention.backends.flash_attn import (FlashAttentionBackend,
+                                                       FlashAttentionImpl,
+                                                       FlashAttentionMetadataBuilder)
+    HAVE_VLLM = True
+except Exception:  # vLLM absent: stand-ins with the pieces this module uses
+    HAVE_VLLM = False
+
+    class FlashAttentionBackend:  # type: ignore[no-redef]
+        accept_output_buffer = True
+
+        @staticmethod
+        def get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_size,
+                               cache_dtype_str="auto"):
+            if block_size % 16 != 0:
+                raise ValueError("Block size must be a multiple of 16.")
+            return (2, num_blocks, block_size, num_kv_heads, head_size)
+
+        @classmethod
+        def supports_kv_cache_dtype(cls, kv_cache_dtype) -> bool:
+            return kv_cache_dtype in (None, "auto")
+
+    class FlashAttentionImpl:  # type: ignore[no-redef]
+        def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes,
+                     sliding_window, kv_cache_dtype, *args, **kwargs):
+            self.num_heads = num_heads
+            self.head_size = head_size
+            self.scale = float(scale)
+            self.num_kv_heads = num_kv_heads
+            self.alibi_slopes = alibi_slopes
+            self.sliding_window = sliding_window
+            self.kv_cache_dtype = kv_cache_dtype
+            self.num_queries_per_kv = num_heads // num_kv_heads
+
+        def forward(self, *args, **kwargs):
+            raise NotImplementedError("fp16 KV cache path needs vLLM's FlashAttention")
+
+    class FlashAttentionMetadataBuilder:  # type: ignore[no-redef]
+        pass
+
+
+_FP8 = ("fp8", "fp8_e4m3")
+
+
+def _next_pow2(n):
+    return 1 if n <= 1 else 1 << (n - 1).bit_length()
+
+
+class TurboQuantBackend(FlashAttentionBackend):
+    """Backend "CUSTOM" (vllm_backend_fused.py:32-86)."""
+
+    # vLLM calls do_kv_cache_update separately from forward
+    forward_includes_kv_cache_update = False
+
+    @staticmethod
+    def get_name():
+        return "CUSTOM"
+
+    @staticmethod
+    def get_impl_cls():
+        return TurboQuantFusedImpl
+
+    @staticmethod
+    def get_builder_cls():
+        return TurboQuantMetadataBuilder
+
+    @classmethod
+    def supports_kv_cache_dtype(cls, kv_cache_dtype) -> bool:
+        if kv_cache_dtype in _FP8:
+            return True
+        return super().supports_kv_cache_dtype(kv_cache_dtype)
+
+    @staticmethod
+    def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int,
+                           head_size: int, cache_dtype_str: str = "auto") -> tuple[int, ...]:
+        if cache_dtype_str in _FP8:
+            _, _, ebs = entry_bytes(head_size)
+            return (2, num_blocks, block_size, num_kv_heads, ebs)
+        return FlashAttentionBackend.get_kv_cache_shape(num_blocks, block_size, num_kv_heads,
+                                                        head_size, cache_dtype_str)
+
+    @classmethod
+    def get_kv_cache_page_size(cls, block_size, num_kv_heads, head_size, dtype,
+                               cache_dtype_str="auto"):
+        """Bytes of one cache block for vLLM's page-size hook
+        (docker/vllm_patches/v1/attention/backend.py:94-113 in the reference)."""
+        if cache_dtype_str in _FP8:
+            _, _, ebs = entry_bytes(head_size)
+            return 2 * block_size * num_kv_heads * ebs
+        return None
+
+
+class TurboQuantMetadataBuilder(FlashAttentionMetadataBuilder):
+    pass
+
+
+class TurboQuantFusedImpl(FlashAttentionImpl):
+    """Quantized KV cache with the HIP kernels (vllm_backend_fused.py:93-468).
+
+    Write: do_kv_cache_update -> turboquant_write::quantize_write_kv_cache.
+    Decode: forward (max_query_len == 1) ->
+            turboquant_v5::decode_v5_from_cache_paged_splitkv_ws.
+    Prefill: attention over the fresh K/V of the batch (the reference's
+    prefill ignores cached context too, vllm_backend_fused.py:335-371).
+    """
+
+    def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes,
+                 sliding_window, kv_cache_dtype, *args, **kwargs):
+        self._real_cache_dtype = kv_cache_dtype
+        parent_dtype = "auto" if kv_cache_dtype in _FP8 else kv_cache_dtype
+        super().__init__(num_heads, head_size, scale, num_kv_heads, alibi_slopes,
+                         sliding_window, parent_dtype, *args, **kwargs)
+        self.kv_cache_dtype = self._real_cache_dtype
+        self._pd = padded_dim(self.head_size)
+        self._dc = self._pd // TILE_DIMS
+        self._qbytes = self._dc * QUANT_BYTES_PER_CHUNK
+        self._nbytes = self._dc * 2
+        self._signs = None
+        self._is_fp8 = kv_cache_dtype in _FP8
+        # (batch_size, max_pages_per_seq) -> workspace tensors
+        self._v5_ws_cache: dict[tuple[int, int], dict] = {}
+        self._decode_op = None
+        self._decode_op_name = None
+        self._write_op = None
+
+    # ---------------------------------------------------------------- setup
+    @staticmethod
+    def _choose_num_splits(batch_size: int, max_len: int, num_kv_heads: int,
+                           device: torch.device | None = None) -> int:
+        return choose_splits(batch_size, max_len, num_kv_heads)[0]
+
+    def _get_v5_ws(self, batch_size: int, max_pages: int, block_size: int,
+                   device: torch.device):
+        """Workspace keyed by (batch_size, max_pages) as in the reference
+        (vllm_backend_fused.py:158-215): allocated on the first call of a
+        shape bucket (vLLM warm-up), reused by graph replays.
+        Returns (ws, max_len, num_splits)."""
+        key = (batch_size, max_pages)
+        max_len = max_pages * block_size
+        ws = self._v5_ws_cache.get(key)
+        if ws is None:
+            num_splits, chunk = choose_splits(batch_size, max_len, self.num_kv_heads)
+            padded_batch = batch_size * num_splits
+            arange = torch.arange(padded_batch, dtype=torch.int32, device=device)
+            ws = {
+                "o": torch.empty((batch_size, self.num_heads, self._pd), dtype=torch.float16,
+                                 device=device),
+                "num_splits": num_splits,
+                "partition_o": torch.empty((padded_batch, self.num_heads, self._pd),
+                                           dtype=torch.float32, device=device),
+                "partition_lse": torch.empty((padded_batch, self.num_heads),
+                                             dtype=torch.float32, device=device),
+                "request_indices": (arange // num_splits).to(torch.int32),
+                "kv_tile_indices": (arange % num_splits).to(torch.int32),
+                "split_indptr": torch.arange(batch_size + 1, dtype=torch.int32,
+                                             device=device) * num_splits,
+                # ceil(max_len / num_splits); the op recomputes it on the host
+                "kv_chunk_size": torch.tensor([-(-max_len // num_splits)], dtype=torch.int32,
+                                              device=device),
+            }
+            self._v5_ws_cache[key] = ws
+        return ws, max_len, ws["num_splits"]
+
+    def _ensure(self, dev):
+        if self._signs is not None:
+            return
+        self._signs = hadamard_signs(self._pd, device=dev)
+
+    def _ensure_kernels_loaded(self):
+        if self._decode_op is None or self._write_op is None:
+            from . import ops
+            from .decoder_dispatch import pick_decode_op
+            ops.register_ops()
+            self._write_op = torch.ops.turboquant_write.quantize_write_kv_cache
+            self._decode_op, self._decode_op_name = pick_decode_op()
+
+    # ---------------------------------------------------------------- write
+    def _write_to_cache(self, key, value, kv_cache, slot_mapping):
+        num_tokens = slot_mapping.shape[0]
+        self._ensure_kernels_loaded()
+        sm = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
+        # fp16/bf16/fp32 rows go in as they are (the kernel converts exactly);
+        # the reference's .float() copy is not needed
+        self._write_op(kv_cache, key[:num_tokens], value[:num_tokens], self._signs, sm,
+                       self.head_size, self._pd)
+
+    @torch.no_grad()
+    def do_kv_cache_update(self, layer, key, value, kv_cache, slot_mapping):
+        self._ensure(key.device)
+        if self._is_fp8:
+            self._write_to_cache(key, value, kv_cache, slot_mapping)
+        else:  # pragma: no cover - needs vLLM
+            from vllm.v1.attention.backends.fa_utils import reshape_and_cache_flash
+            num_tokens = slot_mapping.shape[0]
+            key_cache, value_cache = kv_cache.unbind(0)
+            reshape_and_cache_flash(key[:num_tokens], value[:num_tokens], key_cache,
+                                    value_cache, slot_mapping, self.kv_cache_dtype,
+                                    layer._k_scale, layer._v_scale)
+
+    # -------------------------------------------------------------- forward
+    def _prefill_fresh(self, query, key, value, attn_metadata, output):
+        """Causal attention of each prompt chunk over its own fresh K/V."""
+        n = attn_metadata.num_actual_tokens
+        qsl = attn_metadata.query_start_loc.tolist()
+        g = self.num_heads // self.num_kv_heads
+        for i in range(len(qsl) - 1):
+            a, b = qsl[i], qsl[i + 1]
+            if b <= a:
+                continue
+            q = query[a:b].to(torch.float16).transpose(0, 1)
+            k = key[a:b].to(torch.float16).transpose(0, 1).repeat_interleave(g, dim=0)
+            v = value[a:b].to(torch.float16).transpose(0, 1).repeat_interleave(g, dim=0)
+            o = F.scaled_dot_product_attention(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
+                                               is_causal=True, scale=self.scale)
+            output[a:b] = o.squeeze(0).transpose(0, 1).to(output.dtype)
+        return output
+
+    @torch.no_grad()
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
+                output_scale=None, **kwargs):
+        if attn_metadata is None:
+            if output is None:
+                output = torch.zeros_like(query)
+            return output
+
+        is_decode = attn_metadata.max_query_len == 1
+        if not is_decode:
+            if self._is_fp8:
+                num_tokens = attn_metadata.num_actual_tokens
+                if output is None:
+                    output = torch.empty_like(query[:num_tokens])
+                q = query[:num_tokens].view(num_tokens, self.num_heads, self.head_size)
+                k = key[:num_tokens].view(num_tokens, self.num_kv_heads, self.head_size)
+                v = value[:num_tokens].view(num_tokens, self.num_kv_heads, self.head_size)
+                out3 = output[:num_tokens].view(num_tokens, self.num_heads, self.head_size)
+                self._prefill_fresh(q, k, v, attn_metadata, out3)
+                return output
+            return super().forward(layer, query, key, value, kv_cache, attn_metadata,
+                                   output, output_scale, **kwargs)
+
+        num_actual = attn_metadata.num_actual_tokens
+        q = query[:num_actual]
+        if output is None:
+            output = torch.empty_like(q)
+        block_table = attn_metadata.block_table
+        seq_lens = attn_metadata.seq_lens
+        try:
+            self._ensure_kernels_loaded()
+            if not self._is_fp8:
+                return super().forward(layer, query, key, value, kv_cache, attn_metadata,
+                                       output, output_scale, **kwargs)
+            self._ensure(q.device)
+            block_size = kv_cache.shape[2]
+            # strided page table: static shapes, capturable
+            num_pages = (seq_lens + block_size - 1) // block_size
+            max_pages = block_table.shape[1]
+            kv_indptr = torch.arange(seq_lens.shape[0] + 1, dtype=torch.int32,
+                                     device=q.device) * max_pages
+            kv_last_page_len = seq_lens - (num_pages - 1) * block_size
+            kv_indices = block_table.reshape(-1)
+            if kv_indices.dtype != torch.int32:
+                kv_indices = kv_indices.to(torch.int32)
+            q3 = q.view(num_actual, self.num_heads, self.head_size)
+            q_fp16 = q3.to(torch.float16)
+            if self.head_size < self._pd:
+                q_fp16 = F.pad(q_fp16, (0, self._pd - self.head_size))
+            batch_size = q_fp16.shape[0]
+            ws, max_len, num_splits = self._get_v5_ws(batch_size, max_pages, block_size,
+                                                      q.device)
+            sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+            result = self._decode_op(
+                q_fp16, kv_cache, kv_indices, kv_indptr, kv_last_page_len, sl,
+                self.num_kv_heads, block_size, self.head_size, self._pd, self.scale,
+                self._signs, self._qbytes, self._nbytes, ws["o"], max_len,
+                ws["partition_o"], ws["partition_lse"], ws["request_indices"],
+                ws["kv_tile_indices"], ws["split_indptr"], ws["kv_chunk_size"], num_splits)
+            out3 = output[:num_actual].view(num_actual, self.num_heads, self.head_size)
+            if self.head_size < self._pd:
+                out3.copy_(result[:num_actual, :, :self.head_size])
+            else:
+                out3.copy_(result[:num_actual])
+        except Exception as e:
+            print(f"[TQ] Decode kernel failed: {e}", file=sys.stderr, flush=True)
+            traceback.print_exc(file=sys.stderr)
+            # an fp8 (packed) cache cannot be read by anything else: re-raise
+            if self._is_fp8:
+                raise
+            return super().forward(layer, query, key, value, kv_cache, attn_metadata, output,
+                                   output_scale, **kwargs)
+        return output
