@@ -4,7 +4,7 @@
 // (turboquant/triton_decode_ref.py:89-131, :264-299) computed in the rotated
 // domain as the reference's v5 kernel does
 // (csrc/include/flashinfer_decode_turboquant_v5_tc.cuh:106-795): q is rotated
-// once, q' = fp16(FWHT(s*q)/sqrt(pd)); K^ = codebook[code]*norm/sqrt(pd);
+// once, q' = FWHT(s*q)/sqrt(pd); K^ = codebook[code]*norm/sqrt(pd);
 // softmax(q'.K^ * sm_scale) V^ per split, LSE merge across splits
 // (flashinfer_decode_turboquant_combine.cuh:18-79), then the inverse rotation
 // o = s * FWHT(o')/sqrt(pd), applied once per (sequence, head) after the merge.
@@ -15,7 +15,8 @@
 //    cache lines, so a workgroup consumes whole lines.
 //  * A 16-token tile is one MFMA block.  QK^T: v_mfma_f32_16x16x32_f16 with
 //    A = dequantized K (row = token, lane l loads 16 B of token l%16 with one
-//    dwordx4), B = q' (column = q head; GQA heads padded to 16).  The C layout
+//    dwordx4), B = q' as fp16 hi + lo parts (column = q head; GQA heads
+//    padded to 16).  The C layout
 //    (row 4*(l/16)+r = token, column l%16 = head) is exactly the B layout of
 //    the PV product v_mfma_f32_16x16x16_f16 (A = V^T: row = dim slot l%16,
 //    k = tokens 4*(l/16)..+3), so probabilities never leave registers.
@@ -25,7 +26,10 @@
 //    byte tables (high and low byte of the fp16 value), the sign is OR-ed into
 //    the high byte, and v_perm interleaves the bytes into packed fp16 pairs.
 //  * The K norm scales the score; the V norm and 1/sqrt(pd) fold into the
-//    fp16 probability, so dequantized operands are raw codebook values.
+//    probability, so dequantized operands are (scaled) codebook values.
+//  * Accuracy: q' and the probabilities enter the MFMAs as fp16 hi + lo
+//    pairs and the codebook tables are pre-scaled to fp16-friendly values,
+//    keeping the result within ~1e-3 of fp32 math even for heavy-tailed keys.
 //  * Online softmax in the exp2 domain with a lazy rescale (the running max
 //    only moves when a tile exceeds it by more than 2^3), bounding p <= 8.
 #include <math.h>
@@ -42,11 +46,17 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// fp16 bit patterns of the positive centroids c[8+m], m = 0..7:
-// 0x301c 0x3636 0x3941 0x3b8a 0x3d06 0x3e79 0x4024 0x4177, split into a
-// high-byte table and a low-byte table of 8 bytes each (2 dwords, m = byte).
-constexpr uint32_t kHi0 = 0x3b393630u, kHi1 = 0x41403e3du;
-constexpr uint32_t kLo0 = 0x8a41361cu, kLo1 = 0x77247906u;
+// The dequant tables hold fp16(kCbScale * c[8+m]), m = 0..7: the positive
+// centroids scaled by kCbScale = 1.48098 (fp32 0x3fbd90c1), a factor chosen by
+// search so that all eight products sit close to fp16 grid points (max
+// relative rounding error 8.7e-5 instead of 4.7e-4 for the unscaled values).
+// 1/kCbScale is folded into the score and probability scales, so the math is
+// unchanged and the fp16 operands carry ~5x less codebook rounding.
+// fp16 bits: 0x3216 0x3899 0x3bc8 0x3d95 0x3f71 0x40cb 0x4221 0x440c, split
+// into a high-byte table and a low-byte table of 8 bytes each (byte m).
+constexpr float kCbScale = 1.4809800386428833f;
+constexpr uint32_t kHi0 = 0x3d3b3832u, kHi1 = 0x4442403fu;
+constexpr uint32_t kLo0 = 0x95c89916u, kLo1 = 0x0c21cb71u;
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
   // byte i of the result = byte sel_i of the 8-byte value {hi:lo} (lo = bytes 0-3)
@@ -107,8 +117,9 @@ struct DecodeParams {
   float* plse;
   int64_t num_blocks;
   int B, Hq, Hkv, ratio, block_size, ebs, S, cs, G, HG;
-  float qk_scale;     // sm_scale * log2(e) / sqrt(pd)
+  float qk_scale;     // sm_scale * log2(e) / (sqrt(pd) * kCbScale)
   float inv_sqrt_pd;  // 1/sqrt(pd)
+  float pv_scale;     // 1/(sqrt(pd) * kCbScale)
 };
 
 template <int PD>
@@ -230,7 +241,10 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
   }
   const float qsc = p.signs ? p.inv_sqrt_pd : 1.0f;
   // B operand of the QK MFMA: column n = q head, 8 dims of quarter q4 per MFMA
-  half8_t qop[KD];
+  // q' is split into fp16 high and low parts (q' = hi + lo to ~22 bits), two
+  // MFMAs per K block, so the scores keep fp32-level accuracy even for
+  // heavy-tailed keys; the dequantized K values are exact fp16 centroids.
+  half8_t qhi[KD], qlo[KD];
   {
     constexpr int ord[8] = {1, 3, 5, 7, 0, 2, 4, 6};
 #pragma unroll
@@ -238,7 +252,10 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         const int d = q4 * (PD / 4) + 8 * c + ord[e];
-        qop[c][e] = (n < ratio) ? (_Float16)(qs[n * PD + d] * qsc) : (_Float16)0.0f;
+        const float x = (n < ratio) ? qs[n * PD + d] * qsc : 0.0f;
+        const _Float16 hi = (_Float16)x;
+        qhi[c][e] = hi;
+        qlo[c][e] = (_Float16)(x - (float)hi);
       }
     }
   }
@@ -266,8 +283,9 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
       for (int c = 0; c < KD; c++) {
         uint32_t x[4];
         dq8(cur.k[c], x);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(x[0], x[1], x[2], x[3]), qop[c],
-                                                     acc, 0, 0, 0);
+        const half8_t kv8 = as_half8(x[0], x[1], x[2], x[3]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qhi[c], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qlo[c], acc, 0, 0, 0);
       }
       const float nk[4] = {h2f(quad_bcast<0>(cur.nk)), h2f(quad_bcast<1>(cur.nk)),
                            h2f(quad_bcast<2>(cur.nk)), h2f(quad_bcast<3>(cur.nk))};
@@ -300,10 +318,15 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
         pr[r] = valid[r] ? __builtin_amdgcn_exp2f(sc[r] - m) : 0.0f;
         lsum += pr[r];
       }
-      half4_t pv;
+      // fp16 hi + lo parts of p * norm_v / (sqrt(pd) * kCbScale)
+      half4_t pvh, pvl;
 #pragma unroll
-      for (int r = 0; r < 4; r++)
-        pv[r] = valid[r] ? (_Float16)(pr[r] * nv[r] * p.inv_sqrt_pd) : (_Float16)0.0f;
+      for (int r = 0; r < 4; r++) {
+        const float x = valid[r] ? pr[r] * nv[r] * p.pv_scale : 0.0f;
+        const _Float16 hi = (_Float16)x;
+        pvh[r] = hi;
+        pvl[r] = (_Float16)(x - (float)hi);
+      }
 
       // ---- O[h][dim slot] += V^T P^T
       uint32_t e[VB];
@@ -322,10 +345,11 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
       for (int k = 0; k < VB; k++) {
         uint32_t x[4];
         dq8(e[k], x);
-        O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_half4(x[0], x[1]), pv,
-                                                             O[2 * k + 1], 0, 0, 0);
-        O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_half4(x[2], x[3]), pv, O[2 * k],
-                                                         0, 0, 0);
+        const half4_t lo4 = as_half4(x[0], x[1]), hi4 = as_half4(x[2], x[3]);
+        O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo4, pvh, O[2 * k + 1], 0, 0, 0);
+        O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo4, pvl, O[2 * k + 1], 0, 0, 0);
+        O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi4, pvh, O[2 * k], 0, 0, 0);
+        O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi4, pvl, O[2 * k], 0, 0, 0);
       }
       if (tile < tile1) {
         cur = nxt;
@@ -354,34 +378,66 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
   }
 }
 
+// LSE merge of the splits of one (sequence, q head), inverse rotation, fp16
+// store.  256 threads: split weights are computed once into LDS, then
+// 256/(PD/4) split groups each sum a strided subset of the splits for one
+// float4 column, a tree in LDS adds the groups, and wave 0 runs the inverse
+// FWHT across its 64 lanes.
 template <int PD>
-__global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ po,
-                                                     const float* __restrict__ plse, int S,
-                                                     int Hq, const float* __restrict__ signs,
-                                                     float inv_sqrt_pd, _Float16* __restrict__ o) {
-  constexpr int V = PD / 64;
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ po,
+                                                      const float* __restrict__ plse, int S,
+                                                      int Hq, const float* __restrict__ signs,
+                                                      float inv_sqrt_pd, _Float16* __restrict__ o) {
+  constexpr int C = PD / 4;        // float4 columns
+  constexpr int NG = 256 / C;      // split groups
+  constexpr int V = PD / 64;       // dims per lane in the FWHT
+  extern __shared__ float sm[];    // [S] weights, then [NG][PD] partial sums
+  __shared__ float red[8];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int b = blockIdx.x / Hq, h = blockIdx.x % Hq;
+  const int64_t row0 = (int64_t)b * S * Hq + h;  // row of split s: row0 + s*Hq
+
   float mx = -INFINITY;
-  for (int s = 0; s < S; s++) mx = fmaxf(mx, plse[((int64_t)b * S + s) * Hq + h]);
-  float acc[V];
+  for (int s = tid; s < S; s += 256) mx = fmaxf(mx, plse[row0 + (int64_t)s * Hq]);
 #pragma unroll
-  for (int i = 0; i < V; i++) acc[i] = 0.f;
-  if (mx > -INFINITY) {
-    float den = 0.f;
-    for (int s = 0; s < S; s++) {
-      const int64_t row = ((int64_t)b * S + s) * Hq + h;
-      const float l = plse[row];
-      if (!(l > -INFINITY)) continue;
-      const float wgt = __expf(l - mx);
-      den += wgt;
-      const float* src = po + row * PD + lane * V;
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if (lane == 0) red[wv] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float den = 0.f;
+  for (int s = tid; s < S; s += 256) {
+    const float l = plse[row0 + (int64_t)s * Hq];
+    const float wgt = (l > -INFINITY && mx > -INFINITY) ? __expf(l - mx) : 0.0f;
+    sm[s] = wgt;
+    den += wgt;
+  }
 #pragma unroll
-      for (int i = 0; i < V; i++) acc[i] += wgt * src[i];
+  for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off);
+  __syncthreads();  // red[] reads done, weights visible
+  if (lane == 0) red[4 + wv] = den;
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const int col = tid % C, grp = tid / C;
+  for (int s = grp; s < S; s += NG) {
+    const float wgt = sm[s];
+    if (wgt != 0.0f) {
+      const float4_t v = *reinterpret_cast<const float4_t*>(po + (row0 + (int64_t)s * Hq) * PD + col * 4);
+      acc += wgt * v;
     }
-    const float inv = 1.0f / den;
+  }
+  __syncthreads();  // weights no longer needed; reuse LDS for group sums
+  float* part = sm;
+  *reinterpret_cast<float4_t*>(part + grp * PD + col * 4) = acc;
+  __syncthreads();
+  if (wv == 0) {
+    den = (red[4] + red[5]) + (red[6] + red[7]);
+    const float inv = den > 0.f ? 1.0f / den : 0.0f;
+    float x[V];
 #pragma unroll
-    for (int i = 0; i < V; i++) acc[i] *= inv;
+    for (int i = 0; i < V; i++) {
+      float t = 0.f;
+      for (int g = 0; g < NG; g++) t += part[g * PD + lane * V + i];
+      x[i] = t * inv;
+    }
     if (signs) {
 #pragma unroll
       for (int hh = 1; hh < V; hh <<= 1)
@@ -389,24 +445,24 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ p
         for (int i = 0; i < V; i += 2 * hh)
 #pragma unroll
           for (int k = 0; k < hh; k++) {
-            const float a = acc[i + k], c = acc[i + k + hh];
-            acc[i + k] = a + c;
-            acc[i + k + hh] = a - c;
+            const float a = x[i + k], c = x[i + k + hh];
+            x[i + k] = a + c;
+            x[i + k + hh] = a - c;
           }
 #pragma unroll
       for (int delta = 1; delta < 64; delta <<= 1)
 #pragma unroll
         for (int i = 0; i < V; i++) {
-          const float partner = __shfl_xor(acc[i], delta);
-          acc[i] = (lane & delta) ? (partner - acc[i]) : (acc[i] + partner);
+          const float partner = __shfl_xor(x[i], delta);
+          x[i] = (lane & delta) ? (partner - x[i]) : (x[i] + partner);
         }
 #pragma unroll
-      for (int i = 0; i < V; i++) acc[i] = acc[i] * inv_sqrt_pd * signs[lane * V + i];
+      for (int i = 0; i < V; i++) x[i] = x[i] * inv_sqrt_pd * signs[lane * V + i];
     }
-  }
-  _Float16* dst = o + ((int64_t)b * Hq + h) * PD + lane * V;
+    _Float16* dst = o + ((int64_t)b * Hq + h) * PD + lane * V;
 #pragma unroll
-  for (int i = 0; i < V; i++) dst[i] = (_Float16)acc[i];
+    for (int i = 0; i < V; i++) dst[i] = (_Float16)x[i];
+  }
 }
 
 int check_geometry(int pd, int hq, int hkv, int bs, int ebs, const char* who) {
@@ -490,7 +546,8 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   p.G = G;
   p.HG = num_kv_heads / G;
   p.inv_sqrt_pd = 1.0f / sqrtf((float)pd);
-  p.qk_scale = sm_scale * 1.4426950408889634f * p.inv_sqrt_pd;
+  p.qk_scale = sm_scale * 1.4426950408889634f * p.inv_sqrt_pd / kCbScale;
+  p.pv_scale = p.inv_sqrt_pd / kCbScale;
   const int64_t blocks = (int64_t)batch * num_splits * p.HG;
   if (blocks > 0x7fffffffLL) {
     set_error("decode: grid too large");
@@ -544,18 +601,24 @@ extern "C" int tq_combine_splits(const float* partition_o, const float* partitio
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const float isq = 1.0f / sqrtf((float)pd);
   _Float16* out = static_cast<_Float16*>(o);
-  dim3 grid((unsigned)blocks), block(64);
+  // LDS: split weights, later reused for the group partial sums (256*4 floats)
+  const size_t lds = sizeof(float) * (size_t)(num_splits > 1024 ? num_splits : 1024);
+  if (lds > 60 * 1024) {
+    set_error("combine: num_splits %d too large", num_splits);
+    return kEinval;
+  }
+  dim3 grid((unsigned)blocks), block(256);
   switch (pd) {
     case 64:
-      hipLaunchKernelGGL(combine_kernel<64>, grid, block, 0, st, partition_o, partition_lse,
+      hipLaunchKernelGGL(combine_kernel<64>, grid, block, lds, st, partition_o, partition_lse,
                          num_splits, num_qo_heads, signs, isq, out);
       break;
     case 128:
-      hipLaunchKernelGGL(combine_kernel<128>, grid, block, 0, st, partition_o, partition_lse,
+      hipLaunchKernelGGL(combine_kernel<128>, grid, block, lds, st, partition_o, partition_lse,
                          num_splits, num_qo_heads, signs, isq, out);
       break;
     default:
-      hipLaunchKernelGGL(combine_kernel<256>, grid, block, 0, st, partition_o, partition_lse,
+      hipLaunchKernelGGL(combine_kernel<256>, grid, block, lds, st, partition_o, partition_lse,
                          num_splits, num_qo_heads, signs, isq, out);
   }
   hipError_t e = hipGetLastError();
