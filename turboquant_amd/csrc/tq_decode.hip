@@ -115,7 +115,7 @@ struct DecodeParams {
   const float* signs;
   float* po;
   float* plse;
-  int64_t num_blocks;
+  int num_blocks;  // clamped to INT_MAX (page ids are int32)
   int B, Hq, Hkv, ratio, block_size, ebs, S, cs, G, HG;
   float qk_scale;     // sm_scale * log2(e) / (sqrt(pd) * kCbScale)
   float inv_sqrt_pd;  // 1/sqrt(pd)
@@ -124,69 +124,56 @@ struct DecodeParams {
 
 template <int PD>
 struct Tile {
-  static constexpr int KD = PD / 32;            // K dwords per lane = QK MFMAs
-  static constexpr int VB = PD / 32;            // V bytes per lane per token
+  static constexpr int KD = PD / 32;               // K dwords per lane = QK MFMA pairs
+  static constexpr int VB = PD / 32;               // V bytes per lane per token
   static constexpr int VW = VB >= 4 ? VB / 4 : 1;  // V dwords per lane per token
   uint32_t k[KD];
   uint32_t v[4][VW];
   uint32_t nk, nv;
 };
 
+// Per-lane byte offsets inside one 16-token tile of one kv head, relative to
+// the tile's first entry (constant over the whole loop).
+struct LaneOffsets {
+  uint32_t k;     // K codes: token n, bytes [q4*PD/8, (q4+1)*PD/8)
+  uint32_t v[4];  // V codes: token 4*q4 + j, bytes [n*PD/32, (n+1)*PD/32)
+  uint32_t nrm;   // norm of token 4*q4 + (lane & 3)
+};
+
+// Issue the loads of one tile through buffer resources whose base is the
+// tile's first entry of this kv head (wave-uniform) and whose size is the
+// tile's extent, or 0 for a tile that is not fetched: out-of-range buffer
+// loads return zeros without touching memory, so every tile issues the same
+// instruction sequence and the load counters stay in order.
 template <int PD>
-__device__ __forceinline__ void load_tile(const DecodeParams& p, int b, int kvh, int tile,
-                                          int lane, bool& ok, Tile<PD>& t) {
-  constexpr int KB = PD / 8;
-  constexpr int VB = PD / 32;
-  const int T = tile * kTile;
-  int page = p.indices[p.indptr[b] + T / p.block_size];
-  page = __builtin_amdgcn_readfirstlane(page);
-  ok = page >= 0 && (int64_t)page < p.num_blocks;
-  if (!ok) {
-#pragma unroll
-    for (int i = 0; i < Tile<PD>::KD; i++) t.k[i] = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-      for (int i = 0; i < Tile<PD>::VW; i++) t.v[j][i] = 0;
-    t.nk = t.nv = 0;
-    return;
-  }
-  const int64_t tokstride = (int64_t)p.Hkv * p.ebs;
-  const int64_t rowbase =
-      ((int64_t)page * p.block_size + (T % p.block_size)) * tokstride + (int64_t)kvh * p.ebs;
-  const int q4 = lane >> 4, n = lane & 15;
-  // K: token n, bytes [q4*KB, (q4+1)*KB)
-  const uint8_t* kp = p.ks + rowbase + n * tokstride + q4 * KB;
+__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
+                                          const LaneOffsets& o, Tile<PD>& t) {
   if constexpr (PD == 64) {
-    u32x2 w = *reinterpret_cast<const u32x2*>(kp);
+    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(kr, o.k, 0, 0);
     t.k[0] = w[0]; t.k[1] = w[1];
   } else if constexpr (PD == 128) {
-    u32x4 w = *reinterpret_cast<const u32x4*>(kp);
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(kr, o.k, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; i++) t.k[i] = w[i];
   } else {
-    u32x4 w0 = *reinterpret_cast<const u32x4*>(kp);
-    u32x4 w1 = *reinterpret_cast<const u32x4*>(kp + 16);
+    const u32x4 w0 = __builtin_amdgcn_raw_buffer_load_b128(kr, o.k, 0, 0);
+    const u32x4 w1 = __builtin_amdgcn_raw_buffer_load_b128(kr, o.k + 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; i++) { t.k[i] = w0[i]; t.k[4 + i] = w1[i]; }
   }
-  // V: tokens 4*q4 + j, bytes [n*VB, (n+1)*VB)
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    const uint8_t* vp = p.vs + rowbase + (4 * q4 + j) * tokstride + n * VB;
     if constexpr (PD == 64) {
-      t.v[j][0] = *reinterpret_cast<const uint16_t*>(vp);
+      t.v[j][0] = __builtin_amdgcn_raw_buffer_load_b16(vr, o.v[j], 0, 0);
     } else if constexpr (PD == 128) {
-      t.v[j][0] = *reinterpret_cast<const uint32_t*>(vp);
+      t.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(vr, o.v[j], 0, 0);
     } else {
-      u32x2 w = *reinterpret_cast<const u32x2*>(vp);
+      const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(vr, o.v[j], 0, 0);
       t.v[j][0] = w[0]; t.v[j][1] = w[1];
     }
   }
-  // norms of token 4*q4 + (lane & 3), broadcast within the quad later
-  const int64_t noff = rowbase + (4 * q4 + (lane & 3)) * tokstride + PD / 2;
-  t.nk = *reinterpret_cast<const uint16_t*>(p.ks + noff);
-  t.nv = *reinterpret_cast<const uint16_t*>(p.vs + noff);
+  t.nk = __builtin_amdgcn_raw_buffer_load_b16(kr, o.nrm, 0, 0);
+  t.nv = __builtin_amdgcn_raw_buffer_load_b16(vr, o.nrm, 0, 0);
 }
 
 // 4x4 byte transpose: E_k byte j = byte k of D_j
@@ -200,15 +187,109 @@ __device__ __forceinline__ void transpose4(uint32_t d0, uint32_t d1, uint32_t d2
   e[3] = perm(b23, b01, 0x07060302u);
 }
 
+// Online-softmax state of one wave: O[i][r] = unnormalised o[h = n][dim
+// (4*q4 + r)*NO + i] in the rotated domain, m = running max (log2 units, per
+// column h), lsum = this lane's share of the denominator.
+template <int PD>
+struct SoftmaxState {
+  static constexpr int NO = PD / 16;
+  float4_t O[NO];
+  float m;
+  float lsum;
+};
+
+template <int PD>
+__device__ __forceinline__ void attend_tile(const Tile<PD>& cur, bool ok, int tile, int c0,
+                                            int c1, int q4, int n, int ratio,
+                                            const half8_t* qhi, const half8_t* qlo,
+                                            float qk_scale, float pv_scale,
+                                            SoftmaxState<PD>& st) {
+  constexpr int KD = PD / 32;
+  constexpr int VB = PD / 32;
+  constexpr int NO = PD / 16;
+  // ---- scores S[t = 4*q4 + r][h = n]
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < KD; c++) {
+    uint32_t x[4];
+    dq8(cur.k[c], x);
+    const half8_t kv8 = as_half8(x[0], x[1], x[2], x[3]);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qhi[c], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qlo[c], acc, 0, 0, 0);
+  }
+  const float nk[4] = {h2f(quad_bcast<0>(cur.nk)), h2f(quad_bcast<1>(cur.nk)),
+                       h2f(quad_bcast<2>(cur.nk)), h2f(quad_bcast<3>(cur.nk))};
+  const float nv[4] = {h2f(quad_bcast<0>(cur.nv)), h2f(quad_bcast<1>(cur.nv)),
+                       h2f(quad_bcast<2>(cur.nv)), h2f(quad_bcast<3>(cur.nv))};
+  const int tbase = tile * kTile + 4 * q4;
+  float sc[4];
+  bool valid[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int t = tbase + r;
+    valid[r] = ok && t >= c0 && t < c1;
+    sc[r] = valid[r] ? acc[r] * nk[r] * qk_scale : -INFINITY;
+  }
+  float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+  const float m_new = fmaxf(st.m, tmax);
+  const bool need = (n < ratio) && (m_new > st.m + 3.0f);
+  if (__any(need)) {
+    const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(st.m - m_new);
+#pragma unroll
+    for (int i = 0; i < NO; i++) st.O[i] *= alpha;
+    st.lsum *= alpha;
+    st.m = m_new;
+  }
+  float pr[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    pr[r] = valid[r] ? __builtin_amdgcn_exp2f(sc[r] - st.m) : 0.0f;
+    st.lsum += pr[r];
+  }
+  // fp16 hi + lo parts of p * norm_v / (sqrt(pd) * kCbScale)
+  half4_t pvh, pvl;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const float x = valid[r] ? pr[r] * nv[r] * pv_scale : 0.0f;
+    const _Float16 hi = (_Float16)x;
+    pvh[r] = hi;
+    pvl[r] = (_Float16)(x - (float)hi);
+  }
+  // ---- O[h][dim slot] += V^T P^T
+  uint32_t e[VB];
+  if constexpr (PD == 64) {
+    const uint32_t p01 = cur.v[0][0] | (cur.v[1][0] << 16);
+    const uint32_t p23 = cur.v[2][0] | (cur.v[3][0] << 16);
+    e[0] = perm(p23, p01, 0x06040200u);
+    e[1] = perm(p23, p01, 0x07050301u);
+  } else if constexpr (PD == 128) {
+    transpose4(cur.v[0][0], cur.v[1][0], cur.v[2][0], cur.v[3][0], e);
+  } else {
+    transpose4(cur.v[0][0], cur.v[1][0], cur.v[2][0], cur.v[3][0], e);
+    transpose4(cur.v[0][1], cur.v[1][1], cur.v[2][1], cur.v[3][1], e + 4);
+  }
+#pragma unroll
+  for (int k = 0; k < VB; k++) {
+    uint32_t x[4];
+    dq8(e[k], x);
+    const half4_t lo4 = as_half4(x[0], x[1]), hi4 = as_half4(x[2], x[3]);
+    st.O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo4, pvh, st.O[2 * k + 1], 0, 0, 0);
+    st.O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo4, pvl, st.O[2 * k + 1], 0, 0, 0);
+    st.O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi4, pvh, st.O[2 * k], 0, 0, 0);
+    st.O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi4, pvl, st.O[2 * k], 0, 0, 0);
+  }
+}
+
 template <int PD>
 __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
   constexpr int KD = PD / 32;
-  constexpr int VB = PD / 32;
   constexpr int NO = PD / 16;  // PV MFMAs = dim slots per lane
   extern __shared__ float smem[];
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int q4 = lane >> 4, n = lane & 15;
   int bid = blockIdx.x;
   const int hg = bid % p.HG;
@@ -218,7 +299,7 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
   const int kvh = hg * p.G + w;
   const int ratio = p.ratio;
 
-  // ---- q' = fp16(FWHT(s*q)/sqrt(pd)) for this wave's `ratio` heads, in LDS
+  // ---- q' = FWHT(s*q)/sqrt(pd) for this wave's `ratio` heads, in LDS
   float* qs = smem + (size_t)w * ratio * PD;
   for (int i = lane; i < ratio * PD; i += 64) {
     const int r = i / PD, d = i - r * PD;
@@ -240,10 +321,9 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
     }
   }
   const float qsc = p.signs ? p.inv_sqrt_pd : 1.0f;
-  // B operand of the QK MFMA: column n = q head, 8 dims of quarter q4 per MFMA
   // q' is split into fp16 high and low parts (q' = hi + lo to ~22 bits), two
   // MFMAs per K block, so the scores keep fp32-level accuracy even for
-  // heavy-tailed keys; the dequantized K values are exact fp16 centroids.
+  // heavy-tailed keys.
   half8_t qhi[KD], qlo[KD];
   {
     constexpr int ord[8] = {1, 3, 5, 7, 0, 2, 4, 6};
@@ -260,106 +340,72 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
     }
   }
 
-  float4_t O[NO];
+  SoftmaxState<PD> st;
 #pragma unroll
-  for (int i = 0; i < NO; i++) O[i] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY;
-  float lsum = 0.f;
+  for (int i = 0; i < NO; i++) st.O[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.lsum = 0.f;
 
   const int L = p.seq_lens[b];
   const int c0 = s * p.cs;
   const int c1 = min(c0 + p.cs, L);
   if (c0 < c1) {
     const int tile0 = c0 / kTile, tile1 = (c1 - 1) / kTile;
-    Tile<PD> cur, nxt;
-    bool ok_cur, ok_nxt = false;
-    load_tile<PD>(p, b, kvh, tile0, lane, ok_cur, cur);
-    for (int tile = tile0; tile <= tile1; tile++) {
-      if (tile < tile1) load_tile<PD>(p, b, kvh, tile + 1, lane, ok_nxt, nxt);
+    const int tpp = p.block_size / kTile;  // tiles per page
+    const int64_t tokstride = (int64_t)p.Hkv * p.ebs;
+    const int ip = p.indptr[b];
+    LaneOffsets lo;
+    lo.k = (uint32_t)(n * tokstride + q4 * (PD / 8));
+#pragma unroll
+    for (int j = 0; j < 4; j++) lo.v[j] = (uint32_t)((4 * q4 + j) * tokstride + n * (PD / 32));
+    lo.nrm = (uint32_t)((4 * q4 + (lane & 3)) * tokstride + PD / 2);
+    const uint8_t* kslab = p.ks + (int64_t)kvh * p.ebs;
+    const uint8_t* vslab = p.vs + (int64_t)kvh * p.ebs;
+    const int tile_bytes = (int)(kTile * tokstride);
 
-      // ---- scores S[t = 4*q4 + r][h = n]
-      float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < KD; c++) {
-        uint32_t x[4];
-        dq8(cur.k[c], x);
-        const half8_t kv8 = as_half8(x[0], x[1], x[2], x[3]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qhi[c], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qlo[c], acc, 0, 0, 0);
-      }
-      const float nk[4] = {h2f(quad_bcast<0>(cur.nk)), h2f(quad_bcast<1>(cur.nk)),
-                           h2f(quad_bcast<2>(cur.nk)), h2f(quad_bcast<3>(cur.nk))};
-      const float nv[4] = {h2f(quad_bcast<0>(cur.nv)), h2f(quad_bcast<1>(cur.nv)),
-                           h2f(quad_bcast<2>(cur.nv)), h2f(quad_bcast<3>(cur.nv))};
-      const int tbase = tile * kTile + 4 * q4;
-      float sc[4];
-      bool valid[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int t = tbase + r;
-        valid[r] = ok_cur && t >= c0 && t < c1;
-        sc[r] = valid[r] ? acc[r] * nk[r] * p.qk_scale : -INFINITY;
-      }
-      float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float m_new = fmaxf(m, tmax);
-      const bool need = (n < ratio) && (m_new > m + 3.0f);
-      if (__any(need)) {
-        const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
-#pragma unroll
-        for (int i = 0; i < NO; i++) O[i] *= alpha;
-        lsum *= alpha;
-        m = m_new;
-      }
-      float pr[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        pr[r] = valid[r] ? __builtin_amdgcn_exp2f(sc[r] - m) : 0.0f;
-        lsum += pr[r];
-      }
-      // fp16 hi + lo parts of p * norm_v / (sqrt(pd) * kCbScale)
-      half4_t pvh, pvl;
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float x = valid[r] ? pr[r] * nv[r] * p.pv_scale : 0.0f;
-        const _Float16 hi = (_Float16)x;
-        pvh[r] = hi;
-        pvl[r] = (_Float16)(x - (float)hi);
-      }
+    // windows of 64 tiles: lane i holds the page id of tile w0 + i
+    for (int w0 = tile0; w0 <= tile1; w0 += 64) {
+      const int wend = min(w0 + 63, tile1);
+      int vpage = -1;
+      if (w0 + lane <= wend) vpage = p.indices[ip + (w0 + lane) / tpp];
 
-      // ---- O[h][dim slot] += V^T P^T
-      uint32_t e[VB];
-      if constexpr (PD == 64) {
-        const uint32_t p01 = cur.v[0][0] | (cur.v[1][0] << 16);
-        const uint32_t p23 = cur.v[2][0] | (cur.v[3][0] << 16);
-        e[0] = perm(p23, p01, 0x06040200u);
-        e[1] = perm(p23, p01, 0x07050301u);
-      } else if constexpr (PD == 128) {
-        transpose4(cur.v[0][0], cur.v[1][0], cur.v[2][0], cur.v[3][0], e);
-      } else {
-        transpose4(cur.v[0][0], cur.v[1][0], cur.v[2][0], cur.v[3][0], e);
-        transpose4(cur.v[0][1], cur.v[1][1], cur.v[2][1], cur.v[3][1], e + 4);
-      }
-#pragma unroll
-      for (int k = 0; k < VB; k++) {
-        uint32_t x[4];
-        dq8(e[k], x);
-        const half4_t lo4 = as_half4(x[0], x[1]), hi4 = as_half4(x[2], x[3]);
-        O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo4, pvh, O[2 * k + 1], 0, 0, 0);
-        O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo4, pvl, O[2 * k + 1], 0, 0, 0);
-        O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi4, pvh, O[2 * k], 0, 0, 0);
-        O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi4, pvl, O[2 * k], 0, 0, 0);
-      }
-      if (tile < tile1) {
-        cur = nxt;
-        ok_cur = ok_nxt;
+      // Issue tile t's loads into `t_`; tiles past the window fetch nothing.
+      auto issue = [&](int t, Tile<PD>& t_, bool& ok_) {
+        const int rel = t - w0;
+        int pg = __builtin_amdgcn_readlane(vpage, rel & 63);
+        ok_ = rel <= wend - w0 && pg >= 0 && pg < p.num_blocks;
+        const int64_t off =
+            ok_ ? ((int64_t)pg * p.block_size + (t % tpp) * kTile) * tokstride : 0;
+        const int nrec = ok_ ? tile_bytes : 0;
+        const __amdgpu_buffer_rsrc_t kr =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(kslab + off), (short)0, nrec, 0x00020000);
+        const __amdgpu_buffer_rsrc_t vr =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(vslab + off), (short)0, nrec, 0x00020000);
+        load_tile<PD>(kr, vr, lo, t_);
+      };
+
+      // three-deep register ring: tiles t+1 and t+2 are in flight while t runs
+      Tile<PD> b0, b1, b2;
+      bool ok0, ok1, ok2;
+      issue(w0, b0, ok0);
+      issue(w0 + 1, b1, ok1);
+      // Whole groups of three tiles: a tile past the window end is fetched as
+      // an empty buffer and fully masked, so the body has no early exits.
+      for (int t = w0; t <= wend; t += 3) {
+        issue(t + 2, b2, ok2);
+        attend_tile<PD>(b0, ok0, t, c0, c1, q4, n, ratio, qhi, qlo, p.qk_scale, p.pv_scale, st);
+        issue(t + 3, b0, ok0);
+        attend_tile<PD>(b1, ok1, t + 1, c0, c1, q4, n, ratio, qhi, qlo, p.qk_scale,
+                        p.pv_scale, st);
+        issue(t + 4, b1, ok1);
+        attend_tile<PD>(b2, ok2, t + 2, c0, c1, q4, n, ratio, qhi, qlo, p.qk_scale,
+                        p.pv_scale, st);
       }
     }
   }
 
   // ---- finish: O[i][r] = o[h = n][dim (4*q4 + r)*NO + i]
-  float lt = lsum + __shfl_xor(lsum, 16);
+  float lt = st.lsum + __shfl_xor(st.lsum, 16);
   lt = lt + __shfl_xor(lt, 32);
   if (n < ratio) {
     const float inv = lt > 0.f ? 1.0f / lt : 0.0f;
@@ -369,20 +415,16 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
     for (int r = 0; r < 4; r++) {
 #pragma unroll
       for (int i = 0; i < NO; i += 4) {
-        float4_t v = {O[i][r] * inv, O[i + 1][r] * inv, O[i + 2][r] * inv, O[i + 3][r] * inv};
+        float4_t v = {st.O[i][r] * inv, st.O[i + 1][r] * inv, st.O[i + 2][r] * inv,
+                      st.O[i + 3][r] * inv};
         *reinterpret_cast<float4_t*>(out + r * NO + i) = v;
       }
     }
     if (q4 == 0)
-      p.plse[row] = lt > 0.f ? (m + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
+      p.plse[row] = lt > 0.f ? (st.m + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
   }
 }
 
-// LSE merge of the splits of one (sequence, q head), inverse rotation, fp16
-// store.  256 threads: split weights are computed once into LDS, then
-// 256/(PD/4) split groups each sum a strided subset of the splits for one
-// float4 column, a tree in LDS adds the groups, and wave 0 runs the inverse
-// FWHT across its 64 lanes.
 template <int PD>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ po,
                                                       const float* __restrict__ plse, int S,
@@ -534,7 +576,7 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   p.signs = signs;
   p.po = partition_o;
   p.plse = partition_lse;
-  p.num_blocks = num_blocks;
+  p.num_blocks = num_blocks > 0x7fffffffLL ? 0x7fffffff : (int)num_blocks;
   p.B = batch;
   p.Hq = num_qo_heads;
   p.Hkv = num_kv_heads;
