@@ -188,26 +188,61 @@ __device__ __forceinline__ void transpose4(uint32_t d0, uint32_t d1, uint32_t d2
 }
 
 // Online-softmax state of one wave: O[i][r] = unnormalised o[h = n][dim
-// (4*q4 + r)*NO + i] in the rotated domain, m = running max (log2 units, per
-// column h), lsum = this lane's share of the denominator.
+// (4*q4 + r)*NO + i] in the rotated domain (times pv_scale^-1, see below),
+// m = running max of the scores (log2 units, per column h), lsum = this
+// lane's share of the denominator.  Probabilities are formed as
+// p' = exp2(s - mb), mb = m + Lpv with Lpv = -log2(pv_scale), i.e. p' = p *
+// pv_scale: the V norm then multiplies in without leaving the fp16 range;
+// o = pv_scale * O / lsum', and mb + log2(lsum') is the LSE (log2 units).
 template <int PD>
 struct SoftmaxState {
   static constexpr int NO = PD / 16;
   float4_t O[NO];
   float m;
+  float mb;
   float lsum;
 };
 
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// fp16 value held in the low / high half of a dword
+__device__ __forceinline__ float lo_half(uint32_t v) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu));
+}
+__device__ __forceinline__ float hi_half(uint32_t v) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+}
+
+// One 16-token tile of one kv head.  `full` (wave-uniform): every token of
+// the tile is valid (page valid and inside [c0, c1)), so no masking is needed.
 template <int PD>
-__device__ __forceinline__ void attend_tile(const Tile<PD>& cur, bool ok, int tile, int c0,
+__device__ __forceinline__ void attend_tile(bool full, const Tile<PD>& cur, bool ok, int tile, int c0,
                                             int c1, int q4, int n, int ratio,
-                                            const half8_t* qhi, const half8_t* qlo,
-                                            float qk_scale, float pv_scale,
+                                            const half8_t* qhi, const half8_t* qlo, float lpv,
                                             SoftmaxState<PD>& st) {
   constexpr int KD = PD / 32;
   constexpr int VB = PD / 32;
   constexpr int NO = PD / 16;
-  // ---- scores S[t = 4*q4 + r][h = n]
+  // ---- scores S[t = 4*q4 + r][h = n]; q' carries sm_scale*log2(e)/(sqrt(pd)*kCbScale)
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < KD; c++) {
@@ -217,22 +252,28 @@ __device__ __forceinline__ void attend_tile(const Tile<PD>& cur, bool ok, int ti
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qhi[c], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qlo[c], acc, 0, 0, 0);
   }
-  const float nk[4] = {h2f(quad_bcast<0>(cur.nk)), h2f(quad_bcast<1>(cur.nk)),
-                       h2f(quad_bcast<2>(cur.nk)), h2f(quad_bcast<3>(cur.nk))};
-  const float nv[4] = {h2f(quad_bcast<0>(cur.nv)), h2f(quad_bcast<1>(cur.nv)),
-                       h2f(quad_bcast<2>(cur.nv)), h2f(quad_bcast<3>(cur.nv))};
-  const int tbase = tile * kTile + 4 * q4;
+  // norms of tokens 4*q4 + r: K norm in the low half, V norm in the high half
+  const uint32_t nkv = cur.nk | (cur.nv << 16);
+  const uint32_t nr[4] = {quad_bcast<0>(nkv), quad_bcast<1>(nkv), quad_bcast<2>(nkv),
+                          quad_bcast<3>(nkv)};
   float sc[4];
   bool valid[4];
 #pragma unroll
   for (int r = 0; r < 4; r++) {
-    const int t = tbase + r;
-    valid[r] = ok && t >= c0 && t < c1;
-    sc[r] = valid[r] ? acc[r] * nk[r] * qk_scale : -INFINITY;
+    sc[r] = acc[r] * lo_half(nr[r]);
+    valid[r] = true;
+  }
+  if (!full) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int t = tile * kTile + 4 * q4 + r;
+      valid[r] = ok && t >= c0 && t < c1;
+      sc[r] = valid[r] ? sc[r] : -INFINITY;
+    }
   }
   float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+  tmax = xor16_max(tmax);
+  tmax = xor32_max(tmax);
   const float m_new = fmaxf(st.m, tmax);
   const bool need = (n < ratio) && (m_new > st.m + 3.0f);
   if (__any(need)) {
@@ -241,18 +282,23 @@ __device__ __forceinline__ void attend_tile(const Tile<PD>& cur, bool ok, int ti
     for (int i = 0; i < NO; i++) st.O[i] *= alpha;
     st.lsum *= alpha;
     st.m = m_new;
+    st.mb = m_new + lpv;
   }
   float pr[4];
 #pragma unroll
   for (int r = 0; r < 4; r++) {
-    pr[r] = valid[r] ? __builtin_amdgcn_exp2f(sc[r] - st.m) : 0.0f;
-    st.lsum += pr[r];
+    pr[r] = __builtin_amdgcn_exp2f(sc[r] - st.mb);
   }
-  // fp16 hi + lo parts of p * norm_v / (sqrt(pd) * kCbScale)
+  if (!full) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) pr[r] = valid[r] ? pr[r] : 0.0f;
+  }
+  st.lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+  // fp16 hi + lo parts of p' * norm_v
   half4_t pvh, pvl;
 #pragma unroll
   for (int r = 0; r < 4; r++) {
-    const float x = valid[r] ? pr[r] * nv[r] * pv_scale : 0.0f;
+    const float x = pr[r] * hi_half(nr[r]);
     const _Float16 hi = (_Float16)x;
     pvh[r] = hi;
     pvl[r] = (_Float16)(x - (float)hi);
@@ -283,7 +329,16 @@ __device__ __forceinline__ void attend_tile(const Tile<PD>& cur, bool ok, int ti
 }
 
 template <int PD>
-__global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
+__device__ __forceinline__ void attend(const Tile<PD>& cur, bool ok, int tile, int c0, int c1,
+                                       int q4, int n, int ratio, const half8_t* qhi,
+                                       const half8_t* qlo, float lpv, SoftmaxState<PD>& st) {
+  const bool full = ok && tile * kTile >= c0 && tile * kTile + kTile <= c1;
+  attend_tile<PD>(full, cur, ok, tile, c0, c1, q4, n, ratio, qhi, qlo, lpv, st);
+}
+
+template <int PD>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : 4)))
+void decode_partials_kernel(DecodeParams p) {
   constexpr int KD = PD / 32;
   constexpr int NO = PD / 16;  // PV MFMAs = dim slots per lane
   extern __shared__ float smem[];
@@ -320,7 +375,7 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
       __syncthreads();
     }
   }
-  const float qsc = p.signs ? p.inv_sqrt_pd : 1.0f;
+  const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
   // q' is split into fp16 high and low parts (q' = hi + lo to ~22 bits), two
   // MFMAs per K block, so the scores keep fp32-level accuracy even for
   // heavy-tailed keys.
@@ -344,7 +399,9 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
 #pragma unroll
   for (int i = 0; i < NO; i++) st.O[i] = float4_t{0.f, 0.f, 0.f, 0.f};
   st.m = -INFINITY;
+  st.mb = -INFINITY;
   st.lsum = 0.f;
+  const float lpv = -__log2f(p.pv_scale);
 
   const int L = p.seq_lens[b];
   const int c0 = s * p.cs;
@@ -393,22 +450,20 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
       // an empty buffer and fully masked, so the body has no early exits.
       for (int t = w0; t <= wend; t += 3) {
         issue(t + 2, b2, ok2);
-        attend_tile<PD>(b0, ok0, t, c0, c1, q4, n, ratio, qhi, qlo, p.qk_scale, p.pv_scale, st);
+        attend<PD>(b0, ok0, t, c0, c1, q4, n, ratio, qhi, qlo, lpv, st);
         issue(t + 3, b0, ok0);
-        attend_tile<PD>(b1, ok1, t + 1, c0, c1, q4, n, ratio, qhi, qlo, p.qk_scale,
-                        p.pv_scale, st);
+        attend<PD>(b1, ok1, t + 1, c0, c1, q4, n, ratio, qhi, qlo, lpv, st);
         issue(t + 4, b1, ok1);
-        attend_tile<PD>(b2, ok2, t + 2, c0, c1, q4, n, ratio, qhi, qlo, p.qk_scale,
-                        p.pv_scale, st);
+        attend<PD>(b2, ok2, t + 2, c0, c1, q4, n, ratio, qhi, qlo, lpv, st);
       }
     }
   }
 
   // ---- finish: O[i][r] = o[h = n][dim (4*q4 + r)*NO + i]
-  float lt = st.lsum + __shfl_xor(st.lsum, 16);
-  lt = lt + __shfl_xor(lt, 32);
+  const float lt = xor32_sum(xor16_sum(st.lsum));
   if (n < ratio) {
-    const float inv = lt > 0.f ? 1.0f / lt : 0.0f;
+    // o = pv_scale * O / lsum' (p' = p * pv_scale in both O and lsum')
+    const float inv = lt > 0.f ? p.pv_scale / lt : 0.0f;
     const int64_t row = ((int64_t)b * p.S + s) * p.Hq + kvh * ratio + n;
     float* out = p.po + row * PD + q4 * (PD / 4);
 #pragma unroll
@@ -420,8 +475,9 @@ __global__ __launch_bounds__(512) void decode_partials_kernel(DecodeParams p) {
         *reinterpret_cast<float4_t*>(out + r * NO + i) = v;
       }
     }
+    // natural-log LSE: (m + log2(sum p)) * ln 2 = (mb + log2(lsum')) * ln 2
     if (q4 == 0)
-      p.plse[row] = lt > 0.f ? (st.m + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
+      p.plse[row] = lt > 0.f ? (st.mb + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
   }
 }
 
