@@ -33,6 +33,7 @@
 //  * Online softmax in the exp2 domain with a lazy rescale (the running max
 //    only moves when a tile exceeds it by more than 2^3), bounding p <= 8.
 #include <math.h>
+#include <stdlib.h>
 
 #include "tq_common.h"
 
@@ -100,9 +101,6 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, R * 0x55, 0xf, 0xf, false);
 }
 
-__device__ __forceinline__ float h2f(uint32_t bits) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
-}
 
 struct DecodeParams {
   const _Float16* q;
@@ -122,60 +120,6 @@ struct DecodeParams {
   float pv_scale;     // 1/(sqrt(pd) * kCbScale)
 };
 
-template <int PD>
-struct Tile {
-  static constexpr int KD = PD / 32;               // K dwords per lane = QK MFMA pairs
-  static constexpr int VB = PD / 32;               // V bytes per lane per token
-  static constexpr int VW = VB >= 4 ? VB / 4 : 1;  // V dwords per lane per token
-  uint32_t k[KD];
-  uint32_t v[4][VW];
-  uint32_t nk, nv;
-};
-
-// Per-lane byte offsets inside one 16-token tile of one kv head, relative to
-// the tile's first entry (constant over the whole loop).
-struct LaneOffsets {
-  uint32_t k;     // K codes: token n, bytes [q4*PD/8, (q4+1)*PD/8)
-  uint32_t v[4];  // V codes: token 4*q4 + j, bytes [n*PD/32, (n+1)*PD/32)
-  uint32_t nrm;   // norm of token 4*q4 + (lane & 3)
-};
-
-// Issue the loads of one tile through buffer resources whose base is the
-// tile's first entry of this kv head (wave-uniform) and whose size is the
-// tile's extent, or 0 for a tile that is not fetched: out-of-range buffer
-// loads return zeros without touching memory, so every tile issues the same
-// instruction sequence and the load counters stay in order.
-template <int PD>
-__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
-                                          const LaneOffsets& o, Tile<PD>& t) {
-  if constexpr (PD == 64) {
-    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(kr, o.k, 0, 0);
-    t.k[0] = w[0]; t.k[1] = w[1];
-  } else if constexpr (PD == 128) {
-    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(kr, o.k, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 4; i++) t.k[i] = w[i];
-  } else {
-    const u32x4 w0 = __builtin_amdgcn_raw_buffer_load_b128(kr, o.k, 0, 0);
-    const u32x4 w1 = __builtin_amdgcn_raw_buffer_load_b128(kr, o.k + 16, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 4; i++) { t.k[i] = w0[i]; t.k[4 + i] = w1[i]; }
-  }
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    if constexpr (PD == 64) {
-      t.v[j][0] = __builtin_amdgcn_raw_buffer_load_b16(vr, o.v[j], 0, 0);
-    } else if constexpr (PD == 128) {
-      t.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(vr, o.v[j], 0, 0);
-    } else {
-      const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(vr, o.v[j], 0, 0);
-      t.v[j][0] = w[0]; t.v[j][1] = w[1];
-    }
-  }
-  t.nk = __builtin_amdgcn_raw_buffer_load_b16(kr, o.nrm, 0, 0);
-  t.nv = __builtin_amdgcn_raw_buffer_load_b16(vr, o.nrm, 0, 0);
-}
-
 // 4x4 byte transpose: E_k byte j = byte k of D_j
 __device__ __forceinline__ void transpose4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
                                            uint32_t* e) {
@@ -186,22 +130,6 @@ __device__ __forceinline__ void transpose4(uint32_t d0, uint32_t d1, uint32_t d2
   e[2] = perm(b23, b01, 0x05040100u);
   e[3] = perm(b23, b01, 0x07060302u);
 }
-
-// Online-softmax state of one wave: O[i][r] = unnormalised o[h = n][dim
-// (4*q4 + r)*NO + i] in the rotated domain (times pv_scale^-1, see below),
-// m = running max of the scores (log2 units, per column h), lsum = this
-// lane's share of the denominator.  Probabilities are formed as
-// p' = exp2(s - mb), mb = m + Lpv with Lpv = -log2(pv_scale), i.e. p' = p *
-// pv_scale: the V norm then multiplies in without leaving the fp16 range;
-// o = pv_scale * O / lsum', and mb + log2(lsum') is the LSE (log2 units).
-template <int PD>
-struct SoftmaxState {
-  static constexpr int NO = PD / 16;
-  float4_t O[NO];
-  float m;
-  float mb;
-  float lsum;
-};
 
 __device__ __forceinline__ float xor16_max(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
@@ -223,7 +151,10 @@ __device__ __forceinline__ float xor32_sum(float x) {
                                                   false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-
+// rotate by 8 lanes inside each 16-lane row (DPP row_ror:8)
+__device__ __forceinline__ float ror8(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
+}
 // fp16 value held in the low / high half of a dword
 __device__ __forceinline__ float lo_half(uint32_t v) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu));
@@ -232,89 +163,69 @@ __device__ __forceinline__ float hi_half(uint32_t v) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
 }
 
-// One 16-token tile of one kv head.  `full` (wave-uniform): every token of
-// the tile is valid (page valid and inside [c0, c1)), so no masking is needed.
+// Static LDS geometry of the decode kernel.  A step is two 16-token tiles;
+// one staged step holds, for the workgroup's G heads, the K slab then the V
+// slab, each [32 token rows][G*ebs bytes].  ROW = the largest G*ebs a
+// workgroup may take for this head size.
 template <int PD>
-__device__ __forceinline__ void attend_tile(bool full, const Tile<PD>& cur, bool ok, int tile, int c0,
-                                            int c1, int q4, int n, int ratio,
-                                            const half8_t* qhi, const half8_t* qlo, float lpv,
-                                            SoftmaxState<PD>& st) {
+struct DecodeGeom {
+  static constexpr int KD = PD / 32;  // K dwords per lane per tile = QK MFMA pairs
+  static constexpr int VB = PD / 32;  // V bytes per lane per token
+  static constexpr int NO = PD / 16;  // PV MFMAs = output dim slots per lane
+  static constexpr int EBS = PD == 64 ? 48 : (PD == 128 ? 80 : 144);  // entry bytes
+  static constexpr int MAXG = PD == 256 ? 4 : 8;          // kv heads (waves) per workgroup
+  static constexpr int WAVE_STEP = 2 * 2 * kTile * EBS;  // one wave's staged step (K+V, 2 tiles)
+};
+
+// Online-softmax state of one wave.  O[i][r] = unnormalised o[h = l%16][dim
+// (4*q4 + r)*NO + i] in the rotated domain.  m = running max of the scores
+// (log2 units, replicated over the lanes of a head), lsum = this lane's
+// share of the denominator.  Probabilities are formed as p' = exp2(s - mb),
+// mb = m + Lpv with Lpv = -log2(pv_scale), i.e. p' = p * pv_scale: the V
+// norm then multiplies in without leaving the fp16 range; o = pv_scale * O /
+// lsum', and mb + log2(lsum') is the LSE (log2 units).
+template <int PD>
+struct SoftmaxState {
+  float4_t O[DecodeGeom<PD>::NO];
+  float m, mb, lsum;
+};
+
+// Scores of one tile, S[t = 4*q4 + r][h = l%16]: dequantize the K codes
+// this lane holds (token l%16, dims of quarter q4) and run the QK MFMAs
+// against q' (fp16 hi + lo parts, pre-scaled to log2 units).
+template <int PD>
+__device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_t* qhi,
+                                                const half8_t* qlo) {
   constexpr int KD = PD / 32;
-  constexpr int VB = PD / 32;
-  constexpr int NO = PD / 16;
-  // ---- scores S[t = 4*q4 + r][h = n]; q' carries sm_scale*log2(e)/(sqrt(pd)*kCbScale)
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < KD; c++) {
     uint32_t x[4];
-    dq8(cur.k[c], x);
+    dq8(kw[c], x);
     const half8_t kv8 = as_half8(x[0], x[1], x[2], x[3]);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qhi[c], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qlo[c], acc, 0, 0, 0);
   }
-  // norms of tokens 4*q4 + r: K norm in the low half, V norm in the high half
-  const uint32_t nkv = cur.nk | (cur.nv << 16);
-  const uint32_t nr[4] = {quad_bcast<0>(nkv), quad_bcast<1>(nkv), quad_bcast<2>(nkv),
-                          quad_bcast<3>(nkv)};
-  float sc[4];
-  bool valid[4];
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    sc[r] = acc[r] * lo_half(nr[r]);
-    valid[r] = true;
-  }
-  if (!full) {
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int t = tile * kTile + 4 * q4 + r;
-      valid[r] = ok && t >= c0 && t < c1;
-      sc[r] = valid[r] ? sc[r] : -INFINITY;
-    }
-  }
-  float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-  tmax = xor16_max(tmax);
-  tmax = xor32_max(tmax);
-  const float m_new = fmaxf(st.m, tmax);
-  const bool need = (n < ratio) && (m_new > st.m + 3.0f);
-  if (__any(need)) {
-    const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(st.m - m_new);
-#pragma unroll
-    for (int i = 0; i < NO; i++) st.O[i] *= alpha;
-    st.lsum *= alpha;
-    st.m = m_new;
-    st.mb = m_new + lpv;
-  }
-  float pr[4];
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    pr[r] = __builtin_amdgcn_exp2f(sc[r] - st.mb);
-  }
-  if (!full) {
-#pragma unroll
-    for (int r = 0; r < 4; r++) pr[r] = valid[r] ? pr[r] : 0.0f;
-  }
-  st.lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-  // fp16 hi + lo parts of p' * norm_v
-  half4_t pvh, pvl;
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const float x = pr[r] * hi_half(nr[r]);
-    const _Float16 hi = (_Float16)x;
-    pvh[r] = hi;
-    pvl[r] = (_Float16)(x - (float)hi);
-  }
-  // ---- O[h][dim slot] += V^T P^T
+  return acc;
+}
+
+// O[h][dim slot] += V^T P^T for one tile: v[j] = this lane's V code bytes
+// [n*VB, (n+1)*VB) of token 4*q4 + j.
+template <int PD>
+__device__ __forceinline__ void tile_pv(const uint32_t (*v)[(PD / 32) >= 4 ? PD / 128 : 1],
+                                        half4_t pvh, half4_t pvl, SoftmaxState<PD>& st) {
+  constexpr int VB = PD / 32;
   uint32_t e[VB];
   if constexpr (PD == 64) {
-    const uint32_t p01 = cur.v[0][0] | (cur.v[1][0] << 16);
-    const uint32_t p23 = cur.v[2][0] | (cur.v[3][0] << 16);
+    const uint32_t p01 = v[0][0] | (v[1][0] << 16);
+    const uint32_t p23 = v[2][0] | (v[3][0] << 16);
     e[0] = perm(p23, p01, 0x06040200u);
     e[1] = perm(p23, p01, 0x07050301u);
   } else if constexpr (PD == 128) {
-    transpose4(cur.v[0][0], cur.v[1][0], cur.v[2][0], cur.v[3][0], e);
+    transpose4(v[0][0], v[1][0], v[2][0], v[3][0], e);
   } else {
-    transpose4(cur.v[0][0], cur.v[1][0], cur.v[2][0], cur.v[3][0], e);
-    transpose4(cur.v[0][1], cur.v[1][1], cur.v[2][1], cur.v[3][1], e + 4);
+    transpose4(v[0][0], v[1][0], v[2][0], v[3][0], e);
+    transpose4(v[0][1], v[1][1], v[2][1], v[3][1], e + 4);
   }
 #pragma unroll
   for (int k = 0; k < VB; k++) {
@@ -328,20 +239,264 @@ __device__ __forceinline__ void attend_tile(bool full, const Tile<PD>& cur, bool
   }
 }
 
+// This wave's share of one staged step, read from LDS into registers.
 template <int PD>
-__device__ __forceinline__ void attend(const Tile<PD>& cur, bool ok, int tile, int c0, int c1,
-                                       int q4, int n, int ratio, const half8_t* qhi,
-                                       const half8_t* qlo, float lpv, SoftmaxState<PD>& st) {
-  const bool full = ok && tile * kTile >= c0 && tile * kTile + kTile <= c1;
-  attend_tile<PD>(full, cur, ok, tile, c0, c1, q4, n, ratio, qhi, qlo, lpv, st);
+struct StepData {
+  static constexpr int KD = PD / 32;
+  static constexpr int VW = (PD / 32) >= 4 ? PD / 128 : 1;
+  uint32_t k[2][KD];     // K codes of tiles 0 and 1
+  uint32_t v[2][4][VW];  // V codes of tiles 0 and 1, tokens 4*q4 + j
+  uint32_t nkv[2];       // norms (K low, V high) of the packed tokens, per group
+};
+
+template <int PD, int PACK>
+__device__ __forceinline__ void read_step(const uint8_t* buf, int slab, int tilebytes, int row,
+                                          uint32_t koff, uint32_t voff, uint32_t noff,
+                                          StepData<PD>& d) {
+#pragma unroll
+  for (int T = 0; T < 2; T++) {
+    const uint8_t* kp = buf + T * tilebytes + koff;
+    if constexpr (PD == 64) {
+      const u32x2 w = *reinterpret_cast<const u32x2*>(kp);
+      d.k[T][0] = w[0]; d.k[T][1] = w[1];
+    } else if constexpr (PD == 128) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(kp);
+#pragma unroll
+      for (int i = 0; i < 4; i++) d.k[T][i] = w[i];
+    } else {
+      const u32x4 w0 = *reinterpret_cast<const u32x4*>(kp);
+      const u32x4 w1 = *reinterpret_cast<const u32x4*>(kp + 16);
+#pragma unroll
+      for (int i = 0; i < 4; i++) { d.k[T][i] = w0[i]; d.k[T][4 + i] = w1[i]; }
+    }
+    const uint8_t* vp = buf + slab + T * tilebytes + voff;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if constexpr (PD == 64) {
+        d.v[T][j][0] = *reinterpret_cast<const uint16_t*>(vp + j * row);
+      } else if constexpr (PD == 128) {
+        d.v[T][j][0] = *reinterpret_cast<const uint32_t*>(vp + j * row);
+      } else {
+        const u32x2 w = *reinterpret_cast<const u32x2*>(vp + j * row);
+        d.v[T][j][0] = w[0]; d.v[T][j][1] = w[1];
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < 2 / PACK; g++) {
+    const uint32_t gofs = PACK == 2 ? 0u : (uint32_t)(g * tilebytes);
+    const uint32_t nk = *reinterpret_cast<const uint16_t*>(buf + noff + gofs);
+    const uint32_t nv = *reinterpret_cast<const uint16_t*>(buf + slab + noff + gofs);
+    d.nkv[g] = nk | (nv << 16);
+  }
 }
 
-template <int PD>
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
+// vmcnt[5:4] in [15:14]; expcnt and lgkmcnt left at their maximum).
+__host__ __device__ constexpr int vmcnt_imm(int n) {
+  return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14);
+}
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)ptr;
+}
+
+// read_step for the per-wave slot layout ([K t0][K t1][V t0][V t1], entry
+// stride EBS), as inline assembly ending in lgkmcnt(0): the compiler does
+// not see these LDS reads, so it adds no conservative wait for the copies in
+// flight; the caller waits for exactly the copy it reads (vmcnt).
+template <int PD, int PACK>
+__device__ __forceinline__ void read_step_asm(const uint8_t* wslot, uint32_t koff,
+                                              uint32_t voff, uint32_t noff, StepData<PD>& d) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the kernel stubs
+  const uint32_t base = lds_addr(wslot);
+  const uint32_t ka = base + koff;
+  if constexpr (PD == 128) {  // EBS 80, tile 1280 B, V slab at 2560
+    const uint32_t va = base + 2560 + voff;
+    u32x4 k0, k1;
+    asm volatile(
+        "ds_read_b128 %0, %10\n\t"
+        "ds_read_b128 %1, %10 offset:1280\n\t"
+        "ds_read_b32 %2, %11\n\t"
+        "ds_read_b32 %3, %11 offset:80\n\t"
+        "ds_read_b32 %4, %11 offset:160\n\t"
+        "ds_read_b32 %5, %11 offset:240\n\t"
+        "ds_read_b32 %6, %11 offset:1280\n\t"
+        "ds_read_b32 %7, %11 offset:1360\n\t"
+        "ds_read_b32 %8, %11 offset:1440\n\t"
+        "ds_read_b32 %9, %11 offset:1520\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(k0), "=&v"(k1), "=&v"(d.v[0][0][0]), "=&v"(d.v[0][1][0]), "=&v"(d.v[0][2][0]),
+          "=&v"(d.v[0][3][0]), "=&v"(d.v[1][0][0]), "=&v"(d.v[1][1][0]), "=&v"(d.v[1][2][0]),
+          "=&v"(d.v[1][3][0])
+        : "v"(ka), "v"(va)
+        : "memory");
+#pragma unroll
+    for (int i = 0; i < 4; i++) { d.k[0][i] = k0[i]; d.k[1][i] = k1[i]; }
+  } else if constexpr (PD == 64) {  // EBS 48, tile 768 B, V slab at 1536
+    const uint32_t va = base + 1536 + voff;
+    u32x2 k0, k1;
+    asm volatile(
+        "ds_read_b64 %0, %10\n\t"
+        "ds_read_b64 %1, %10 offset:768\n\t"
+        "ds_read_u16 %2, %11\n\t"
+        "ds_read_u16 %3, %11 offset:48\n\t"
+        "ds_read_u16 %4, %11 offset:96\n\t"
+        "ds_read_u16 %5, %11 offset:144\n\t"
+        "ds_read_u16 %6, %11 offset:768\n\t"
+        "ds_read_u16 %7, %11 offset:816\n\t"
+        "ds_read_u16 %8, %11 offset:864\n\t"
+        "ds_read_u16 %9, %11 offset:912\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(k0), "=&v"(k1), "=&v"(d.v[0][0][0]), "=&v"(d.v[0][1][0]), "=&v"(d.v[0][2][0]),
+          "=&v"(d.v[0][3][0]), "=&v"(d.v[1][0][0]), "=&v"(d.v[1][1][0]), "=&v"(d.v[1][2][0]),
+          "=&v"(d.v[1][3][0])
+        : "v"(ka), "v"(va)
+        : "memory");
+    d.k[0][0] = k0[0]; d.k[0][1] = k0[1]; d.k[1][0] = k1[0]; d.k[1][1] = k1[1];
+  } else {  // PD 256: EBS 144, tile 2304 B, V slab at 4608
+    const uint32_t va = base + 4608 + voff;
+    u32x4 k0a, k0b, k1a, k1b;
+    u32x2 v0, v1, v2, v3, v4, v5, v6, v7;
+    asm volatile(
+        "ds_read_b128 %0, %12\n\t"
+        "ds_read_b128 %1, %12 offset:16\n\t"
+        "ds_read_b128 %2, %12 offset:2304\n\t"
+        "ds_read_b128 %3, %12 offset:2320\n\t"
+        "ds_read_b64 %4, %13\n\t"
+        "ds_read_b64 %5, %13 offset:144\n\t"
+        "ds_read_b64 %6, %13 offset:288\n\t"
+        "ds_read_b64 %7, %13 offset:432\n\t"
+        "ds_read_b64 %8, %13 offset:2304\n\t"
+        "ds_read_b64 %9, %13 offset:2448\n\t"
+        "ds_read_b64 %10, %13 offset:2592\n\t"
+        "ds_read_b64 %11, %13 offset:2736\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(k0a), "=&v"(k0b), "=&v"(k1a), "=&v"(k1b), "=&v"(v0), "=&v"(v1), "=&v"(v2),
+          "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6), "=&v"(v7)
+        : "v"(ka), "v"(va)
+        : "memory");
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      d.k[0][i] = k0a[i]; d.k[0][4 + i] = k0b[i]; d.k[1][i] = k1a[i]; d.k[1][4 + i] = k1b[i];
+    }
+    const u32x2 vv[8] = {v0, v1, v2, v3, v4, v5, v6, v7};
+#pragma unroll
+    for (int T = 0; T < 2; T++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) { d.v[T][j][0] = vv[4 * T + j][0]; d.v[T][j][1] = vv[4 * T + j][1]; }
+  }
+  // norms (K, then V one slab further); PACK 1 needs both tiles
+  constexpr int SLAB = 2 * kTile * (PD == 64 ? 48 : (PD == 128 ? 80 : 144));
+  constexpr int TBN = SLAB / 2;
+  const uint32_t na = base + noff;
+  if constexpr (PACK == 2) {
+    uint32_t nk, nv;
+    asm volatile(
+        "ds_read_u16 %0, %2\n\t"
+        "ds_read_u16 %1, %2 offset:%3\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(nk), "=&v"(nv)
+        : "v"(na), "i"(SLAB)
+        : "memory");
+    d.nkv[0] = nk | (nv << 16);
+  } else {
+    uint32_t nk0, nv0, nk1, nv1;
+    asm volatile(
+        "ds_read_u16 %0, %4\n\t"
+        "ds_read_u16 %1, %4 offset:%5\n\t"
+        "ds_read_u16 %2, %4 offset:%6\n\t"
+        "ds_read_u16 %3, %4 offset:%7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(nk0), "=&v"(nv0), "=&v"(nk1), "=&v"(nv1)
+        : "v"(na), "i"(SLAB), "i"(TBN), "i"(SLAB + TBN)
+        : "memory");
+    d.nkv[0] = nk0 | (nv0 << 16);
+    d.nkv[1] = nk1 | (nv1 << 16);
+  }
+#endif
+}
+
+// Online softmax over PACK tiles whose scores sit packed in one float4
+// (slot width 16/PACK lanes per 16-lane row: lane l holds tile (l%16) /
+// (16/PACK), head l % (16/PACK), tokens 4*q4 + r).  nkv: quad-broadcast
+// norms (K low half, V high half) of those tokens.  valid: token masks,
+// `full` when all are valid.  Returns the fp16 hi/lo probabilities * V norm.
+template <int PD, int PACK>
+__device__ __forceinline__ void softmax_step(float4_t acc, const uint32_t* nkv, bool full,
+                                             const bool* valid, int head, int ratio, float lpv,
+                                             SoftmaxState<PD>& st, half4_t& pvh, half4_t& pvl) {
+  constexpr int NO = PD / 16;
+  float sc[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) sc[r] = acc[r] * lo_half(nkv[r]);
+  if (!full) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) sc[r] = valid[r] ? sc[r] : -INFINITY;
+  }
+  float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+  if constexpr (PACK == 2) tmax = fmaxf(tmax, ror8(tmax));
+  tmax = xor16_max(tmax);
+  tmax = xor32_max(tmax);
+  const float m_new = fmaxf(st.m, tmax);
+  const bool need = (head < ratio) && (m_new > st.m + 3.0f);
+  if (__any(need)) {
+    const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(st.m - m_new);
+#pragma unroll
+    for (int i = 0; i < NO; i++) st.O[i] *= alpha;
+    st.lsum *= alpha;
+    st.m = m_new;
+    st.mb = m_new + lpv;
+  }
+  float pr[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) pr[r] = __builtin_amdgcn_exp2f(sc[r] - st.mb);
+  if (!full) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) pr[r] = valid[r] ? pr[r] : 0.0f;
+  }
+  st.lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    float x = pr[r] * hi_half(nkv[r]);
+    if (!full) x = valid[r] ? x : 0.0f;  // masked entries may hold any bits
+    const _Float16 hi = (_Float16)x;
+    pvh[r] = hi;
+    pvl[r] = (_Float16)(x - (float)hi);
+  }
+}
+
+// Bring tile 1's packed probabilities (lanes 8..15 of each row) to lanes
+// 0..7 (DPP row_shl:8), the B-operand position of the PV MFMA.
+__device__ __forceinline__ half4_t shl8(half4_t v) {
+  u32x2 u = __builtin_bit_cast(u32x2, v);
+  u[0] = (uint32_t)__builtin_amdgcn_mov_dpp((int)u[0], 0x108, 0xf, 0xf, false);
+  u[1] = (uint32_t)__builtin_amdgcn_mov_dpp((int)u[1], 0x108, 0xf, 0xf, false);
+  return __builtin_bit_cast(half4_t, u);
+}
+
+// Split-KV partials.  Workgroup = (sequence b, split s, group hg of G kv
+// heads), one wave per kv head.  Each wave streams its own head's cache
+// entries of each step (two 16-token tiles, K and V) into its own region of
+// NSLOT LDS slots with direct-to-LDS 16-byte loads, NSLOT - 1 steps ahead of
+// the step it computes.  Waves never wait on each other after the q setup:
+// the slots are distinct LDS arrays, so the compiler ties every LDS read to
+// the one copy it depends on and leaves the later copies in flight.
+template <int PD, int PACK, int NSLOT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : 4)))
 void decode_partials_kernel(DecodeParams p) {
-  constexpr int KD = PD / 32;
-  constexpr int NO = PD / 16;  // PV MFMAs = dim slots per lane
-  extern __shared__ float smem[];
+  using Geo = DecodeGeom<PD>;
+  constexpr int KD = Geo::KD;
+  constexpr int NO = Geo::NO;
+  constexpr int EBS = Geo::EBS;
+  constexpr int WB = Geo::WAVE_STEP;  // bytes of one staged step of one wave
+  constexpr int MG = Geo::MAXG;
+  __shared__ __attribute__((aligned(16))) uint8_t slot0[MG * WB];
+  __shared__ __attribute__((aligned(16))) uint8_t slot1[MG * WB];
+  __shared__ __attribute__((aligned(16))) uint8_t slot2[NSLOT > 2 ? MG * WB : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t slot3[NSLOT > 3 ? MG * WB : 16];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -351,36 +506,40 @@ void decode_partials_kernel(DecodeParams p) {
   bid /= p.HG;
   const int s = bid % p.S;
   const int b = bid / p.S;
-  const int kvh = hg * p.G + w;
+  const int G = p.G;
+  const int kvh = hg * G + w;
   const int ratio = p.ratio;
 
-  // ---- q' = FWHT(s*q)/sqrt(pd) for this wave's `ratio` heads, in LDS
-  float* qs = smem + (size_t)w * ratio * PD;
-  for (int i = lane; i < ratio * PD; i += 64) {
-    const int r = i / PD, d = i - r * PD;
-    float x = (float)p.q[b * p.q_sb + (int64_t)(kvh * ratio + r) * p.q_sh + d];
-    if (p.signs) x = x * p.signs[d];
-    qs[i] = x;
-  }
-  __syncthreads();
-  if (p.signs) {
-    for (int h = 1; h < PD; h <<= 1) {
-      for (int i = lane; i < ratio * PD / 2; i += 64) {
-        const int r = i / (PD / 2), j = i - r * (PD / 2);
-        const int lo = r * PD + (j / h) * 2 * h + (j % h);
-        const float a = qs[lo], c = qs[lo + h];
-        qs[lo] = a + c;
-        qs[lo + h] = a - c;
+  // ---- q' = FWHT(s*q)/sqrt(pd) for this wave's `ratio` heads (scratch in slot0)
+  {
+    float* qs = reinterpret_cast<float*>(slot0) + (size_t)w * ratio * PD;
+    for (int i = lane; i < ratio * PD; i += 64) {
+      const int r = i / PD, d = i - r * PD;
+      float x = (float)p.q[b * p.q_sb + (int64_t)(kvh * ratio + r) * p.q_sh + d];
+      if (p.signs) x = x * p.signs[d];
+      qs[i] = x;
+    }
+    __syncthreads();
+    if (p.signs) {
+      for (int h = 1; h < PD; h <<= 1) {
+        for (int i = lane; i < ratio * PD / 2; i += 64) {
+          const int r = i / (PD / 2), j = i - r * (PD / 2);
+          const int lo = r * PD + (j / h) * 2 * h + (j % h);
+          const float a = qs[lo], c = qs[lo + h];
+          qs[lo] = a + c;
+          qs[lo + h] = a - c;
+        }
+        __syncthreads();
       }
-      __syncthreads();
     }
   }
-  const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
-  // q' is split into fp16 high and low parts (q' = hi + lo to ~22 bits), two
-  // MFMAs per K block, so the scores keep fp32-level accuracy even for
-  // heavy-tailed keys.
+  // q' (pre-scaled to log2 units) split into fp16 high and low parts
+  // (q' = hi + lo to ~22 bits), two MFMAs per K block, so the scores keep
+  // fp32-level accuracy even for heavy-tailed keys.
   half8_t qhi[KD], qlo[KD];
   {
+    const float* qs = reinterpret_cast<const float*>(slot0) + (size_t)w * ratio * PD;
+    const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
     constexpr int ord[8] = {1, 3, 5, 7, 0, 2, 4, 6};
 #pragma unroll
     for (int c = 0; c < KD; c++) {
@@ -394,6 +553,7 @@ void decode_partials_kernel(DecodeParams p) {
       }
     }
   }
+  __syncthreads();  // the q scratch is reused by the slots below
 
   SoftmaxState<PD> st;
 #pragma unroll
@@ -406,66 +566,186 @@ void decode_partials_kernel(DecodeParams p) {
   const int L = p.seq_lens[b];
   const int c0 = s * p.cs;
   const int c1 = min(c0 + p.cs, L);
-  if (c0 < c1) {
-    const int tile0 = c0 / kTile, tile1 = (c1 - 1) / kTile;
+  if (c0 < c1) {  // uniform over the workgroup
+    constexpr int STEP = 2 * kTile;
+    constexpr int CH = EBS / 16;                   // 16-byte chunks per entry
+    constexpr int IPR = (kTile * CH + 63) / 64;    // copy instructions per region
+    constexpr int TB = kTile * EBS;                // one tile of one slab (LDS)
+    const int step0 = c0 / STEP, step1 = (c1 - 1) / STEP;
     const int tpp = p.block_size / kTile;  // tiles per page
-    const int64_t tokstride = (int64_t)p.Hkv * p.ebs;
+    const int64_t tokstride = (int64_t)p.Hkv * EBS;
     const int ip = p.indptr[b];
-    LaneOffsets lo;
-    lo.k = (uint32_t)(n * tokstride + q4 * (PD / 8));
+    const uint8_t* kslab = p.ks + (int64_t)kvh * EBS;
+    const uint8_t* vslab = p.vs + (int64_t)kvh * EBS;
+    const int tile_last = (c1 - 1) / kTile;
+    const int rec = (int)((kTile - 1) * tokstride + EBS);
+
+    // page ids: lane i holds the page of tile wtile + i; a window covers 32
+    // steps (64 tiles), reloaded between windows with the copies drained
+    int vpage = -1;
+    int wtile = 2 * step0;
+    auto page_of = [&](int t) -> int {  // wave-uniform; -1 = not present
+      const int pg = __builtin_amdgcn_readlane(vpage, (t - wtile) & 63);
+      return (t <= tile_last && pg >= 0 && pg < p.num_blocks) ? pg : -1;
+    };
+
+    // copy offsets: instruction i of a region moves chunks 64*i + lane
+    // (token c / CH, chunk c % CH) of the 16 entries of one tile
+    uint32_t goff[IPR];
+    bool gact[IPR];
 #pragma unroll
-    for (int j = 0; j < 4; j++) lo.v[j] = (uint32_t)((4 * q4 + j) * tokstride + n * (PD / 32));
-    lo.nrm = (uint32_t)((4 * q4 + (lane & 3)) * tokstride + PD / 2);
-    const uint8_t* kslab = p.ks + (int64_t)kvh * p.ebs;
-    const uint8_t* vslab = p.vs + (int64_t)kvh * p.ebs;
-    const int tile_bytes = (int)(kTile * tokstride);
-
-    // windows of 64 tiles: lane i holds the page id of tile w0 + i
-    for (int w0 = tile0; w0 <= tile1; w0 += 64) {
-      const int wend = min(w0 + 63, tile1);
-      int vpage = -1;
-      if (w0 + lane <= wend) vpage = p.indices[ip + (w0 + lane) / tpp];
-
-      // Issue tile t's loads into `t_`; tiles past the window fetch nothing.
-      auto issue = [&](int t, Tile<PD>& t_, bool& ok_) {
-        const int rel = t - w0;
-        int pg = __builtin_amdgcn_readlane(vpage, rel & 63);
-        ok_ = rel <= wend - w0 && pg >= 0 && pg < p.num_blocks;
-        const int64_t off =
-            ok_ ? ((int64_t)pg * p.block_size + (t % tpp) * kTile) * tokstride : 0;
-        const int nrec = ok_ ? tile_bytes : 0;
-        const __amdgpu_buffer_rsrc_t kr =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(kslab + off), (short)0, nrec, 0x00020000);
-        const __amdgpu_buffer_rsrc_t vr =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(vslab + off), (short)0, nrec, 0x00020000);
-        load_tile<PD>(kr, vr, lo, t_);
-      };
-
-      // three-deep register ring: tiles t+1 and t+2 are in flight while t runs
-      Tile<PD> b0, b1, b2;
-      bool ok0, ok1, ok2;
-      issue(w0, b0, ok0);
-      issue(w0 + 1, b1, ok1);
-      // Whole groups of three tiles: a tile past the window end is fetched as
-      // an empty buffer and fully masked, so the body has no early exits.
-      for (int t = w0; t <= wend; t += 3) {
-        issue(t + 2, b2, ok2);
-        attend<PD>(b0, ok0, t, c0, c1, q4, n, ratio, qhi, qlo, lpv, st);
-        issue(t + 3, b0, ok0);
-        attend<PD>(b1, ok1, t + 1, c0, c1, q4, n, ratio, qhi, qlo, lpv, st);
-        issue(t + 4, b1, ok1);
-        attend<PD>(b2, ok2, t + 2, c0, c1, q4, n, ratio, qhi, qlo, lpv, st);
+    for (int i = 0; i < IPR; i++) {
+      const int c = 64 * i + lane;
+      gact[i] = c < kTile * CH;
+      goff[i] = (uint32_t)((c / CH) * tokstride + (c % CH) * 16);
+    }
+    // stage step k into this wave's region of one slot: regions K t0, K t1,
+    // V t0, V t1 of TB bytes each
+    auto stage = [&](int k, uint8_t* dst) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the LDS-copy builtin has no host form
+      const int pg0 = page_of(2 * k), pg1 = page_of(2 * k + 1);
+      const int64_t off0 =
+          pg0 < 0 ? 0 : ((int64_t)pg0 * p.block_size + ((2 * k) % tpp) * kTile) * tokstride;
+      const int64_t off1 =
+          pg1 < 0 ? 0 : ((int64_t)pg1 * p.block_size + ((2 * k + 1) % tpp) * kTile) * tokstride;
+      // absent tiles get an empty range: their chunks read as zeros
+      const __amdgpu_buffer_rsrc_t rk0 = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(kslab + off0), (short)0, pg0 < 0 ? 0 : rec, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rk1 = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(kslab + off1), (short)0, pg1 < 0 ? 0 : rec, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rv0 = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(vslab + off0), (short)0, pg0 < 0 ? 0 : rec, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rv1 = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(vslab + off1), (short)0, pg1 < 0 ? 0 : rec, 0x00020000);
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const __amdgpu_buffer_rsrc_t rs = r == 0 ? rk0 : (r == 1 ? rk1 : (r == 2 ? rv0 : rv1));
+#pragma unroll
+        for (int i = 0; i < IPR; i++)
+          if (gact[i])
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void*)(dst + r * TB + i * 1024), 16,
+                                                     goff[i], 0, 0, 0);
       }
+#else
+      (void)k;
+      (void)dst;
+#endif
+    };
+
+    // per-lane LDS offsets inside a staged step of this wave
+    const uint32_t koff = (uint32_t)(n * EBS + q4 * (PD / 8));
+    const uint32_t voff = (uint32_t)((4 * q4) * EBS + n * (PD / 32));
+    const int slot = 16 / PACK;    // lanes per packed tile slot
+    const int ptile = n / slot;    // tile of this lane's packed scores
+    const int head = n % slot;     // head of this lane's packed scores
+    const uint32_t noff = (uint32_t)(ptile * TB + (4 * q4 + (lane & 3)) * EBS + PD / 2);
+
+    // math of one step from registers
+    auto compute = [&](int k, const StepData<PD>& d) {
+      const int pgA = page_of(2 * k), pgB = page_of(2 * k + 1);
+      const bool okT[2] = {pgA >= 0, pgB >= 0};
+      // scores of both tiles (scheduling barriers keep the two tiles'
+      // dequant temporaries from being live at the same time)
+      float4_t acc[2];
+      acc[0] = tile_scores<PD>(d.k[0], qhi, qlo);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[1] = tile_scores<PD>(d.k[1], qhi, qlo);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int g = 0; g < 2 / PACK; g++) {
+        const uint32_t nkv = d.nkv[g];
+        const uint32_t nr[4] = {quad_bcast<0>(nkv), quad_bcast<1>(nkv), quad_bcast<2>(nkv),
+                                quad_bcast<3>(nkv)};
+        float4_t sc = acc[g];
+        if constexpr (PACK == 2) {
+          // tile 1's scores (lanes 0..7 of each row) into lanes 8..15
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            sc[r] = __int_as_float(__builtin_amdgcn_update_dpp(
+                __float_as_int(acc[0][r]), __float_as_int(acc[1][r]), 0x118, 0xf, 0xc, false));
+        }
+        const int t_first = (2 * k + g) * kTile;  // first token of this group
+        const int t_end = t_first + PACK * kTile;
+        const bool allok = PACK == 2 ? (okT[0] && okT[1]) : okT[g];
+        const bool full = allok && t_first >= c0 && t_end <= c1;
+        bool valid[4];
+        if (!full) {
+          const int T = PACK == 2 ? ptile : g;
+          const bool okl = PACK == 2 ? okT[ptile] : okT[g];
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int t = (2 * k + T) * kTile + 4 * q4 + r;
+            valid[r] = okl && t >= c0 && t < c1;
+          }
+        }
+        half4_t pvh, pvl;
+        softmax_step<PD, PACK>(sc, nr, full, valid, head, ratio, lpv, st, pvh, pvl);
+        if constexpr (PACK == 2) {
+          tile_pv<PD>(d.v[0], pvh, pvl, st);
+          __builtin_amdgcn_sched_barrier(0);
+          tile_pv<PD>(d.v[1], shl8(pvh), shl8(pvl), st);
+        } else {
+          tile_pv<PD>(d.v[g], pvh, pvl, st);
+        }
+      }
+    };
+    // one step: wait until its copy has landed (`later` = copy instructions
+    // issued after it, which may stay in flight), read this wave's region of
+    // `src` into registers, then the math
+    constexpr int NCOPY = 4 * IPR;  // copy instructions per step
+    auto run = [&](int k, const uint8_t* src, int later) {
+      if (later >= 3 * NCOPY) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * NCOPY));
+      else if (later >= 2 * NCOPY) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NCOPY));
+      else if (later >= NCOPY) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NCOPY));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      StepData<PD> d;
+      read_step_asm<PD, PACK>(src, koff, voff, noff, d);
+      compute(k, d);
+    };
+    // copies issued after step k's (those of steps k+1 .. min(k+NSLOT-1, wend))
+    auto later_of = [&](int k, int wend) { return NCOPY * max(0, min(NSLOT - 1, wend - k)); };
+
+    const size_t wofs = (size_t)w * WB;
+    for (int wstep = step0; wstep <= step1; wstep += 32) {
+      const int wend = min(wstep + 31, step1);
+      wtile = 2 * wstep;
+      vpage = (wtile + lane <= tile_last) ? p.indices[ip + (wtile + lane) / tpp] : -1;
+      // steps wstep + j live in slot j % NSLOT; NSLOT - 1 steps are in flight
+      stage(wstep, slot0 + wofs);
+      if (NSLOT > 1 && wstep + 1 <= wend) stage(wstep + 1, slot1 + wofs);
+      if (NSLOT > 2 && wstep + 2 <= wend) stage(wstep + 2, slot2 + wofs);
+      if (NSLOT > 3 && wstep + 3 <= wend) stage(wstep + 3, slot3 + wofs);
+      for (int k = wstep; k <= wend; k += NSLOT) {
+        run(k, slot0 + wofs, later_of(k, wend));
+        if (k + NSLOT <= wend) stage(k + NSLOT, slot0 + wofs);
+        if (k + 1 > wend) break;
+        run(k + 1, slot1 + wofs, later_of(k + 1, wend));
+        if (k + 1 + NSLOT <= wend) stage(k + 1 + NSLOT, slot1 + wofs);
+        if constexpr (NSLOT > 2) {
+          if (k + 2 > wend) break;
+          run(k + 2, slot2 + wofs, later_of(k + 2, wend));
+          if (k + 2 + NSLOT <= wend) stage(k + 2 + NSLOT, slot2 + wofs);
+        }
+        if constexpr (NSLOT > 3) {
+          if (k + 3 > wend) break;
+          run(k + 3, slot3 + wofs, later_of(k + 3, wend));
+          if (k + 3 + NSLOT <= wend) stage(k + 3 + NSLOT, slot3 + wofs);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // drain before the next window's page ids
     }
   }
 
   // ---- finish: O[i][r] = o[h = n][dim (4*q4 + r)*NO + i]
-  const float lt = xor32_sum(xor16_sum(st.lsum));
+  float lt = st.lsum;
+  if constexpr (PACK == 2) lt = lt + __int_as_float(__builtin_amdgcn_mov_dpp(
+                                         __float_as_int(lt), 0x128, 0xf, 0xf, false));
+  lt = xor32_sum(xor16_sum(lt));
   if (n < ratio) {
     // o = pv_scale * O / lsum' (p' = p * pv_scale in both O and lsum')
     const float inv = lt > 0.f ? p.pv_scale / lt : 0.0f;
-    const int64_t row = ((int64_t)b * p.S + s) * p.Hq + kvh * ratio + n;
-    float* out = p.po + row * PD + q4 * (PD / 4);
+    const int64_t orow = ((int64_t)b * p.S + s) * p.Hq + kvh * ratio + n;
+    float* out = p.po + orow * PD + q4 * (PD / 4);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
 #pragma unroll
@@ -477,10 +757,14 @@ void decode_partials_kernel(DecodeParams p) {
     }
     // natural-log LSE: (m + log2(sum p)) * ln 2 = (mb + log2(lsum')) * ln 2
     if (q4 == 0)
-      p.plse[row] = lt > 0.f ? (st.mb + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
+      p.plse[orow] = lt > 0.f ? (st.mb + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
   }
 }
-
+// LSE merge of the splits of one (sequence, q head), inverse rotation, fp16
+// store.  256 threads: split weights are computed once into LDS, then
+// 256/(PD/4) split groups each sum a strided subset of the splits for one
+// float4 column, a tree in LDS adds the groups, and wave 0 runs the inverse
+// FWHT across its 64 lanes.
 template <int PD>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ po,
                                                       const float* __restrict__ plse, int S,
@@ -614,12 +898,27 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   }
   const int pd = padded_dim;
   const int ratio = num_qo_heads / num_kv_heads;
-  int G = 1;
-  for (int g = 8; g >= 1; g--)
-    if (num_kv_heads % g == 0 && g * ratio * pd <= 16384) {
+  // heads per workgroup: a divisor of num_kv_heads whose staged rows fit the
+  // static LDS buffers (G*ebs <= ROW) and whose q scratch fits one buffer
+  const int ebs_expected = pd == 64 ? 48 : (pd == 128 ? 80 : 144);
+  if (ebs != ebs_expected) {
+    set_error("decode: ebs %d does not match padded_dim %d (expected %d)", ebs, pd, ebs_expected);
+    return kEinval;
+  }
+  // heads (waves) per workgroup: a divisor of num_kv_heads up to MAXG whose
+  // q scratch fits the first slot
+  const int maxg = pd == 256 ? 4 : 8;
+  const size_t slot_bytes = (size_t)maxg * 2 * 2 * kTile * ebs_expected;
+  int G = 0;
+  for (int g = maxg; g >= 1; g--)
+    if (num_kv_heads % g == 0 && (size_t)g * ratio * pd * sizeof(float) <= slot_bytes) {
       G = g;
       break;
     }
+  if (G == 0) {
+    set_error("decode: no workgroup shape for %d kv heads, ratio %d", num_kv_heads, ratio);
+    return kEinval;
+  }
   DecodeParams p;
   p.q = static_cast<const _Float16*>(q);
   p.q_sb = q_stride_b;
@@ -651,19 +950,34 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
     set_error("decode: grid too large");
     return kEinval;
   }
-  const size_t lds = (size_t)G * ratio * pd * sizeof(float);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   dim3 grid((unsigned)blocks), block(64 * G);
+  // scores of two tiles share one register set when ratio <= 8 (head size
+  // 256 keeps one tile per set: two would exceed the register file)
+  const bool pack2 = ratio <= 8 && pd <= 128;
+  // LDS slots per wave: steps in flight + 1 (TQ_DECODE_SLOTS=2|4 overrides)
+  int nslot = 2;
+  if (const char* e = getenv("TQ_DECODE_SLOTS")) nslot = atoi(e) == 4 ? 4 : 2;
+#define TQ_LAUNCH(PDV, PK)                                                                     \
+  do {                                                                                         \
+    if (nslot == 4)                                                                            \
+      hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, 4>), grid, block, 0, st, p);         \
+    else                                                                                       \
+      hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, 2>), grid, block, 0, st, p);         \
+  } while (0)
   switch (pd) {
     case 64:
-      hipLaunchKernelGGL(decode_partials_kernel<64>, grid, block, lds, st, p);
+      if (pack2) TQ_LAUNCH(64, 2);
+      else TQ_LAUNCH(64, 1);
       break;
     case 128:
-      hipLaunchKernelGGL(decode_partials_kernel<128>, grid, block, lds, st, p);
+      if (pack2) TQ_LAUNCH(128, 2);
+      else TQ_LAUNCH(128, 1);
       break;
     default:
-      hipLaunchKernelGGL(decode_partials_kernel<256>, grid, block, lds, st, p);
+      TQ_LAUNCH(256, 1);
   }
+#undef TQ_LAUNCH
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("decode: launch failed: %s", hipGetErrorString(e));

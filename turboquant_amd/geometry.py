@@ -55,12 +55,12 @@ def hadamard_signs(pd: int, device="cpu"):
 # the per-workgroup q rotation, and the grid should carry several waves per
 # SIMD (256 CUs x 4 SIMDs) to keep enough loads in flight.
 MIN_CHUNK_TOKENS = 256
-CHUNK_ALIGN = 48
+CHUNK_ALIGN = 16
 TARGET_WAVES = 256 * 4 * 6
 
 
 def choose_splits(batch: int, max_len: int, num_kv_heads: int) -> tuple[int, int]:
-    """Return (num_splits, kv_chunk_size) with kv_chunk_size a multiple of 48
+    """Return (num_splits, kv_chunk_size) with kv_chunk_size a multiple of 16
     and num_splits * kv_chunk_size >= max_len.  Pure function of its inputs,
     so a captured graph keeps its split layout."""
     max_len = max(1, int(max_len))
@@ -68,7 +68,7 @@ def choose_splits(batch: int, max_len: int, num_kv_heads: int) -> tuple[int, int
     by_len = max(1, max_len // MIN_CHUNK_TOKENS)
     splits = max(1, min(want, by_len))
     chunk = math.ceil(max_len / splits)
-    # the decode kernel walks tiles of 16 tokens in groups of three
+    # the decode kernel walks 16-token tiles
     chunk = (chunk + CHUNK_ALIGN - 1) // CHUNK_ALIGN * CHUNK_ALIGN
     splits = math.ceil(max_len / chunk)
     return splits, chunk
