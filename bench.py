@@ -25,6 +25,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the partials kernel at the default split layout,
+# from rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), each scale taken from a
+# 256 MiB device copy (profiles/decode_partials_cfg3_hbm_traffic.md); keyed by
+# (num_splits, kv_chunk_size) so an overridden layout reports null.
+PROFILED_TRAFFIC = {(64, 512): 403502855}
 
 
 def log(msg):
@@ -59,7 +64,7 @@ def make_decode_workload(torch, batch=8, seq_len=32768, hq=32, hkv=8, hd=128, se
     seq = torch.full((batch,), seq_len, dtype=torch.int32, device=dev)
     indices = bt.reshape(-1).contiguous()
     indptr = (torch.arange(batch + 1, dtype=torch.int32, device=dev) * pages_per_seq)
-    splits, cs = choose_splits(batch, seq_len, hkv)
+    splits, cs = choose_splits(batch, seq_len, hkv, hq, pd)
     torch.cuda.synchronize()
     return dict(cache=cache, q=q, seq=seq, indices=indices, indptr=indptr, bt=bt, signs=signs,
                 splits=splits, cs=cs, nb=nb, ebs=ebs, pd=pd, hd=hd, hq=hq, hkv=hkv,
@@ -149,6 +154,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--splits", type=int, default=0, help="override num_splits")
+    ap.add_argument("--copy-ref", action="store_true",
+                    help="only run a plain 256 MiB device copy x5 (HBM counter scale reference)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's path runs on a single MI355X; "
@@ -157,6 +164,17 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_ref:
+        # FETCH_SIZE / WRITE_SIZE of a copy of known size calibrate the
+        # counters used for roofline.traffic
+        a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda:0")
+        c = torch.empty_like(a)
+        for _ in range(5):
+            c.copy_(a)
+        torch.cuda.synchronize()
+        log("copied 256 MiB x5")
+        return
 
     from turboquant_amd import _lib, ops
     _lib.load()
@@ -228,7 +246,8 @@ def main():
         "layout_GB/s": round(layout_bytes / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "decode_partials_kernel<128>",
+                     "traffic": PROFILED_TRAFFIC.get((S, w["cs"])),
+                     "kernel": "decode_partials_kernel<128, 2, 2>",
                      "kernel_us": round(ms_k * 1e3, 2), "alg_bytes": nbytes},
         "cpu_baseline": cpu,
         "write_kernel": wr,

@@ -37,7 +37,7 @@ def run_decode(case, cache, pd, num_splits=None, chunk=None, signs=True, sm_scal
     seq = torch.from_numpy(np.asarray(case["seq_lens"], np.int32)).to(DEV)
     max_len = bt.shape[1] * W.BLOCK
     if num_splits is None:
-        num_splits, chunk = choose_splits(b, max_len, case["num_kv_heads"])
+        num_splits, chunk = choose_splits(b, max_len, case["num_kv_heads"], hq, pd)
     elif chunk is None:
         chunk = -(-max_len // num_splits)
     o = torch.empty((b, hq, pd), dtype=torch.float16, device=DEV)

@@ -51,20 +51,48 @@ def hadamard_signs(pd: int, device="cpu"):
 
 
 # Decode split heuristic for MI355X.  A workgroup serves (sequence, split,
-# group of kv heads); each split should hold enough 16-token tiles to amortise
-# the per-workgroup q rotation, and the grid should carry several waves per
-# SIMD (256 CUs x 4 SIMDs) to keep enough loads in flight.
+# group of G kv heads) with one wave per kv head, and holds a double-buffered
+# LDS staging area sized for the largest G of its head size.  The split count
+# is chosen so the grid fills the workgroup slots of all CUs once: a second,
+# partial round of workgroups would leave most CUs idle at the end.  Each
+# split keeps at least MIN_CHUNK_TOKENS tokens to amortise the per-workgroup
+# q rotation and the LSE merge.
 MIN_CHUNK_TOKENS = 256
 CHUNK_ALIGN = 16
-TARGET_WAVES = 256 * 4 * 6
+MI355X_CUS = 256
+LDS_BYTES_PER_CU = 160 * 1024
+# waves per SIMD the decode kernel's register use allows, by padded head size
+_WAVES_PER_SIMD = {64: 6, 128: 4, 256: 2}
 
 
-def choose_splits(batch: int, max_len: int, num_kv_heads: int) -> tuple[int, int]:
+def decode_workgroup_shape(num_qo_heads: int, num_kv_heads: int, pd: int) -> tuple[int, int]:
+    """(G, workgroups per CU) of the decode kernel; G mirrors the launcher in
+    tq_decode.hip (largest divisor of num_kv_heads up to 8 (4 for pd 256)
+    whose rotated-q scratch fits the first LDS slot)."""
+    ebs = entry_bytes(pd)[2]
+    maxg = 4 if pd == 256 else 8
+    slot_bytes = maxg * 2 * 2 * 16 * ebs
+    ratio = max(1, num_qo_heads // max(1, num_kv_heads))
+    G = 1
+    for g in range(maxg, 0, -1):
+        if num_kv_heads % g == 0 and g * ratio * pd * 4 <= slot_bytes:
+            G = g
+            break
+    by_lds = LDS_BYTES_PER_CU // (2 * slot_bytes)
+    by_waves = 4 * _WAVES_PER_SIMD.get(pd, 2) // G
+    return G, max(1, min(by_lds, by_waves))
+
+
+def choose_splits(batch: int, max_len: int, num_kv_heads: int, num_qo_heads: int | None = None,
+                  padded_dim: int = 128, num_cus: int = MI355X_CUS) -> tuple[int, int]:
     """Return (num_splits, kv_chunk_size) with kv_chunk_size a multiple of 16
     and num_splits * kv_chunk_size >= max_len.  Pure function of its inputs,
     so a captured graph keeps its split layout."""
     max_len = max(1, int(max_len))
-    want = max(1, TARGET_WAVES // max(1, batch * num_kv_heads))
+    hq = num_qo_heads if num_qo_heads else 4 * num_kv_heads
+    G, per_cu = decode_workgroup_shape(hq, num_kv_heads, padded_dim)
+    units = max(1, batch * (num_kv_heads // G))
+    want = max(1, (num_cus * per_cu) // units)
     by_len = max(1, max_len // MIN_CHUNK_TOKENS)
     splits = max(1, min(want, by_len))
     chunk = math.ceil(max_len / splits)

@@ -168,7 +168,8 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
         max_len = max_pages * block_size
         ws = self._v5_ws_cache.get(key)
         if ws is None:
-            num_splits, chunk = choose_splits(batch_size, max_len, self.num_kv_heads)
+            num_splits, chunk = choose_splits(batch_size, max_len, self.num_kv_heads,
+                                             self.num_heads, self._pd)
             padded_batch = batch_size * num_splits
             arange = torch.arange(padded_batch, dtype=torch.int32, device=device)
             ws = {
