@@ -21,8 +21,10 @@ def _check(case, what, **kw):
 def test_cfg1_decode():
     print("case: cfg1 decode B=1 L=1024 32/8/128", flush=True)
     c = W.cfg1()
-    c["block_table"] = c["block_table"]
-    _check(c, "cfg1")
+    got, _ = _check(c, "cfg1")
+    import os
+    want = np.load(os.path.join(os.path.dirname(__file__), "golden", "cfg1_decode.npy"))
+    G.assert_close(got, want, "cfg1 vs golden fixture")
 
 
 def test_cfg3_decode_full_size():

@@ -1,4 +1,6 @@
 """GPU parity of the write kernel against the C oracle: bit-exact cache bytes."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -123,3 +125,32 @@ def test_write_empty_is_noop():
     ops.quantize_write_kv_cache(cache, e, e, hadamard_signs(128, dev),
                                 torch.zeros(0, dtype=torch.int32, device=dev), 128, 128)
     assert int(cache.sum()) == 0
+
+
+def test_cfg1_write_matches_golden_fixture():
+    """configs[0] written on the GPU hashes to the committed golden cache."""
+    import hashlib
+    import json
+    import os
+    print("case: cfg1 write vs tests/golden/cfg1.json", flush=True)
+    with open(os.path.join(os.path.dirname(__file__), "golden", "cfg1.json")) as f:
+        meta = json.load(f)
+    c = W.cfg1()
+    shape, pd = W.cache_bytes(c["num_blocks"], 8, 128)
+    got = _gpu_cache(shape, c["k"], c["v"], c["slots"], 128, pd)
+    assert hashlib.sha256(got.tobytes()).hexdigest() == meta["cache_sha256"]
+
+
+def test_write_kat_vectors():
+    """The golden known-answer rows (normal, tiny, huge, zero, one-hot, outlier
+    rows at head sizes 64/96/128/256) written by the GPU equal the fixture."""
+    import os
+    print("case: write KAT fixture", flush=True)
+    kat = np.load(os.path.join(os.path.dirname(__file__), "golden", "write_kat.npz"))
+    for hd in (64, 96, 128, 256):
+        x, e = kat[f"x{hd}"], kat[f"e{hd}"]
+        n = x.shape[0]
+        shape, pd = W.cache_bytes(math.ceil(n / 16), 1, hd)
+        got = _gpu_cache(shape, x[:, None, :], x[:, None, :], np.arange(n, dtype=np.int32), hd, pd)
+        k_entries = got[0].reshape(-1, shape[-1])[:n, :e.shape[1]]
+        assert np.array_equal(k_entries, e), f"hd {hd}: {_diff_report(k_entries, e)}"

@@ -1,0 +1,162 @@
+"""CPU tests of the host side: geometry, split heuristic, backend class
+surface (reference turboquant/vllm_backend_fused.py:32-86), dispatch
+(reference tests/test_decoder_dispatch.py), plugin registration, and the
+C-ABI library: every symbol include/turboquant_amd.h declares is exported,
+argument errors come back as codes + messages without touching a GPU, and a
+missing library fails loudly."""
+import ctypes
+import math
+import os
+import re
+
+import pytest
+import torch
+
+from turboquant_amd import _lib, geometry
+from turboquant_amd.geometry import choose_splits, entry_bytes, padded_dim
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "turboquant_amd.h")
+
+
+def _header_symbols():
+    text = open(HEADER).read()
+    return set(re.findall(r"^(?:int|int32_t|const char\*)\s+(tq_\w+)\(", text, re.M))
+
+
+def test_geometry_table():
+    assert [padded_dim(h) for h in (32, 64, 80, 96, 128, 200, 256)] == [64, 64, 128, 128, 128,
+                                                                        256, 256]
+    assert entry_bytes(64) == (32, 2, 48)
+    assert entry_bytes(96) == (64, 4, 80)
+    assert entry_bytes(128) == (64, 4, 80)
+    assert entry_bytes(256) == (128, 8, 144)
+
+
+@pytest.mark.parametrize("batch,max_len,hkv,hq,pd", [
+    (8, 32768, 8, 32, 128), (1, 1024, 8, 32, 128), (64, 32768, 8, 32, 128),
+    (8, 32768, 2, 16, 256), (8, 4096, 4, 16, 64), (3, 17, 8, 32, 128), (1, 1, 1, 1, 128),
+    (2, 100000, 1, 16, 128)])
+def test_choose_splits_invariants(batch, max_len, hkv, hq, pd):
+    s, c = choose_splits(batch, max_len, hkv, hq, pd)
+    assert s >= 1 and c % 16 == 0 and c >= 16
+    assert s * c >= max_len and (s - 1) * c < max_len  # no empty trailing split
+    if s > 1:
+        assert c >= geometry.MIN_CHUNK_TOKENS
+    assert choose_splits(batch, max_len, hkv, hq, pd) == (s, c)  # pure
+
+
+def test_choose_splits_fills_one_round_of_workgroups():
+    # B=8, 8 kv heads in one workgroup, 2 workgroups per CU at hd 128
+    assert geometry.decode_workgroup_shape(32, 8, 128) == (8, 2)
+    assert choose_splits(8, 32768, 8, 32, 128) == (64, 512)
+
+
+def test_backend_surface():
+    from turboquant_amd.vllm_backend_fused import TurboQuantBackend, TurboQuantFusedImpl
+    assert TurboQuantBackend.get_name() == "CUSTOM"
+    assert TurboQuantBackend.forward_includes_kv_cache_update is False
+    assert TurboQuantBackend.get_impl_cls() is TurboQuantFusedImpl
+    for dt in ("fp8", "fp8_e4m3"):
+        assert TurboQuantBackend.supports_kv_cache_dtype(dt)
+        assert TurboQuantBackend.get_kv_cache_shape(100, 16, 8, 128, dt) == (2, 100, 16, 8, 80)
+        assert TurboQuantBackend.get_kv_cache_shape(7, 32, 2, 64, dt) == (2, 7, 32, 2, 48)
+        assert TurboQuantBackend.get_kv_cache_page_size(16, 8, 128, torch.uint8, dt) == 20480
+        assert TurboQuantBackend.get_kv_cache_page_size(16, 2, 256, torch.uint8, dt) == 9216
+    assert TurboQuantBackend.get_kv_cache_page_size(16, 8, 128, torch.float16, "auto") is None
+
+
+def test_impl_constructor_and_signs():
+    from turboquant_amd.vllm_backend_fused import TurboQuantFusedImpl
+    impl = TurboQuantFusedImpl(32, 128, 1 / math.sqrt(128), 8, None, None, "fp8")
+    assert impl.kv_cache_dtype == "fp8" and impl._pd == 128
+    assert impl._qbytes == 64 and impl._nbytes == 4
+    impl96 = TurboQuantFusedImpl(16, 96, 0.1, 4, None, None, "fp8_e4m3")
+    assert impl96._pd == 128 and impl96._qbytes == 64
+
+
+def test_signs_recipe():
+    s = geometry.hadamard_signs(128)
+    g = torch.Generator(device="cpu")
+    g.manual_seed(42)
+    r = torch.sign(torch.randn(128, generator=g))
+    r[r == 0] = 1
+    assert torch.equal(s, r) and set(s.tolist()) <= {-1.0, 1.0}
+
+
+def test_dispatch_forced_names(monkeypatch):
+    from turboquant_amd import decoder_dispatch as dd
+    for name, exc in (("v5", RuntimeError), ("v7", RuntimeError), ("bogus", ValueError)):
+        monkeypatch.setenv("TQ_FORCE_KERNEL", name)
+        dd.pick_decode_op.cache_clear()
+        with pytest.raises(exc, match=name):
+            dd.pick_decode_op()
+    dd.pick_decode_op.cache_clear()
+
+
+def test_dispatch_default_registers_reference_op_names(monkeypatch):
+    from turboquant_amd import decoder_dispatch as dd
+    monkeypatch.delenv("TQ_FORCE_KERNEL", raising=False)
+    dd.pick_decode_op.cache_clear()
+    op, name = dd.pick_decode_op()
+    assert name == dd.KERNEL_NAME
+    assert hasattr(torch.ops.turboquant_v5, "decode_v5_from_cache_paged_splitkv_ws")
+    assert hasattr(torch.ops.turboquant_write, "quantize_write_kv_cache")
+    dd.pick_decode_op.cache_clear()
+
+
+def test_plugin_register_idempotent():
+    from turboquant_amd import vllm_plugin
+    vllm_plugin.register()
+    vllm_plugin.register()
+    assert hasattr(torch.ops.turboquant_write, "quantize_write_kv_cache")
+
+
+def test_cabi_exports_every_header_symbol():
+    syms = _header_symbols()
+    assert syms == set(_lib.SIGNATURES), (syms, set(_lib.SIGNATURES))
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for s in syms:
+        assert hasattr(lib, s), s
+    loaded = _lib.load()
+    assert loaded.tq_abi_version() == _lib.ABI_VERSION
+
+
+def test_cabi_argument_errors_without_gpu():
+    lib = _lib.load()
+    null = None
+    # padded_dim 100 is not a supported head geometry
+    rc = lib.tq_decode_paged_splitkv(null, 0, 0, null, null, null, null, null, 1, 32, 8, 100,
+                                     100, 16, 80, 10, 0.1, null, 1, 16, null, null, null, null)
+    assert rc == -22
+    assert b"padded_dim" in lib.tq_last_error()
+    # GQA ratio must divide
+    rc = lib.tq_decode_paged_splitkv(null, 0, 0, null, null, null, null, null, 1, 30, 8, 128,
+                                     128, 16, 80, 10, 0.1, null, 1, 16, null, null, null, null)
+    assert rc == -22
+    # wrong entry size for the head size
+    rc = lib.tq_quantize_write_kv_cache(null, null, null, null, 1, 0, 0, 0, 0, null, null, 4, 8,
+                                        128, 128, 16, 96, 10, null)
+    assert rc == -22 and lib.tq_last_error()
+    rc = lib.tq_combine_splits(null, null, 1, 0, 32, 128, null, null, null)
+    assert rc == -22
+    # an empty batch is a no-op that succeeds
+    assert lib.tq_combine_splits(null, null, 0, 1, 32, 128, null, null, null) == 0
+
+
+def test_missing_library_raises(monkeypatch):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", os.path.join(ROOT, "no_such_dir", "libtq_hip.so"))
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load()
+
+
+def test_ops_raise_instead_of_falling_back(monkeypatch):
+    from turboquant_amd import ops
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", os.path.join(ROOT, "no_such_dir", "libtq_hip.so"))
+    cache = torch.zeros((2, 4, 16, 8, 80), dtype=torch.uint8)
+    k = torch.zeros((3, 8, 128), dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        ops.quantize_write_kv_cache(cache, k, k, geometry.hadamard_signs(128),
+                                    torch.zeros(3, dtype=torch.int32), 128, 128)
