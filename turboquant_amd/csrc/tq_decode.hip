@@ -209,13 +209,12 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
   return acc;
 }
 
-// O[h][dim slot] += V^T P^T for one tile: v[j] = this lane's V code bytes
-// [n*VB, (n+1)*VB) of token 4*q4 + j.
+// This lane's V codes of one tile, transposed so that dword k holds code
+// byte k of tokens 4*q4 + 0..3 (byte j = token j).  v[j] = the lane's V
+// code bytes [n*VB, (n+1)*VB) of token 4*q4 + j.
 template <int PD>
-__device__ __forceinline__ void tile_pv(const uint32_t (*v)[(PD / 32) >= 4 ? PD / 128 : 1],
-                                        half4_t pvh, half4_t pvl, SoftmaxState<PD>& st) {
-  constexpr int VB = PD / 32;
-  uint32_t e[VB];
+__device__ __forceinline__ void tile_v_columns(const uint32_t (*v)[(PD / 32) >= 4 ? PD / 128 : 1],
+                                               uint32_t* e) {
   if constexpr (PD == 64) {
     const uint32_t p01 = v[0][0] | (v[1][0] << 16);
     const uint32_t p23 = v[2][0] | (v[3][0] << 16);
@@ -227,15 +226,29 @@ __device__ __forceinline__ void tile_pv(const uint32_t (*v)[(PD / 32) >= 4 ? PD 
     transpose4(v[0][0], v[1][0], v[2][0], v[3][0], e);
     transpose4(v[0][1], v[1][1], v[2][1], v[3][1], e + 4);
   }
+}
+
+// O[h][dim slot] += V^T P^T over the 32 tokens of one step with
+// v_mfma_f32_16x16x32_f16: the 8 k-values of a lane are tokens 4*q4 + 0..3
+// of tile 0 followed by the same tokens of tile 1, in both A (dequantized
+// V^T, row = dim slot) and B (probabilities p * nv, column = head).
+template <int PD>
+__device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD / 128 : 1],
+                                        const uint32_t (*v1)[(PD / 32) >= 4 ? PD / 128 : 1],
+                                        half8_t p, SoftmaxState<PD>& st) {
+  constexpr int VB = PD / 32;
+  uint32_t e0[VB], e1[VB];
+  tile_v_columns<PD>(v0, e0);
+  tile_v_columns<PD>(v1, e1);
 #pragma unroll
   for (int k = 0; k < VB; k++) {
-    uint32_t x[4];
-    dq8(e[k], x);
-    const half4_t lo4 = as_half4(x[0], x[1]), hi4 = as_half4(x[2], x[3]);
-    st.O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo4, pvh, st.O[2 * k + 1], 0, 0, 0);
-    st.O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo4, pvl, st.O[2 * k + 1], 0, 0, 0);
-    st.O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi4, pvh, st.O[2 * k], 0, 0, 0);
-    st.O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi4, pvl, st.O[2 * k], 0, 0, 0);
+    uint32_t x0[4], x1[4];
+    dq8(e0[k], x0);
+    dq8(e1[k], x1);
+    const half8_t lo8 = as_half8(x0[0], x0[1], x1[0], x1[1]);
+    const half8_t hi8 = as_half8(x0[2], x0[3], x1[2], x1[3]);
+    st.O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo8, p, st.O[2 * k + 1], 0, 0, 0);
+    st.O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi8, p, st.O[2 * k], 0, 0, 0);
   }
 }
 
@@ -419,25 +432,27 @@ __device__ __forceinline__ void read_step_asm(const uint8_t* wslot, uint32_t kof
 #endif
 }
 
-// Online softmax over PACK tiles whose scores sit packed in one float4
-// (slot width 16/PACK lanes per 16-lane row: lane l holds tile (l%16) /
-// (16/PACK), head l % (16/PACK), tokens 4*q4 + r).  nkv: quad-broadcast
-// norms (K low half, V high half) of those tokens.  valid: token masks,
-// `full` when all are valid.  Returns the fp16 hi/lo probabilities * V norm.
-template <int PD, int PACK>
-__device__ __forceinline__ void softmax_step(float4_t acc, const uint32_t* nkv, bool full,
-                                             const bool* valid, int head, int ratio, float lpv,
-                                             SoftmaxState<PD>& st, half4_t& pvh, half4_t& pvl) {
+// Online softmax over the NV score values this lane holds for one step
+// (PACK 2: 4 values, tile (l%16)/8, head l%8; PACK 1: 8 values, tile 0 then
+// tile 1, head l%16; tokens 4*q4 + r).  nk / nv: the tokens' K and V norms.
+// valid: token masks, `full` when all are valid.  Writes p * nv (fp16) to
+// pv; the running max only moves when the step exceeds it by more than 2^3,
+// so p <= 8.
+template <int PD, int NV>
+__device__ __forceinline__ void softmax_step(float* sc, const float* nk, const float* nv,
+                                             bool full, const bool* valid, bool rot8, int head,
+                                             int ratio, float lpv, SoftmaxState<PD>& st,
+                                             _Float16* pv) {
   constexpr int NO = PD / 16;
-  float sc[4];
 #pragma unroll
-  for (int r = 0; r < 4; r++) sc[r] = acc[r] * lo_half(nkv[r]);
+  for (int r = 0; r < NV; r++) sc[r] = sc[r] * nk[r];
   if (!full) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) sc[r] = valid[r] ? sc[r] : -INFINITY;
+    for (int r = 0; r < NV; r++) sc[r] = valid[r] ? sc[r] : -INFINITY;
   }
   float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-  if constexpr (PACK == 2) tmax = fmaxf(tmax, ror8(tmax));
+  if constexpr (NV == 8) tmax = fmaxf(tmax, fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+  if (rot8) tmax = fmaxf(tmax, ror8(tmax));
   tmax = xor16_max(tmax);
   tmax = xor32_max(tmax);
   const float m_new = fmaxf(st.m, tmax);
@@ -450,21 +465,21 @@ __device__ __forceinline__ void softmax_step(float4_t acc, const uint32_t* nkv, 
     st.m = m_new;
     st.mb = m_new + lpv;
   }
-  float pr[4];
+  float pr[NV];
 #pragma unroll
-  for (int r = 0; r < 4; r++) pr[r] = __builtin_amdgcn_exp2f(sc[r] - st.mb);
+  for (int r = 0; r < NV; r++) pr[r] = __builtin_amdgcn_exp2f(sc[r] - st.mb);
   if (!full) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) pr[r] = valid[r] ? pr[r] : 0.0f;
+    for (int r = 0; r < NV; r++) pr[r] = valid[r] ? pr[r] : 0.0f;
   }
-  st.lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+  float ls = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+  if constexpr (NV == 8) ls += (pr[4] + pr[5]) + (pr[6] + pr[7]);
+  st.lsum += ls;
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    float x = pr[r] * hi_half(nkv[r]);
+  for (int r = 0; r < NV; r++) {
+    float x = pr[r] * nv[r];
     if (!full) x = valid[r] ? x : 0.0f;  // masked entries may hold any bits
-    const _Float16 hi = (_Float16)x;
-    pvh[r] = hi;
-    pvl[r] = (_Float16)(x - (float)hi);
+    pv[r] = (_Float16)x;
   }
 }
 
@@ -651,43 +666,48 @@ void decode_partials_kernel(DecodeParams p) {
       __builtin_amdgcn_sched_barrier(0);
       acc[1] = tile_scores<PD>(d.k[1], qhi, qlo);
       __builtin_amdgcn_sched_barrier(0);
+      constexpr int NV = 4 * (2 / PACK);  // score values per lane
+      float sc[NV], nk[NV], nv[NV];
+      bool valid[NV];
 #pragma unroll
       for (int g = 0; g < 2 / PACK; g++) {
         const uint32_t nkv = d.nkv[g];
         const uint32_t nr[4] = {quad_bcast<0>(nkv), quad_bcast<1>(nkv), quad_bcast<2>(nkv),
                                 quad_bcast<3>(nkv)};
-        float4_t sc = acc[g];
-        if constexpr (PACK == 2) {
-          // tile 1's scores (lanes 0..7 of each row) into lanes 8..15
 #pragma unroll
-          for (int r = 0; r < 4; r++)
+        for (int r = 0; r < 4; r++) {
+          nk[4 * g + r] = lo_half(nr[r]);
+          nv[4 * g + r] = hi_half(nr[r]);
+          if constexpr (PACK == 2) {
+            // tile 1's scores (lanes 0..7 of each row) into lanes 8..15
             sc[r] = __int_as_float(__builtin_amdgcn_update_dpp(
                 __float_as_int(acc[0][r]), __float_as_int(acc[1][r]), 0x118, 0xf, 0xc, false));
-        }
-        const int t_first = (2 * k + g) * kTile;  // first token of this group
-        const int t_end = t_first + PACK * kTile;
-        const bool allok = PACK == 2 ? (okT[0] && okT[1]) : okT[g];
-        const bool full = allok && t_first >= c0 && t_end <= c1;
-        bool valid[4];
-        if (!full) {
-          const int T = PACK == 2 ? ptile : g;
-          const bool okl = PACK == 2 ? okT[ptile] : okT[g];
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const int t = (2 * k + T) * kTile + 4 * q4 + r;
-            valid[r] = okl && t >= c0 && t < c1;
+          } else {
+            sc[4 * g + r] = acc[g][r];
           }
         }
-        half4_t pvh, pvl;
-        softmax_step<PD, PACK>(sc, nr, full, valid, head, ratio, lpv, st, pvh, pvl);
-        if constexpr (PACK == 2) {
-          tile_pv<PD>(d.v[0], pvh, pvl, st);
-          __builtin_amdgcn_sched_barrier(0);
-          tile_pv<PD>(d.v[1], shl8(pvh), shl8(pvl), st);
-        } else {
-          tile_pv<PD>(d.v[g], pvh, pvl, st);
+      }
+      const int t_first = 2 * k * kTile;  // first token of this step
+      const bool full = okT[0] && okT[1] && t_first >= c0 && t_first + 2 * kTile <= c1;
+      if (!full) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+          const int T = PACK == 2 ? ptile : i / 4;
+          const int t = (2 * k + T) * kTile + 4 * q4 + (i & 3);
+          valid[i] = okT[T] && t >= c0 && t < c1;
         }
       }
+      _Float16 pv[NV];
+      softmax_step<PD, NV>(sc, nk, nv, full, valid, PACK == 2, head, ratio, lpv, st, pv);
+      half8_t p8;
+      if constexpr (PACK == 2) {
+        half4_t p4 = {pv[0], pv[1], pv[2], pv[3]};
+        const half4_t p4b = shl8(p4);
+        p8 = half8_t{p4[0], p4[1], p4[2], p4[3], p4b[0], p4b[1], p4b[2], p4b[3]};
+      } else {
+        p8 = half8_t{pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
+      }
+      step_pv<PD>(d.v[0], d.v[1], p8, st);
     };
     // one step: wait until its copy has landed (`later` = copy instructions
     // issued after it, which may stay in flight), read this wave's region of
