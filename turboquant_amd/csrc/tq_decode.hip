@@ -595,13 +595,20 @@ void decode_partials_kernel(DecodeParams p) {
     const int tile_last = (c1 - 1) / kTile;
     const int rec = (int)((kTile - 1) * tokstride + EBS);
 
-    // page ids: lane i holds the page of tile wtile + i; a window covers 32
-    // steps (64 tiles), reloaded between windows with the copies drained
-    int vpage = -1;
+    // tile offsets: lane i holds the byte offset inside a slab of tile
+    // wtile + i (64 bit, as lo/hi halves) and tmask bit i says whether that
+    // tile is present (within the split and on a page inside the cache).  A
+    // window covers 32 steps (64 tiles) and is rebuilt between windows with
+    // the copies drained.
+    uint32_t tlo = 0, thi = 0;
+    uint64_t tmask = 0;
     int wtile = 2 * step0;
-    auto page_of = [&](int t) -> int {  // wave-uniform; -1 = not present
-      const int pg = __builtin_amdgcn_readlane(vpage, (t - wtile) & 63);
-      return (t <= tile_last && pg >= 0 && pg < p.num_blocks) ? pg : -1;
+    auto tile_ok = [&](int t) -> bool { return (tmask >> ((t - wtile) & 63)) & 1; };
+    auto tile_base = [&](const uint8_t* slab, int t) -> const uint8_t* {
+      const int j = (t - wtile) & 63;
+      const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)tlo, j);
+      const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)thi, j);
+      return slab + (int64_t)((hi << 32) | lo);
     };
 
     // copy offsets: instruction i of a region moves chunks 64*i + lane
@@ -618,20 +625,16 @@ void decode_partials_kernel(DecodeParams p) {
     // V t0, V t1 of TB bytes each
     auto stage = [&](int k, uint8_t* dst) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the LDS-copy builtin has no host form
-      const int pg0 = page_of(2 * k), pg1 = page_of(2 * k + 1);
-      const int64_t off0 =
-          pg0 < 0 ? 0 : ((int64_t)pg0 * p.block_size + ((2 * k) % tpp) * kTile) * tokstride;
-      const int64_t off1 =
-          pg1 < 0 ? 0 : ((int64_t)pg1 * p.block_size + ((2 * k + 1) % tpp) * kTile) * tokstride;
+      const bool ok0 = tile_ok(2 * k), ok1 = tile_ok(2 * k + 1);
       // absent tiles get an empty range: their chunks read as zeros
       const __amdgpu_buffer_rsrc_t rk0 = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(kslab + off0), (short)0, pg0 < 0 ? 0 : rec, 0x00020000);
+          (void*)tile_base(kslab, 2 * k), (short)0, ok0 ? rec : 0, 0x00020000);
       const __amdgpu_buffer_rsrc_t rk1 = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(kslab + off1), (short)0, pg1 < 0 ? 0 : rec, 0x00020000);
+          (void*)tile_base(kslab, 2 * k + 1), (short)0, ok1 ? rec : 0, 0x00020000);
       const __amdgpu_buffer_rsrc_t rv0 = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(vslab + off0), (short)0, pg0 < 0 ? 0 : rec, 0x00020000);
+          (void*)tile_base(vslab, 2 * k), (short)0, ok0 ? rec : 0, 0x00020000);
       const __amdgpu_buffer_rsrc_t rv1 = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(vslab + off1), (short)0, pg1 < 0 ? 0 : rec, 0x00020000);
+          (void*)tile_base(vslab, 2 * k + 1), (short)0, ok1 ? rec : 0, 0x00020000);
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const __amdgpu_buffer_rsrc_t rs = r == 0 ? rk0 : (r == 1 ? rk1 : (r == 2 ? rv0 : rv1));
@@ -657,8 +660,7 @@ void decode_partials_kernel(DecodeParams p) {
 
     // math of one step from registers
     auto compute = [&](int k, const StepData<PD>& d) {
-      const int pgA = page_of(2 * k), pgB = page_of(2 * k + 1);
-      const bool okT[2] = {pgA >= 0, pgB >= 0};
+      const bool okT[2] = {tile_ok(2 * k), tile_ok(2 * k + 1)};
       // scores of both tiles (scheduling barriers keep the two tiles'
       // dequant temporaries from being live at the same time)
       float4_t acc[2];
@@ -729,7 +731,15 @@ void decode_partials_kernel(DecodeParams p) {
     for (int wstep = step0; wstep <= step1; wstep += 32) {
       const int wend = min(wstep + 31, step1);
       wtile = 2 * wstep;
-      vpage = (wtile + lane <= tile_last) ? p.indices[ip + (wtile + lane) / tpp] : -1;
+      {
+        const int t = wtile + lane;
+        const int pg = (t <= tile_last) ? p.indices[ip + t / tpp] : -1;
+        const bool ok = pg >= 0 && pg < p.num_blocks;
+        const int64_t off = ok ? ((int64_t)pg * p.block_size + (t % tpp) * kTile) * tokstride : 0;
+        tlo = (uint32_t)off;
+        thi = (uint32_t)((uint64_t)off >> 32);
+        tmask = __ballot(ok);
+      }
       // steps wstep + j live in slot j % NSLOT; NSLOT - 1 steps are in flight
       stage(wstep, slot0 + wofs);
       if (NSLOT > 1 && wstep + 1 <= wend) stage(wstep + 1, slot1 + wofs);
