@@ -33,7 +33,6 @@
 //  * Online softmax in the exp2 domain with a lazy rescale (the running max
 //    only moves when a tile exceeds it by more than 2^3), bounding p <= 8.
 #include <math.h>
-#include <stdlib.h>
 
 #include "tq_common.h"
 
@@ -56,8 +55,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // fp16 bits: 0x3216 0x3899 0x3bc8 0x3d95 0x3f71 0x40cb 0x4221 0x440c, split
 // into a high-byte table and a low-byte table of 8 bytes each (byte m).
 constexpr float kCbScale = 1.4809800386428833f;
-constexpr uint32_t kHi0 = 0x3d3b3832u, kHi1 = 0x4442403fu;
-constexpr uint32_t kLo0 = 0x95c89916u, kLo1 = 0x0c21cb71u;
+// tables indexed by 7 - m (byte j holds magnitude 7 - j)
+constexpr uint32_t kHiR0 = 0x3f404244u, kHiR1 = 0x32383b3du;
+constexpr uint32_t kLoR0 = 0x71cb210cu, kLoR1 = 0x1699c895u;
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
   // byte i of the result = byte sel_i of the 8-byte value {hi:lo} (lo = bytes 0-3)
@@ -70,16 +70,17 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 //   x[2] = (byte0 high, byte1 high) x[3] = (byte2 high, byte3 high)
 // i.e. element order {1,3,5,7,0,2,4,6} of the 8 dims the dword holds.
 __device__ __forceinline__ void dq8(uint32_t D, uint32_t* x) {
-  // fold: nibble n -> (neg flag in bit 3, magnitude index m in bits 0-2) with
-  // c[n] = (n >= 8) ? M[n-8] : -M[7-n]
+  // c[n] = (n >= 8) ? M[n-8] : -M[7-n].  G = D ^ (7 in every nibble whose
+  // bit 3 is set): the low 3 bits of each nibble of G are 7 - magnitude
+  // index and bit 3 stays set exactly for the non-negative codes.
   const uint32_t a = D & 0x88888888u;
-  const uint32_t F = ~D ^ (a - (a >> 3));
-  const uint32_t SL = F & 0x07070707u;
-  const uint32_t SH = (F >> 4) & 0x07070707u;
-  const uint32_t hL = perm(kHi1, kHi0, SL) | ((F << 4) & 0x80808080u);
-  const uint32_t lL = perm(kLo1, kLo0, SL);
-  const uint32_t hH = perm(kHi1, kHi0, SH) | (F & 0x80808080u);
-  const uint32_t lH = perm(kLo1, kLo0, SH);
+  const uint32_t G = D ^ (a - (a >> 3));
+  const uint32_t SL = G & 0x07070707u;
+  const uint32_t SH = (G >> 4) & 0x07070707u;
+  const uint32_t hL = perm(kHiR1, kHiR0, SL) | (~(G << 4) & 0x80808080u);
+  const uint32_t lL = perm(kLoR1, kLoR0, SL);
+  const uint32_t hH = perm(kHiR1, kHiR0, SH) | (~G & 0x80808080u);
+  const uint32_t lH = perm(kLoR1, kLoR0, SH);
   x[0] = perm(hL, lL, 0x05010400u);
   x[1] = perm(hL, lL, 0x07030602u);
   x[2] = perm(hH, lH, 0x05010400u);
@@ -192,10 +193,14 @@ struct SoftmaxState {
 
 // Scores of one tile, S[t = 4*q4 + r][h = l%16]: dequantize the K codes
 // this lane holds (token l%16, dims of quarter q4) and run the QK MFMAs
-// against q' (fp16 hi + lo parts, pre-scaled to log2 units).
-template <int PD>
-__device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_t* qhi,
-                                                const half8_t* qlo) {
+// against q' (pre-scaled to log2 units) as fp16 hi + lo parts.  QC: the
+// B operand holds the hi parts in columns 0..7 and the lo parts in columns
+// 8..15 (GQA ratio <= 8), one MFMA per K block, and the two halves are
+// added across lanes n and n+8 (both end up with the sum); otherwise qb/ql
+// are separate hi/lo operands, two MFMAs per K block.
+template <int PD, bool QC>
+__device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_t* qb,
+                                                const half8_t* ql) {
   constexpr int KD = PD / 32;
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -203,8 +208,12 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
     uint32_t x[4];
     dq8(kw[c], x);
     const half8_t kv8 = as_half8(x[0], x[1], x[2], x[3]);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qhi[c], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qlo[c], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qb[c], acc, 0, 0, 0);
+    if constexpr (!QC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, ql[c], acc, 0, 0, 0);
+  }
+  if constexpr (QC) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[r] = acc[r] + ror8(acc[r]);
   }
   return acc;
 }
@@ -262,48 +271,6 @@ struct StepData {
   uint32_t nkv[2];       // norms (K low, V high) of the packed tokens, per group
 };
 
-template <int PD, int PACK>
-__device__ __forceinline__ void read_step(const uint8_t* buf, int slab, int tilebytes, int row,
-                                          uint32_t koff, uint32_t voff, uint32_t noff,
-                                          StepData<PD>& d) {
-#pragma unroll
-  for (int T = 0; T < 2; T++) {
-    const uint8_t* kp = buf + T * tilebytes + koff;
-    if constexpr (PD == 64) {
-      const u32x2 w = *reinterpret_cast<const u32x2*>(kp);
-      d.k[T][0] = w[0]; d.k[T][1] = w[1];
-    } else if constexpr (PD == 128) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(kp);
-#pragma unroll
-      for (int i = 0; i < 4; i++) d.k[T][i] = w[i];
-    } else {
-      const u32x4 w0 = *reinterpret_cast<const u32x4*>(kp);
-      const u32x4 w1 = *reinterpret_cast<const u32x4*>(kp + 16);
-#pragma unroll
-      for (int i = 0; i < 4; i++) { d.k[T][i] = w0[i]; d.k[T][4 + i] = w1[i]; }
-    }
-    const uint8_t* vp = buf + slab + T * tilebytes + voff;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      if constexpr (PD == 64) {
-        d.v[T][j][0] = *reinterpret_cast<const uint16_t*>(vp + j * row);
-      } else if constexpr (PD == 128) {
-        d.v[T][j][0] = *reinterpret_cast<const uint32_t*>(vp + j * row);
-      } else {
-        const u32x2 w = *reinterpret_cast<const u32x2*>(vp + j * row);
-        d.v[T][j][0] = w[0]; d.v[T][j][1] = w[1];
-      }
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < 2 / PACK; g++) {
-    const uint32_t gofs = PACK == 2 ? 0u : (uint32_t)(g * tilebytes);
-    const uint32_t nk = *reinterpret_cast<const uint16_t*>(buf + noff + gofs);
-    const uint32_t nv = *reinterpret_cast<const uint16_t*>(buf + slab + noff + gofs);
-    d.nkv[g] = nk | (nv << 16);
-  }
-}
-
 // s_waitcnt immediate that waits until at most n vector-memory operations
 // are outstanding (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
 // vmcnt[5:4] in [15:14]; expcnt and lgkmcnt left at their maximum).
@@ -316,80 +283,86 @@ __device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)ptr;
 }
 
-// read_step for the per-wave slot layout ([K t0][K t1][V t0][V t1], entry
-// stride EBS), as inline assembly ending in lgkmcnt(0): the compiler does
-// not see these LDS reads, so it adds no conservative wait for the copies in
-// flight; the caller waits for exactly the copy it reads (vmcnt).
+// This wave's share of one staged step, read from LDS into registers, as
+// inline assembly ending in lgkmcnt(0): the compiler does not see these LDS
+// reads, so it adds no conservative wait for the copies in flight; the
+// caller waits for exactly the copy it reads (vmcnt).  Staged layout of one
+// step of one wave: regions K t0, K t1, V t0, V t1 of TB bytes; a region
+// holds the 16 tokens' codes (CB bytes each, token-major) followed by their
+// 16-byte entry tails (norm copies and pad).
 template <int PD, int PACK>
 __device__ __forceinline__ void read_step_asm(const uint8_t* wslot, uint32_t koff,
                                               uint32_t voff, uint32_t noff, StepData<PD>& d) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the kernel stubs
+  constexpr int CB = PD / 2;            // code bytes per token
+  constexpr int TB = kTile * (CB + 16);  // one staged tile
   const uint32_t base = lds_addr(wslot);
   const uint32_t ka = base + koff;
-  if constexpr (PD == 128) {  // EBS 80, tile 1280 B, V slab at 2560
-    const uint32_t va = base + 2560 + voff;
+  const uint32_t va = base + 2 * TB + voff;
+  if constexpr (PD == 128) {
     u32x4 k0, k1;
     asm volatile(
         "ds_read_b128 %0, %10\n\t"
-        "ds_read_b128 %1, %10 offset:1280\n\t"
+        "ds_read_b128 %1, %10 offset:%12\n\t"
         "ds_read_b32 %2, %11\n\t"
-        "ds_read_b32 %3, %11 offset:80\n\t"
-        "ds_read_b32 %4, %11 offset:160\n\t"
-        "ds_read_b32 %5, %11 offset:240\n\t"
-        "ds_read_b32 %6, %11 offset:1280\n\t"
-        "ds_read_b32 %7, %11 offset:1360\n\t"
-        "ds_read_b32 %8, %11 offset:1440\n\t"
-        "ds_read_b32 %9, %11 offset:1520\n\t"
+        "ds_read_b32 %3, %11 offset:%13\n\t"
+        "ds_read_b32 %4, %11 offset:%14\n\t"
+        "ds_read_b32 %5, %11 offset:%15\n\t"
+        "ds_read_b32 %6, %11 offset:%12\n\t"
+        "ds_read_b32 %7, %11 offset:%16\n\t"
+        "ds_read_b32 %8, %11 offset:%17\n\t"
+        "ds_read_b32 %9, %11 offset:%18\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(k0), "=&v"(k1), "=&v"(d.v[0][0][0]), "=&v"(d.v[0][1][0]), "=&v"(d.v[0][2][0]),
           "=&v"(d.v[0][3][0]), "=&v"(d.v[1][0][0]), "=&v"(d.v[1][1][0]), "=&v"(d.v[1][2][0]),
           "=&v"(d.v[1][3][0])
-        : "v"(ka), "v"(va)
+        : "v"(ka), "v"(va), "i"(TB), "i"(CB), "i"(2 * CB), "i"(3 * CB), "i"(TB + CB),
+          "i"(TB + 2 * CB), "i"(TB + 3 * CB)
         : "memory");
 #pragma unroll
     for (int i = 0; i < 4; i++) { d.k[0][i] = k0[i]; d.k[1][i] = k1[i]; }
-  } else if constexpr (PD == 64) {  // EBS 48, tile 768 B, V slab at 1536
-    const uint32_t va = base + 1536 + voff;
+  } else if constexpr (PD == 64) {
     u32x2 k0, k1;
     asm volatile(
         "ds_read_b64 %0, %10\n\t"
-        "ds_read_b64 %1, %10 offset:768\n\t"
+        "ds_read_b64 %1, %10 offset:%12\n\t"
         "ds_read_u16 %2, %11\n\t"
-        "ds_read_u16 %3, %11 offset:48\n\t"
-        "ds_read_u16 %4, %11 offset:96\n\t"
-        "ds_read_u16 %5, %11 offset:144\n\t"
-        "ds_read_u16 %6, %11 offset:768\n\t"
-        "ds_read_u16 %7, %11 offset:816\n\t"
-        "ds_read_u16 %8, %11 offset:864\n\t"
-        "ds_read_u16 %9, %11 offset:912\n\t"
+        "ds_read_u16 %3, %11 offset:%13\n\t"
+        "ds_read_u16 %4, %11 offset:%14\n\t"
+        "ds_read_u16 %5, %11 offset:%15\n\t"
+        "ds_read_u16 %6, %11 offset:%12\n\t"
+        "ds_read_u16 %7, %11 offset:%16\n\t"
+        "ds_read_u16 %8, %11 offset:%17\n\t"
+        "ds_read_u16 %9, %11 offset:%18\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(k0), "=&v"(k1), "=&v"(d.v[0][0][0]), "=&v"(d.v[0][1][0]), "=&v"(d.v[0][2][0]),
           "=&v"(d.v[0][3][0]), "=&v"(d.v[1][0][0]), "=&v"(d.v[1][1][0]), "=&v"(d.v[1][2][0]),
           "=&v"(d.v[1][3][0])
-        : "v"(ka), "v"(va)
+        : "v"(ka), "v"(va), "i"(TB), "i"(CB), "i"(2 * CB), "i"(3 * CB), "i"(TB + CB),
+          "i"(TB + 2 * CB), "i"(TB + 3 * CB)
         : "memory");
     d.k[0][0] = k0[0]; d.k[0][1] = k0[1]; d.k[1][0] = k1[0]; d.k[1][1] = k1[1];
-  } else {  // PD 256: EBS 144, tile 2304 B, V slab at 4608
-    const uint32_t va = base + 4608 + voff;
+  } else {
     u32x4 k0a, k0b, k1a, k1b;
     u32x2 v0, v1, v2, v3, v4, v5, v6, v7;
     asm volatile(
         "ds_read_b128 %0, %12\n\t"
         "ds_read_b128 %1, %12 offset:16\n\t"
-        "ds_read_b128 %2, %12 offset:2304\n\t"
-        "ds_read_b128 %3, %12 offset:2320\n\t"
+        "ds_read_b128 %2, %12 offset:%14\n\t"
+        "ds_read_b128 %3, %12 offset:%15\n\t"
         "ds_read_b64 %4, %13\n\t"
-        "ds_read_b64 %5, %13 offset:144\n\t"
-        "ds_read_b64 %6, %13 offset:288\n\t"
-        "ds_read_b64 %7, %13 offset:432\n\t"
-        "ds_read_b64 %8, %13 offset:2304\n\t"
-        "ds_read_b64 %9, %13 offset:2448\n\t"
-        "ds_read_b64 %10, %13 offset:2592\n\t"
-        "ds_read_b64 %11, %13 offset:2736\n\t"
+        "ds_read_b64 %5, %13 offset:%16\n\t"
+        "ds_read_b64 %6, %13 offset:%17\n\t"
+        "ds_read_b64 %7, %13 offset:%18\n\t"
+        "ds_read_b64 %8, %13 offset:%14\n\t"
+        "ds_read_b64 %9, %13 offset:%19\n\t"
+        "ds_read_b64 %10, %13 offset:%20\n\t"
+        "ds_read_b64 %11, %13 offset:%21\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(k0a), "=&v"(k0b), "=&v"(k1a), "=&v"(k1b), "=&v"(v0), "=&v"(v1), "=&v"(v2),
           "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6), "=&v"(v7)
-        : "v"(ka), "v"(va)
+        : "v"(ka), "v"(va), "i"(TB), "i"(TB + 16), "i"(CB), "i"(2 * CB), "i"(3 * CB),
+          "i"(TB + CB), "i"(TB + 2 * CB), "i"(TB + 3 * CB)
         : "memory");
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -401,9 +374,7 @@ __device__ __forceinline__ void read_step_asm(const uint8_t* wslot, uint32_t kof
 #pragma unroll
       for (int j = 0; j < 4; j++) { d.v[T][j][0] = vv[4 * T + j][0]; d.v[T][j][1] = vv[4 * T + j][1]; }
   }
-  // norms (K, then V one slab further); PACK 1 needs both tiles
-  constexpr int SLAB = 2 * kTile * (PD == 64 ? 48 : (PD == 128 ? 80 : 144));
-  constexpr int TBN = SLAB / 2;
+  // norms (K, then V two regions further); PACK 1 needs both tiles
   const uint32_t na = base + noff;
   if constexpr (PACK == 2) {
     uint32_t nk, nv;
@@ -412,7 +383,7 @@ __device__ __forceinline__ void read_step_asm(const uint8_t* wslot, uint32_t kof
         "ds_read_u16 %1, %2 offset:%3\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(nk), "=&v"(nv)
-        : "v"(na), "i"(SLAB)
+        : "v"(na), "i"(2 * TB)
         : "memory");
     d.nkv[0] = nk | (nv << 16);
   } else {
@@ -424,7 +395,7 @@ __device__ __forceinline__ void read_step_asm(const uint8_t* wslot, uint32_t kof
         "ds_read_u16 %3, %4 offset:%7\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(nk0), "=&v"(nv0), "=&v"(nk1), "=&v"(nv1)
-        : "v"(na), "i"(SLAB), "i"(TBN), "i"(SLAB + TBN)
+        : "v"(na), "i"(2 * TB), "i"(TB), "i"(3 * TB)
         : "memory");
     d.nkv[0] = nk0 | (nv0 << 16);
     d.nkv[1] = nk1 | (nv1 << 16);
@@ -499,7 +470,7 @@ __device__ __forceinline__ half4_t shl8(half4_t v) {
 // the step it computes.  Waves never wait on each other after the q setup:
 // the slots are distinct LDS arrays, so the compiler ties every LDS read to
 // the one copy it depends on and leaves the later copies in flight.
-template <int PD, int PACK, int NSLOT>
+template <int PD, int PACK, bool QC>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : 4)))
 void decode_partials_kernel(DecodeParams p) {
   using Geo = DecodeGeom<PD>;
@@ -510,8 +481,7 @@ void decode_partials_kernel(DecodeParams p) {
   constexpr int MG = Geo::MAXG;
   __shared__ __attribute__((aligned(16))) uint8_t slot0[MG * WB];
   __shared__ __attribute__((aligned(16))) uint8_t slot1[MG * WB];
-  __shared__ __attribute__((aligned(16))) uint8_t slot2[NSLOT > 2 ? MG * WB : 16];
-  __shared__ __attribute__((aligned(16))) uint8_t slot3[NSLOT > 3 ? MG * WB : 16];
+  constexpr int NSLOT = 2;  // LDS slots per wave: one step computed, one in flight
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -525,50 +495,7 @@ void decode_partials_kernel(DecodeParams p) {
   const int kvh = hg * G + w;
   const int ratio = p.ratio;
 
-  // ---- q' = FWHT(s*q)/sqrt(pd) for this wave's `ratio` heads (scratch in slot0)
-  {
-    float* qs = reinterpret_cast<float*>(slot0) + (size_t)w * ratio * PD;
-    for (int i = lane; i < ratio * PD; i += 64) {
-      const int r = i / PD, d = i - r * PD;
-      float x = (float)p.q[b * p.q_sb + (int64_t)(kvh * ratio + r) * p.q_sh + d];
-      if (p.signs) x = x * p.signs[d];
-      qs[i] = x;
-    }
-    __syncthreads();
-    if (p.signs) {
-      for (int h = 1; h < PD; h <<= 1) {
-        for (int i = lane; i < ratio * PD / 2; i += 64) {
-          const int r = i / (PD / 2), j = i - r * (PD / 2);
-          const int lo = r * PD + (j / h) * 2 * h + (j % h);
-          const float a = qs[lo], c = qs[lo + h];
-          qs[lo] = a + c;
-          qs[lo + h] = a - c;
-        }
-        __syncthreads();
-      }
-    }
-  }
-  // q' (pre-scaled to log2 units) split into fp16 high and low parts
-  // (q' = hi + lo to ~22 bits), two MFMAs per K block, so the scores keep
-  // fp32-level accuracy even for heavy-tailed keys.
-  half8_t qhi[KD], qlo[KD];
-  {
-    const float* qs = reinterpret_cast<const float*>(slot0) + (size_t)w * ratio * PD;
-    const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
-    constexpr int ord[8] = {1, 3, 5, 7, 0, 2, 4, 6};
-#pragma unroll
-    for (int c = 0; c < KD; c++) {
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const int d = q4 * (PD / 4) + 8 * c + ord[e];
-        const float x = (n < ratio) ? qs[n * PD + d] * qsc : 0.0f;
-        const _Float16 hi = (_Float16)x;
-        qhi[c][e] = hi;
-        qlo[c][e] = (_Float16)(x - (float)hi);
-      }
-    }
-  }
-  __syncthreads();  // the q scratch is reused by the slots below
+  half8_t qb[KD], ql[QC ? 1 : KD];  // q' operands, filled once the first copy is in flight
 
   SoftmaxState<PD> st;
 #pragma unroll
@@ -583,8 +510,6 @@ void decode_partials_kernel(DecodeParams p) {
   const int c1 = min(c0 + p.cs, L);
   if (c0 < c1) {  // uniform over the workgroup
     constexpr int STEP = 2 * kTile;
-    constexpr int CH = EBS / 16;                   // 16-byte chunks per entry
-    constexpr int IPR = (kTile * CH + 63) / 64;    // copy instructions per region
     constexpr int TB = kTile * EBS;                // one tile of one slab (LDS)
     const int step0 = c0 / STEP, step1 = (c1 - 1) / STEP;
     const int tpp = p.block_size / kTile;  // tiles per page
@@ -611,22 +536,28 @@ void decode_partials_kernel(DecodeParams p) {
       return slab + (int64_t)((hi << 32) | lo);
     };
 
-    // copy offsets: instruction i of a region moves chunks 64*i + lane
-    // (token c / CH, chunk c % CH) of the 16 entries of one tile
-    uint32_t goff[IPR];
-    bool gact[IPR];
+    // Copies of one region (16 tokens of one slab): the codes as CI
+    // instructions of CW bytes per lane (lane-contiguous in LDS, token-major
+    // with CB bytes per token), then the 16-byte entry tails (norm copies and
+    // pad) as one 4-byte-per-lane instruction.  Every lane of every copy is
+    // active, so the copies never sit under divergent control flow.
+    constexpr int CB = PD / 2;                // code bytes per token
+    constexpr int CW = PD == 64 ? 4 : 16;     // bytes per lane of a code copy
+    constexpr int CI = kTile * CB / (64 * CW);  // code copies per region
+    constexpr int CPT = CB / CW;              // lanes per token in a code copy
+    uint32_t goff[CI];
 #pragma unroll
-    for (int i = 0; i < IPR; i++) {
+    for (int i = 0; i < CI; i++) {
       const int c = 64 * i + lane;
-      gact[i] = c < kTile * CH;
-      goff[i] = (uint32_t)((c / CH) * tokstride + (c % CH) * 16);
+      goff[i] = (uint32_t)((c / CPT) * tokstride + (c % CPT) * CW);
     }
+    const uint32_t gtail = (uint32_t)((lane >> 2) * tokstride + CB + (lane & 3) * 4);
     // stage step k into this wave's region of one slot: regions K t0, K t1,
     // V t0, V t1 of TB bytes each
     auto stage = [&](int k, uint8_t* dst) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the LDS-copy builtin has no host form
       const bool ok0 = tile_ok(2 * k), ok1 = tile_ok(2 * k + 1);
-      // absent tiles get an empty range: their chunks read as zeros
+      // absent tiles get an empty range: their bytes read as zeros
       const __amdgpu_buffer_rsrc_t rk0 = __builtin_amdgcn_make_buffer_rsrc(
           (void*)tile_base(kslab, 2 * k), (short)0, ok0 ? rec : 0, 0x00020000);
       const __amdgpu_buffer_rsrc_t rk1 = __builtin_amdgcn_make_buffer_rsrc(
@@ -639,10 +570,11 @@ void decode_partials_kernel(DecodeParams p) {
       for (int r = 0; r < 4; r++) {
         const __amdgpu_buffer_rsrc_t rs = r == 0 ? rk0 : (r == 1 ? rk1 : (r == 2 ? rv0 : rv1));
 #pragma unroll
-        for (int i = 0; i < IPR; i++)
-          if (gact[i])
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void*)(dst + r * TB + i * 1024), 16,
-                                                     goff[i], 0, 0, 0);
+        for (int i = 0; i < CI; i++)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void*)(dst + r * TB + i * 64 * CW), CW,
+                                                   goff[i], 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void*)(dst + r * TB + kTile * CB), 4, gtail,
+                                                 0, 0, 0);
       }
 #else
       (void)k;
@@ -651,12 +583,12 @@ void decode_partials_kernel(DecodeParams p) {
     };
 
     // per-lane LDS offsets inside a staged step of this wave
-    const uint32_t koff = (uint32_t)(n * EBS + q4 * (PD / 8));
-    const uint32_t voff = (uint32_t)((4 * q4) * EBS + n * (PD / 32));
+    const uint32_t koff = (uint32_t)(n * CB + q4 * (PD / 8));
+    const uint32_t voff = (uint32_t)((4 * q4) * CB + n * (PD / 32));
     const int slot = 16 / PACK;    // lanes per packed tile slot
     const int ptile = n / slot;    // tile of this lane's packed scores
     const int head = n % slot;     // head of this lane's packed scores
-    const uint32_t noff = (uint32_t)(ptile * TB + (4 * q4 + (lane & 3)) * EBS + PD / 2);
+    const uint32_t noff = (uint32_t)(ptile * TB + kTile * CB + (4 * q4 + (lane & 3)) * 16);
 
     // math of one step from registers
     auto compute = [&](int k, const StepData<PD>& d) {
@@ -664,9 +596,9 @@ void decode_partials_kernel(DecodeParams p) {
       // scores of both tiles (scheduling barriers keep the two tiles'
       // dequant temporaries from being live at the same time)
       float4_t acc[2];
-      acc[0] = tile_scores<PD>(d.k[0], qhi, qlo);
+      acc[0] = tile_scores<PD, QC>(d.k[0], qb, ql);
       __builtin_amdgcn_sched_barrier(0);
-      acc[1] = tile_scores<PD>(d.k[1], qhi, qlo);
+      acc[1] = tile_scores<PD, QC>(d.k[1], qb, ql);
       __builtin_amdgcn_sched_barrier(0);
       constexpr int NV = 4 * (2 / PACK);  // score values per lane
       float sc[NV], nk[NV], nv[NV];
@@ -681,9 +613,9 @@ void decode_partials_kernel(DecodeParams p) {
           nk[4 * g + r] = lo_half(nr[r]);
           nv[4 * g + r] = hi_half(nr[r]);
           if constexpr (PACK == 2) {
-            // tile 1's scores (lanes 0..7 of each row) into lanes 8..15
-            sc[r] = __int_as_float(__builtin_amdgcn_update_dpp(
-                __float_as_int(acc[0][r]), __float_as_int(acc[1][r]), 0x118, 0xf, 0xc, false));
+            // tile 0's scores in lanes 0..7 of each row, tile 1's in 8..15
+            // (with QC both halves of a row hold the same sums)
+            sc[r] = n < 8 ? acc[0][r] : acc[1][r];
           } else {
             sc[4 * g + r] = acc[g][r];
           }
@@ -714,7 +646,7 @@ void decode_partials_kernel(DecodeParams p) {
     // one step: wait until its copy has landed (`later` = copy instructions
     // issued after it, which may stay in flight), read this wave's region of
     // `src` into registers, then the math
-    constexpr int NCOPY = 4 * IPR;  // copy instructions per step
+    constexpr int NCOPY = 4 * (CI + 1);  // copy instructions per step
     auto run = [&](int k, const uint8_t* src, int later) {
       if (later >= 3 * NCOPY) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * NCOPY));
       else if (later >= 2 * NCOPY) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NCOPY));
@@ -728,41 +660,88 @@ void decode_partials_kernel(DecodeParams p) {
     auto later_of = [&](int k, int wend) { return NCOPY * max(0, min(NSLOT - 1, wend - k)); };
 
     const size_t wofs = (size_t)w * WB;
-    for (int wstep = step0; wstep <= step1; wstep += 32) {
-      const int wend = min(wstep + 31, step1);
+    auto open_window = [&](int wstep) {
       wtile = 2 * wstep;
+      const int t = wtile + lane;
+      const int pg = (t <= tile_last) ? p.indices[ip + t / tpp] : -1;
+      const bool ok = pg >= 0 && pg < p.num_blocks;
+      const int64_t off = ok ? ((int64_t)pg * p.block_size + (t % tpp) * kTile) * tokstride : 0;
+      tlo = (uint32_t)off;
+      thi = (uint32_t)((uint64_t)off >> 32);
+      tmask = __ballot(ok);
+    };
+    // steps wstep + 2j live in slot A (slot1), wstep + 2j + 1 in slot B
+    // (slot0); one step is in flight while the other is computed.  The first
+    // copy is issued before the q setup, which uses slot0 as scratch.
+    uint8_t* const sA = slot1 + wofs;
+    uint8_t* const sB = slot0 + wofs;
+    open_window(step0);
+    stage(step0, sA);
+      // ---- q' = FWHT(s*q)/sqrt(pd) for this wave's `ratio` heads (scratch in slot0)
       {
-        const int t = wtile + lane;
-        const int pg = (t <= tile_last) ? p.indices[ip + t / tpp] : -1;
-        const bool ok = pg >= 0 && pg < p.num_blocks;
-        const int64_t off = ok ? ((int64_t)pg * p.block_size + (t % tpp) * kTile) * tokstride : 0;
-        tlo = (uint32_t)off;
-        thi = (uint32_t)((uint64_t)off >> 32);
-        tmask = __ballot(ok);
+        float* qs = reinterpret_cast<float*>(slot0) + (size_t)w * ratio * PD;
+        for (int i = lane; i < ratio * PD; i += 64) {
+          const int r = i / PD, d = i - r * PD;
+          float x = (float)p.q[b * p.q_sb + (int64_t)(kvh * ratio + r) * p.q_sh + d];
+          if (p.signs) x = x * p.signs[d];
+          qs[i] = x;
+        }
+        __syncthreads();
+        if (p.signs) {
+          for (int h = 1; h < PD; h <<= 1) {
+            for (int i = lane; i < ratio * PD / 2; i += 64) {
+              const int r = i / (PD / 2), j = i - r * (PD / 2);
+              const int lo = r * PD + (j / h) * 2 * h + (j % h);
+              const float a = qs[lo], c = qs[lo + h];
+              qs[lo] = a + c;
+              qs[lo + h] = a - c;
+            }
+            __syncthreads();
+          }
+        }
       }
-      // steps wstep + j live in slot j % NSLOT; NSLOT - 1 steps are in flight
-      stage(wstep, slot0 + wofs);
-      if (NSLOT > 1 && wstep + 1 <= wend) stage(wstep + 1, slot1 + wofs);
-      if (NSLOT > 2 && wstep + 2 <= wend) stage(wstep + 2, slot2 + wofs);
-      if (NSLOT > 3 && wstep + 3 <= wend) stage(wstep + 3, slot3 + wofs);
+      // q' (pre-scaled to log2 units) split into fp16 high and low parts
+      // (q' = hi + lo to ~22 bits), two MFMAs per K block, so the scores keep
+      // fp32-level accuracy even for heavy-tailed keys.
+      {
+        const float* qs = reinterpret_cast<const float*>(slot0) + (size_t)w * ratio * PD;
+        const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
+        constexpr int ord[8] = {1, 3, 5, 7, 0, 2, 4, 6};
+        const int hq = QC ? (n & 7) : n;  // q head of this lane's B column
+    #pragma unroll
+        for (int c = 0; c < KD; c++) {
+    #pragma unroll
+          for (int e = 0; e < 8; e++) {
+            const int d = q4 * (PD / 4) + 8 * c + ord[e];
+            const float x = (hq < ratio) ? qs[hq * PD + d] * qsc : 0.0f;
+            const _Float16 hi = (_Float16)x;
+            const _Float16 lo = (_Float16)(x - (float)hi);
+            if constexpr (QC) {
+              qb[c][e] = n < 8 ? hi : lo;
+            } else {
+              qb[c][e] = hi;
+              ql[c][e] = lo;
+            }
+          }
+        }
+      }
+      __syncthreads();  // the q scratch is reused by the slots below
+
+    for (int wstep = step0;;) {
+      const int wend = min(wstep + 31, step1);
+      if (wstep + 1 <= wend) stage(wstep + 1, sB);
       for (int k = wstep; k <= wend; k += NSLOT) {
-        run(k, slot0 + wofs, later_of(k, wend));
-        if (k + NSLOT <= wend) stage(k + NSLOT, slot0 + wofs);
+        run(k, sA, later_of(k, wend));
+        if (k + NSLOT <= wend) stage(k + NSLOT, sA);
         if (k + 1 > wend) break;
-        run(k + 1, slot1 + wofs, later_of(k + 1, wend));
-        if (k + 1 + NSLOT <= wend) stage(k + 1 + NSLOT, slot1 + wofs);
-        if constexpr (NSLOT > 2) {
-          if (k + 2 > wend) break;
-          run(k + 2, slot2 + wofs, later_of(k + 2, wend));
-          if (k + 2 + NSLOT <= wend) stage(k + 2 + NSLOT, slot2 + wofs);
-        }
-        if constexpr (NSLOT > 3) {
-          if (k + 3 > wend) break;
-          run(k + 3, slot3 + wofs, later_of(k + 3, wend));
-          if (k + 3 + NSLOT <= wend) stage(k + 3 + NSLOT, slot3 + wofs);
-        }
+        run(k + 1, sB, later_of(k + 1, wend));
+        if (k + 1 + NSLOT <= wend) stage(k + 1 + NSLOT, sB);
       }
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // drain before the next window's page ids
+      wstep += 32;
+      if (wstep > step1) break;
+      open_window(wstep);
+      stage(wstep, sA);
     }
   }
 
@@ -985,27 +964,22 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   // scores of two tiles share one register set when ratio <= 8 (head size
   // 256 keeps one tile per set: two would exceed the register file)
   const bool pack2 = ratio <= 8 && pd <= 128;
-  // LDS slots per wave: steps in flight + 1 (TQ_DECODE_SLOTS=2|4 overrides)
-  int nslot = 2;
-  if (const char* e = getenv("TQ_DECODE_SLOTS")) nslot = atoi(e) == 4 ? 4 : 2;
-#define TQ_LAUNCH(PDV, PK)                                                                     \
-  do {                                                                                         \
-    if (nslot == 4)                                                                            \
-      hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, 4>), grid, block, 0, st, p);         \
-    else                                                                                       \
-      hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, 2>), grid, block, 0, st, p);         \
-  } while (0)
+  // q hi/lo parts share one B operand when the GQA ratio leaves 8 columns free
+  const bool qc = ratio <= 8;
+#define TQ_LAUNCH(PDV, PK, QCV) \
+  hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, QCV>), grid, block, 0, st, p)
   switch (pd) {
     case 64:
-      if (pack2) TQ_LAUNCH(64, 2);
-      else TQ_LAUNCH(64, 1);
+      if (pack2) TQ_LAUNCH(64, 2, true);
+      else TQ_LAUNCH(64, 1, false);
       break;
     case 128:
-      if (pack2) TQ_LAUNCH(128, 2);
-      else TQ_LAUNCH(128, 1);
+      if (pack2) TQ_LAUNCH(128, 2, true);
+      else TQ_LAUNCH(128, 1, false);
       break;
     default:
-      TQ_LAUNCH(256, 1);
+      if (qc) TQ_LAUNCH(256, 1, true);
+      else TQ_LAUNCH(256, 1, false);
   }
 #undef TQ_LAUNCH
   hipError_t e = hipGetLastError();
