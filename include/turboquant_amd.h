@@ -66,7 +66,8 @@ int tq_quantize_write_kv_cache(void* k_slab, void* v_slab,
  * SplitKVCombineKernel csrc/include/flashinfer_decode_turboquant_combine.cuh:18-79),
  * called by TurboQuantFusedImpl.forward (turboquant/vllm_backend_fused.py:422-435).
  *
- * q: fp16, element (b, h, d) at q + b*q_stride_b + h*q_stride_h + d, d < pd
+ * q: fp16, element (b, h, d) at q + b*q_stride_b + h*q_stride_h + d, d < pd;
+ *    16-byte aligned, strides multiples of 8 elements, q_stride_h >= pd
  *    (head_dim < pd must be zero padded, as the reference backend does).
  * Sequence b's token t is page indices[indptr[b] + t/block_size], entry
  * t % block_size, for t < seq_lens[b]; block_size % 16 == 0.  Split s of

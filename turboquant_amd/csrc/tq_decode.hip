@@ -497,6 +497,40 @@ void decode_partials_kernel(DecodeParams p) {
 
   half8_t qb[KD], ql[QC ? 1 : KD];  // q' operands, filled once the first copy is in flight
 
+  // s * q of this wave's heads, loaded first so that its latency overlaps
+  // the page-table loads and the first copies: in load j < NQL, lane l holds
+  // the 8 consecutive elements e = 512 j + 8 l .. + 7 (head e / PD, dim
+  // e % PD).  Elements past the wave's heads read as zeros (empty range).
+  // Larger head groups (ratio * PD > 512 * NQL) form q' through LDS below.
+  constexpr int NQL = 2;
+  const bool qreg = ratio * PD <= 512 * NQL;  // uniform
+  float qx[NQL][8];
+#if defined(__HIP_DEVICE_COMPILE__)
+  {
+    const _Float16* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)kvh * ratio * p.q_sh;
+    const int qrec = qreg ? (int)(((ratio - 1) * p.q_sh + PD) * 2) : 0;
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc((void*)qbase, (short)0, qrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsg = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.signs, (short)0, p.signs ? PD * 4 : 0, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < NQL; j++) {
+      const int e = 512 * j + 8 * lane;
+      const int r = e / PD, d = e % PD;
+      const u32x4 qv = __builtin_amdgcn_raw_buffer_load_b128(
+          rq, (uint32_t)((r * p.q_sh + d) * 2), 0, 0);
+      const u32x4 s0 = __builtin_amdgcn_raw_buffer_load_b128(rsg, (uint32_t)(d * 4), 0, 0);
+      const u32x4 s1 = __builtin_amdgcn_raw_buffer_load_b128(rsg, (uint32_t)(d * 4 + 16), 0, 0);
+      const uint32_t sw[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const float x = k & 1 ? hi_half(qv[k / 2]) : lo_half(qv[k / 2]);
+        qx[j][k] = p.signs ? x * __uint_as_float(sw[k]) : x;
+      }
+    }
+  }
+#endif
+
   SoftmaxState<PD> st;
 #pragma unroll
   for (int i = 0; i < NO; i++) st.O[i] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -672,45 +706,135 @@ void decode_partials_kernel(DecodeParams p) {
     };
     // steps wstep + 2j live in slot A (slot1), wstep + 2j + 1 in slot B
     // (slot0); one step is in flight while the other is computed.  The first
-    // copy is issued before the q setup, which uses slot0 as scratch.
+    // copy is issued before the q setup, which may use slot0 as scratch.
     uint8_t* const sA = slot1 + wofs;
     uint8_t* const sB = slot0 + wofs;
     open_window(step0);
     stage(step0, sA);
-      // ---- q' = FWHT(s*q)/sqrt(pd) for this wave's `ratio` heads (scratch in slot0)
-      {
-        float* qs = reinterpret_cast<float*>(slot0) + (size_t)w * ratio * PD;
-        for (int i = lane; i < ratio * PD; i += 64) {
-          const int r = i / PD, d = i - r * PD;
-          float x = (float)p.q[b * p.q_sb + (int64_t)(kvh * ratio + r) * p.q_sh + d];
-          if (p.signs) x = x * p.signs[d];
-          qs[i] = x;
-        }
-        __syncthreads();
-        if (p.signs) {
-          for (int h = 1; h < PD; h <<= 1) {
-            for (int i = lane; i < ratio * PD / 2; i += 64) {
-              const int r = i / (PD / 2), j = i - r * (PD / 2);
-              const int lo = r * PD + (j / h) * 2 * h + (j % h);
-              const float a = qs[lo], c = qs[lo + h];
-              qs[lo] = a + c;
-              qs[lo + h] = a - c;
+    // with q' formed in registers, slot0 is free: the second copy goes too
+    bool staged1 = false;
+    if (qreg && step0 + 1 <= min(step0 + 31, step1)) {
+      stage(step0 + 1, sB);
+      staged1 = true;
+    }
+    // ---- q' = FWHT(s*q)/sqrt(pd), scaled to log2 units and split into
+    // fp16 hi + lo parts (q' = hi + lo to ~22 bits, so the scores keep
+    // fp32-level accuracy even for heavy-tailed keys), in the MFMA B layout.
+    const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
+    constexpr int ord[8] = {1, 3, 5, 7, 0, 2, 4, 6};
+    const int hq = QC ? (n & 7) : n;  // q head of this lane's B column
+    if (qreg) {
+      // in registers: butterflies h = 1, 2, 4 inside a lane, h >= 8 between
+      // lanes l and l ^ (h / 8); no LDS, no barrier
+      if (p.signs) {
+#pragma unroll
+        for (int j = 0; j < NQL; j++) {
+#pragma unroll
+          for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+              if (!(k & h)) {
+                const float a = qx[j][k], c = qx[j][k + h];
+                qx[j][k] = a + c;
+                qx[j][k + h] = a - c;
+              }
+#pragma unroll
+          for (int h = 8; h < PD; h <<= 1) {
+            const bool upper = lane & (h / 8);
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+              const float pt = __shfl_xor(qx[j][k], h / 8);
+              qx[j][k] = upper ? pt - qx[j][k] : qx[j][k] + pt;
             }
-            __syncthreads();
           }
         }
       }
+      // packed fp16 hi / lo pairs in MFMA element order
+      uint32_t ph[NQL][4], pl[NQL][4];
+#pragma unroll
+      for (int j = 0; j < NQL; j++)
+#pragma unroll
+        for (int wd = 0; wd < 4; wd++) {
+          const float x0 = qx[j][ord[2 * wd]] * qsc, x1 = qx[j][ord[2 * wd + 1]] * qsc;
+          const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+          const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+          ph[j][wd] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+                      ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+          pl[j][wd] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+                      ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        }
+      // B operand: column n takes head hq, dims q4 * PD/4 + 8c + ord[.] from
+      // the lane holding those 8 elements
+#pragma unroll
+      for (int c = 0; c < KD; c++) {
+        const int e = hq * PD + q4 * (PD / 4) + 8 * c;
+        const int src = (e % 512) / 8, jsel = e / 512;
+        u32x4 vh, vl;
+#pragma unroll
+        for (int wd = 0; wd < 4; wd++) {
+          uint32_t h = (uint32_t)__shfl((int)ph[0][wd], src);
+          uint32_t l = (uint32_t)__shfl((int)pl[0][wd], src);
+#pragma unroll
+          for (int j = 1; j < NQL; j++) {
+            const uint32_t hj = (uint32_t)__shfl((int)ph[j][wd], src);
+            const uint32_t lj = (uint32_t)__shfl((int)pl[j][wd], src);
+            h = jsel == j ? hj : h;
+            l = jsel == j ? lj : l;
+          }
+          if (hq >= ratio) h = l = 0u;
+          vh[wd] = h;
+          vl[wd] = l;
+        }
+        if constexpr (QC) {
+          qb[c] = __builtin_bit_cast(half8_t, n < 8 ? vh : vl);
+        } else {
+          qb[c] = __builtin_bit_cast(half8_t, vh);
+          ql[c] = __builtin_bit_cast(half8_t, vl);
+        }
+      }
+    } else {
+      // ---- q' = FWHT(s*q)/sqrt(pd) for this wave's `ratio` heads, on an LDS
+      // scratch in slot0.  When it fits, the scratch is this wave's own region
+      // of slot0: only this wave touches it and LDS operations of one wave
+      // complete in order, so no workgroup barrier is needed.  Otherwise the
+      // waves' scratches span slot0 and the workgroup synchronises.
+      const bool qlocal = ratio * PD * 4 <= WB;  // uniform
+      auto qsync = [&]() {
+        if (qlocal) {
+          __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+        } else {
+          __syncthreads();
+        }
+      };
+      float* const qs =
+          reinterpret_cast<float*>(slot0 + (qlocal ? wofs : (size_t)w * ratio * PD * 4));
+      for (int i = lane; i < ratio * PD; i += 64) {
+        const int r = i / PD, d = i - r * PD;
+        float x = (float)p.q[b * p.q_sb + (int64_t)(kvh * ratio + r) * p.q_sh + d];
+        if (p.signs) x = x * p.signs[d];
+        qs[i] = x;
+      }
+      qsync();
+      if (p.signs) {
+        for (int h = 1; h < PD; h <<= 1) {
+          for (int i = lane; i < ratio * PD / 2; i += 64) {
+            const int r = i / (PD / 2), j = i - r * (PD / 2);
+            const int lo = r * PD + (j / h) * 2 * h + (j % h);
+            const float a = qs[lo], c = qs[lo + h];
+            qs[lo] = a + c;
+            qs[lo + h] = a - c;
+          }
+          qsync();
+        }
+      }
       // q' (pre-scaled to log2 units) split into fp16 high and low parts
-      // (q' = hi + lo to ~22 bits), two MFMAs per K block, so the scores keep
-      // fp32-level accuracy even for heavy-tailed keys.
+      // (q' = hi + lo to ~22 bits), so the scores keep fp32-level accuracy
+      // even for heavy-tailed keys.
       {
-        const float* qs = reinterpret_cast<const float*>(slot0) + (size_t)w * ratio * PD;
-        const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
-        constexpr int ord[8] = {1, 3, 5, 7, 0, 2, 4, 6};
-        const int hq = QC ? (n & 7) : n;  // q head of this lane's B column
-    #pragma unroll
+#pragma unroll
         for (int c = 0; c < KD; c++) {
-    #pragma unroll
+#pragma unroll
           for (int e = 0; e < 8; e++) {
             const int d = q4 * (PD / 4) + 8 * c + ord[e];
             const float x = (hq < ratio) ? qs[hq * PD + d] * qsc : 0.0f;
@@ -725,11 +849,20 @@ void decode_partials_kernel(DecodeParams p) {
           }
         }
       }
-      __syncthreads();  // the q scratch is reused by the slots below
+      // the scratch is overwritten by the copies into slot0 below
+      if (qlocal) {
+#if defined(__HIP_DEVICE_COMPILE__)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
+      } else {
+        __syncthreads();
+      }
+    }
 
     for (int wstep = step0;;) {
       const int wend = min(wstep + 31, step1);
-      if (wstep + 1 <= wend) stage(wstep + 1, sB);
+      if (wstep + 1 <= wend && !staged1) stage(wstep + 1, sB);
+      staged1 = false;
       for (int k = wstep; k <= wend; k += NSLOT) {
         run(k, sA, later_of(k, wend));
         if (k + NSLOT <= wend) stage(k + NSLOT, sA);
@@ -903,6 +1036,11 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   }
   if ((uintptr_t)k_slab % 16 || (uintptr_t)v_slab % 16 || (uintptr_t)partition_o % 16) {
     set_error("decode: cache slabs and partition_o must be 16-byte aligned");
+    return kEinval;
+  }
+  if ((uintptr_t)q % 16 || q_stride_b % 8 || q_stride_h % 8 || q_stride_h < padded_dim) {
+    set_error("decode: q must be 16-byte aligned with strides multiple of 8 elements and "
+              "q_stride_h >= padded_dim");
     return kEinval;
   }
   const int pd = padded_dim;
