@@ -119,6 +119,7 @@ struct DecodeParams {
   float qk_scale;     // sm_scale * log2(e) / (sqrt(pd) * kCbScale)
   float inv_sqrt_pd;  // 1/sqrt(pd)
   float pv_scale;     // 1/(sqrt(pd) * kCbScale)
+  int share0;         // two splits per workgroup: 256ths of the pair's tokens for the first
 };
 
 // 4x4 byte transpose: E_k byte j = byte k of D_j
@@ -470,8 +471,9 @@ __device__ __forceinline__ half4_t shl8(half4_t v) {
 // the step it computes.  Waves never wait on each other after the q setup:
 // the slots are distinct LDS arrays, so the compiler ties every LDS read to
 // the one copy it depends on and leaves the later copies in flight.
-template <int PD, int PACK, bool QC>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : 4)))
+template <int PD, int PACK, bool QC, int SPW>
+__global__ __launch_bounds__(64 * DecodeGeom<PD>::MAXG * SPW)
+__attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : 4)))
 void decode_partials_kernel(DecodeParams p) {
   using Geo = DecodeGeom<PD>;
   constexpr int KD = Geo::KD;
@@ -479,20 +481,26 @@ void decode_partials_kernel(DecodeParams p) {
   constexpr int EBS = Geo::EBS;
   constexpr int WB = Geo::WAVE_STEP;  // bytes of one staged step of one wave
   constexpr int MG = Geo::MAXG;
-  __shared__ __attribute__((aligned(16))) uint8_t slot0[MG * WB];
-  __shared__ __attribute__((aligned(16))) uint8_t slot1[MG * WB];
+  __shared__ __attribute__((aligned(16))) uint8_t slot0[SPW * MG * WB];
+  __shared__ __attribute__((aligned(16))) uint8_t slot1[SPW * MG * WB];
   constexpr int NSLOT = 2;  // LDS slots per wave: one step computed, one in flight
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int q4 = lane >> 4, n = lane & 15;
+  // SPW splits per workgroup: waves [sub * G, (sub + 1) * G) serve split
+  // SPW * (split group) + sub, so one workgroup fills a CU's wave slots and
+  // its waves start together
+  const int G = p.G;
+  const int sub = SPW == 1 ? 0 : w / G;  // uniform
+  const int hw = w - sub * G;            // kv head within the group
+  const int nsg = (p.S + SPW - 1) / SPW;  // split groups per sequence
   int bid = blockIdx.x;
   const int hg = bid % p.HG;
   bid /= p.HG;
-  const int s = bid % p.S;
-  const int b = bid / p.S;
-  const int G = p.G;
-  const int kvh = hg * G + w;
+  const int s = (bid % nsg) * SPW + sub;
+  const int b = bid / nsg;
+  const int kvh = hg * G + hw;
   const int ratio = p.ratio;
 
   half8_t qb[KD], ql[QC ? 1 : KD];  // q' operands, filled once the first copy is in flight
@@ -539,9 +547,21 @@ void decode_partials_kernel(DecodeParams p) {
   st.lsum = 0.f;
   const float lpv = -__log2f(p.pv_scale);
 
-  const int L = p.seq_lens[b];
-  const int c0 = s * p.cs;
-  const int c1 = min(c0 + p.cs, L);
+  const int L = s < p.S ? p.seq_lens[b] : 0;  // a split past the last one is empty
+  int c0 = s * p.cs;
+  int c1 = min(c0 + p.cs, L);
+  if (SPW == 2 && s - sub + 1 < p.S) {
+    // The two wave groups of a workgroup do not progress at the same rate
+    // (issue arbitration favours the older waves), so the token range of the
+    // split pair is divided unevenly: the first group takes share0/256 of it,
+    // rounded to whole 32-token steps.  Any partition merges to the same
+    // attention.
+    const int base = (s - sub) * p.cs;
+    const int end = min(base + 2 * p.cs, p.seq_lens[b]);
+    const int mid = min(end, base + ((max(end - base, 0) * p.share0 / 256 + 31) & ~31));
+    c0 = sub ? mid : base;
+    c1 = sub ? end : mid;
+  }
   if (c0 < c1) {  // uniform over the workgroup
     constexpr int STEP = 2 * kTile;
     constexpr int TB = kTile * EBS;                // one tile of one slab (LDS)
@@ -883,7 +903,7 @@ void decode_partials_kernel(DecodeParams p) {
   if constexpr (PACK == 2) lt = lt + __int_as_float(__builtin_amdgcn_mov_dpp(
                                          __float_as_int(lt), 0x128, 0xf, 0xf, false));
   lt = xor32_sum(xor16_sum(lt));
-  if (n < ratio) {
+  if (n < ratio && s < p.S) {
     // o = pv_scale * O / lsum' (p' = p * pv_scale in both O and lsum')
     const float inv = lt > 0.f ? p.pv_scale / lt : 0.0f;
     const int64_t orow = ((int64_t)b * p.S + s) * p.Hq + kvh * ratio + n;
@@ -1092,20 +1112,32 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   p.inv_sqrt_pd = 1.0f / sqrtf((float)pd);
   p.qk_scale = sm_scale * 1.4426950408889634f * p.inv_sqrt_pd / kCbScale;
   p.pv_scale = p.inv_sqrt_pd / kCbScale;
-  const int64_t blocks = (int64_t)batch * num_splits * p.HG;
+  // measured on MI355X at configs[2]: the first (older) group of a
+  // two-split workgroup sustains ~3/4 of the pair's work in the same time
+  p.share0 = 184;
+  // two splits per workgroup (one workgroup per CU) when q' can be formed in
+  // registers, which keeps the workgroup free of barriers; head size 64
+  // keeps three 8-wave workgroups per CU instead
+  const int spw = (ratio * pd <= 1024 && pd >= 128) ? 2 : 1;
+  const int64_t blocks = (int64_t)batch * ((num_splits + spw - 1) / spw) * p.HG;
   if (blocks > 0x7fffffffLL) {
     set_error("decode: grid too large");
     return kEinval;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  dim3 grid((unsigned)blocks), block(64 * G);
+  dim3 grid((unsigned)blocks), block(64 * G * spw);
   // scores of two tiles share one register set when ratio <= 8 (head size
   // 256 keeps one tile per set: two would exceed the register file)
   const bool pack2 = ratio <= 8 && pd <= 128;
   // q hi/lo parts share one B operand when the GQA ratio leaves 8 columns free
   const bool qc = ratio <= 8;
-#define TQ_LAUNCH(PDV, PK, QCV) \
-  hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, QCV>), grid, block, 0, st, p)
+#define TQ_LAUNCH(PDV, PK, QCV)                                                        \
+  do {                                                                                 \
+    if (spw == 2)                                                                      \
+      hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, QCV, 2>), grid, block, 0, st, p); \
+    else                                                                               \
+      hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, QCV, 1>), grid, block, 0, st, p); \
+  } while (0)
   switch (pd) {
     case 64:
       if (pack2) TQ_LAUNCH(64, 2, true);

@@ -66,9 +66,9 @@ _WAVES_PER_SIMD = {64: 6, 128: 4, 256: 2}
 
 
 def decode_workgroup_shape(num_qo_heads: int, num_kv_heads: int, pd: int) -> tuple[int, int]:
-    """(G, workgroups per CU) of the decode kernel; G mirrors the launcher in
-    tq_decode.hip (largest divisor of num_kv_heads up to 8 (4 for pd 256)
-    whose rotated-q scratch fits the first LDS slot)."""
+    """(G, splits resident per CU) of the decode kernel; G mirrors the
+    launcher in tq_decode.hip (largest divisor of num_kv_heads up to 8 (4 for
+    pd 256) whose rotated-q scratch fits the first LDS slot)."""
     ebs = entry_bytes(pd)[2]
     maxg = 4 if pd == 256 else 8
     slot_bytes = maxg * 2 * 2 * 16 * ebs
@@ -78,9 +78,18 @@ def decode_workgroup_shape(num_qo_heads: int, num_kv_heads: int, pd: int) -> tup
         if num_kv_heads % g == 0 and g * ratio * pd * 4 <= slot_bytes:
             G = g
             break
-    by_lds = LDS_BYTES_PER_CU // (2 * slot_bytes)
-    by_waves = 4 * _WAVES_PER_SIMD.get(pd, 2) // G
-    return G, max(1, min(by_lds, by_waves))
+    spw = decode_splits_per_workgroup(num_qo_heads, num_kv_heads, pd)
+    by_lds = LDS_BYTES_PER_CU // (2 * slot_bytes * spw)
+    by_waves = 4 * _WAVES_PER_SIMD.get(pd, 2) // (G * spw)
+    return G, spw * max(1, min(by_lds, by_waves))
+
+
+def decode_splits_per_workgroup(num_qo_heads: int, num_kv_heads: int, pd: int) -> int:
+    """Splits one decode workgroup serves: 2 (one 16-wave workgroup per CU)
+    when q' fits the register path and pd >= 128, else 1 (mirrors the
+    launcher in tq_decode.hip)."""
+    ratio = max(1, num_qo_heads // max(1, num_kv_heads))
+    return 2 if (ratio * pd <= 1024 and pd >= 128) else 1
 
 
 def choose_splits(batch: int, max_len: int, num_kv_heads: int, num_qo_heads: int | None = None,
