@@ -192,25 +192,73 @@ struct SoftmaxState {
   float m, mb, lsum;
 };
 
-// Scores of one tile, S[t = 4*q4 + r][h = l%16]: dequantize the K codes
-// this lane holds (token l%16, dims of quarter q4) and run the QK MFMAs
-// against q' (pre-scaled to log2 units) as fp16 hi + lo parts.  QC: the
-// B operand holds the hi parts in columns 0..7 and the lo parts in columns
-// 8..15 (GQA ratio <= 8), one MFMA per K block, and the two halves are
-// added across lanes n and n+8 (both end up with the sum); otherwise qb/ql
-// are separate hi/lo operands, two MFMAs per K block.
+// Scores of one tile, S[t = 4*q4 + r][h = l%16]: the K codes this lane
+// holds (token l%16, dims of quarter q4; byte j of dword c = dims 8c + 2j,
+// 8c + 2j + 1) are dequantized through the 256-entry LDS table at LDS
+// address 0 (code byte -> two fp16 codebook values, one ds_read each), then
+// the QK MFMAs run against q' (pre-scaled to log2 units) as fp16 hi + lo
+// parts.  QC: the B operand holds the hi parts in columns 0..7 and the lo
+// parts in columns 8..15 (GQA ratio <= 8), one MFMA per K block, and the
+// two halves are added across lanes n and n+8 (both end up with the sum);
+// otherwise qb/ql are separate hi/lo operands, two MFMAs per K block.
+#ifndef TQ_K_LUT
+#define TQ_K_LUT 1
+#endif
+constexpr bool kKLut = TQ_K_LUT;
 template <int PD, bool QC>
 __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_t* qb,
                                                 const half8_t* ql) {
   constexpr int KD = PD / 32;
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (!kKLut) {
 #pragma unroll
-  for (int c = 0; c < KD; c++) {
-    uint32_t x[4];
-    dq8(kw[c], x);
-    const half8_t kv8 = as_half8(x[0], x[1], x[2], x[3]);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qb[c], acc, 0, 0, 0);
-    if constexpr (!QC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, ql[c], acc, 0, 0, 0);
+    for (int c = 0; c < KD; c++) {
+      uint32_t x[4];
+      dq8(kw[c], x);
+      const half8_t kv8 = as_half8(x[0], x[1], x[2], x[3]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qb[c], acc, 0, 0, 0);
+      if constexpr (!QC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, ql[c], acc, 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+  for (int c = 0; c < KD; c += 2) {
+    // two K blocks per batch of 8 table reads and one wait
+    uint32_t x[2][4];
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t a[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      a[u][0] = (kw[c + u] & 0xffu) << 2;
+      a[u][1] = ((kw[c + u] >> 8) & 0xffu) << 2;
+      a[u][2] = ((kw[c + u] >> 16) & 0xffu) << 2;
+      a[u][3] = (kw[c + u] >> 24) << 2;
+    }
+    asm volatile(
+        "ds_read_b32 %0, %8\n\t"
+        "ds_read_b32 %1, %9\n\t"
+        "ds_read_b32 %2, %10\n\t"
+        "ds_read_b32 %3, %11\n\t"
+        "ds_read_b32 %4, %12\n\t"
+        "ds_read_b32 %5, %13\n\t"
+        "ds_read_b32 %6, %14\n\t"
+        "ds_read_b32 %7, %15\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(x[0][0]), "=&v"(x[0][1]), "=&v"(x[0][2]), "=&v"(x[0][3]), "=&v"(x[1][0]),
+          "=&v"(x[1][1]), "=&v"(x[1][2]), "=&v"(x[1][3])
+        : "v"(a[0][0]), "v"(a[0][1]), "v"(a[0][2]), "v"(a[0][3]), "v"(a[1][0]), "v"(a[1][1]),
+          "v"(a[1][2]), "v"(a[1][3])
+        : "memory");
+#else
+    for (int u = 0; u < 2; u++) x[u][0] = x[u][1] = x[u][2] = x[u][3] = kw[c + u];
+#endif
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const half8_t kv8 = as_half8(x[u][0], x[u][1], x[u][2], x[u][3]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qb[c + u], acc, 0, 0, 0);
+      if constexpr (!QC)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, ql[c + u], acc, 0, 0, 0);
+    }
+  }
   }
   if constexpr (QC) {
 #pragma unroll
@@ -284,123 +332,92 @@ __device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)ptr;
 }
 
-// This wave's share of one staged step, read from LDS into registers, as
+// This wave's V share of one staged step, read from LDS into registers, as
 // inline assembly ending in lgkmcnt(0): the compiler does not see these LDS
 // reads, so it adds no conservative wait for the copies in flight; the
 // caller waits for exactly the copy it reads (vmcnt).  Staged layout of one
-// step of one wave: regions K t0, K t1, V t0, V t1 of TB bytes; a region
-// holds the 16 tokens' codes (CB bytes each, token-major) followed by their
-// 16-byte entry tails (norm copies and pad).
+// step of one wave: regions V t0, V t1 of TB bytes; a region holds the 16
+// tokens' codes (CB bytes each, token-major) followed by their 16-byte entry
+// tails (norm copies and pad).  nv[T] = V norm bits of token
+// 4*q4 + (lane & 3) of tile T (PACK 2 reads only the lane's own tile).
 template <int PD, int PACK>
-__device__ __forceinline__ void read_step_asm(const uint8_t* wslot, uint32_t koff,
-                                              uint32_t voff, uint32_t noff, StepData<PD>& d) {
+__device__ __forceinline__ void read_v_asm(const uint8_t* wslot, uint32_t voff, uint32_t noff,
+                                           StepData<PD>& d, uint32_t* nv) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the kernel stubs
   constexpr int CB = PD / 2;            // code bytes per token
   constexpr int TB = kTile * (CB + 16);  // one staged tile
+  constexpr int N1 = PACK == 2 ? 0 : TB;  // second norm: tile 1 (PACK 1 only)
   const uint32_t base = lds_addr(wslot);
-  const uint32_t ka = base + koff;
-  const uint32_t va = base + 2 * TB + voff;
-  if constexpr (PD == 128) {
-    u32x4 k0, k1;
-    asm volatile(
-        "ds_read_b128 %0, %10\n\t"
-        "ds_read_b128 %1, %10 offset:%12\n\t"
-        "ds_read_b32 %2, %11\n\t"
-        "ds_read_b32 %3, %11 offset:%13\n\t"
-        "ds_read_b32 %4, %11 offset:%14\n\t"
-        "ds_read_b32 %5, %11 offset:%15\n\t"
-        "ds_read_b32 %6, %11 offset:%12\n\t"
-        "ds_read_b32 %7, %11 offset:%16\n\t"
-        "ds_read_b32 %8, %11 offset:%17\n\t"
-        "ds_read_b32 %9, %11 offset:%18\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k0), "=&v"(k1), "=&v"(d.v[0][0][0]), "=&v"(d.v[0][1][0]), "=&v"(d.v[0][2][0]),
-          "=&v"(d.v[0][3][0]), "=&v"(d.v[1][0][0]), "=&v"(d.v[1][1][0]), "=&v"(d.v[1][2][0]),
-          "=&v"(d.v[1][3][0])
-        : "v"(ka), "v"(va), "i"(TB), "i"(CB), "i"(2 * CB), "i"(3 * CB), "i"(TB + CB),
-          "i"(TB + 2 * CB), "i"(TB + 3 * CB)
-        : "memory");
-#pragma unroll
-    for (int i = 0; i < 4; i++) { d.k[0][i] = k0[i]; d.k[1][i] = k1[i]; }
-  } else if constexpr (PD == 64) {
-    u32x2 k0, k1;
+  const uint32_t va = base + voff;
+  const uint32_t na = base + noff;
+  if constexpr (PD == 128 || PD == 64) {
+    uint32_t v0, v1, v2, v3, v4, v5, v6, v7;
+    if constexpr (PD == 128) {
+      asm volatile(
+          "ds_read_b32 %0, %10\n\t"
+          "ds_read_b32 %1, %10 offset:%12\n\t"
+          "ds_read_b32 %2, %10 offset:%13\n\t"
+          "ds_read_b32 %3, %10 offset:%14\n\t"
+          "ds_read_b32 %4, %10 offset:%15\n\t"
+          "ds_read_b32 %5, %10 offset:%16\n\t"
+          "ds_read_b32 %6, %10 offset:%17\n\t"
+          "ds_read_b32 %7, %10 offset:%18\n\t"
+          "ds_read_u16 %8, %11\n\t"
+          "ds_read_u16 %9, %11 offset:%19\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6),
+            "=&v"(v7), "=&v"(nv[0]), "=&v"(nv[1])
+          : "v"(va), "v"(na), "i"(CB), "i"(2 * CB), "i"(3 * CB), "i"(TB), "i"(TB + CB),
+            "i"(TB + 2 * CB), "i"(TB + 3 * CB), "i"(N1)
+          : "memory");
+    } else {
+      asm volatile(
+          "ds_read_u16 %0, %10\n\t"
+          "ds_read_u16 %1, %10 offset:%12\n\t"
+          "ds_read_u16 %2, %10 offset:%13\n\t"
+          "ds_read_u16 %3, %10 offset:%14\n\t"
+          "ds_read_u16 %4, %10 offset:%15\n\t"
+          "ds_read_u16 %5, %10 offset:%16\n\t"
+          "ds_read_u16 %6, %10 offset:%17\n\t"
+          "ds_read_u16 %7, %10 offset:%18\n\t"
+          "ds_read_u16 %8, %11\n\t"
+          "ds_read_u16 %9, %11 offset:%19\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6),
+            "=&v"(v7), "=&v"(nv[0]), "=&v"(nv[1])
+          : "v"(va), "v"(na), "i"(CB), "i"(2 * CB), "i"(3 * CB), "i"(TB), "i"(TB + CB),
+            "i"(TB + 2 * CB), "i"(TB + 3 * CB), "i"(N1)
+          : "memory");
+    }
+    d.v[0][0][0] = v0; d.v[0][1][0] = v1; d.v[0][2][0] = v2; d.v[0][3][0] = v3;
+    d.v[1][0][0] = v4; d.v[1][1][0] = v5; d.v[1][2][0] = v6; d.v[1][3][0] = v7;
+  } else {
+    u32x2 v0, v1, v2, v3, v4, v5, v6, v7;
     asm volatile(
         "ds_read_b64 %0, %10\n\t"
         "ds_read_b64 %1, %10 offset:%12\n\t"
-        "ds_read_u16 %2, %11\n\t"
-        "ds_read_u16 %3, %11 offset:%13\n\t"
-        "ds_read_u16 %4, %11 offset:%14\n\t"
-        "ds_read_u16 %5, %11 offset:%15\n\t"
-        "ds_read_u16 %6, %11 offset:%12\n\t"
-        "ds_read_u16 %7, %11 offset:%16\n\t"
-        "ds_read_u16 %8, %11 offset:%17\n\t"
-        "ds_read_u16 %9, %11 offset:%18\n\t"
+        "ds_read_b64 %2, %10 offset:%13\n\t"
+        "ds_read_b64 %3, %10 offset:%14\n\t"
+        "ds_read_b64 %4, %10 offset:%15\n\t"
+        "ds_read_b64 %5, %10 offset:%16\n\t"
+        "ds_read_b64 %6, %10 offset:%17\n\t"
+        "ds_read_b64 %7, %10 offset:%18\n\t"
+        "ds_read_u16 %8, %11\n\t"
+        "ds_read_u16 %9, %11 offset:%19\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k0), "=&v"(k1), "=&v"(d.v[0][0][0]), "=&v"(d.v[0][1][0]), "=&v"(d.v[0][2][0]),
-          "=&v"(d.v[0][3][0]), "=&v"(d.v[1][0][0]), "=&v"(d.v[1][1][0]), "=&v"(d.v[1][2][0]),
-          "=&v"(d.v[1][3][0])
-        : "v"(ka), "v"(va), "i"(TB), "i"(CB), "i"(2 * CB), "i"(3 * CB), "i"(TB + CB),
-          "i"(TB + 2 * CB), "i"(TB + 3 * CB)
+        : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6),
+          "=&v"(v7), "=&v"(nv[0]), "=&v"(nv[1])
+        : "v"(va), "v"(na), "i"(CB), "i"(2 * CB), "i"(3 * CB), "i"(TB), "i"(TB + CB),
+          "i"(TB + 2 * CB), "i"(TB + 3 * CB), "i"(N1)
         : "memory");
-    d.k[0][0] = k0[0]; d.k[0][1] = k0[1]; d.k[1][0] = k1[0]; d.k[1][1] = k1[1];
-  } else {
-    u32x4 k0a, k0b, k1a, k1b;
-    u32x2 v0, v1, v2, v3, v4, v5, v6, v7;
-    asm volatile(
-        "ds_read_b128 %0, %12\n\t"
-        "ds_read_b128 %1, %12 offset:16\n\t"
-        "ds_read_b128 %2, %12 offset:%14\n\t"
-        "ds_read_b128 %3, %12 offset:%15\n\t"
-        "ds_read_b64 %4, %13\n\t"
-        "ds_read_b64 %5, %13 offset:%16\n\t"
-        "ds_read_b64 %6, %13 offset:%17\n\t"
-        "ds_read_b64 %7, %13 offset:%18\n\t"
-        "ds_read_b64 %8, %13 offset:%14\n\t"
-        "ds_read_b64 %9, %13 offset:%19\n\t"
-        "ds_read_b64 %10, %13 offset:%20\n\t"
-        "ds_read_b64 %11, %13 offset:%21\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k0a), "=&v"(k0b), "=&v"(k1a), "=&v"(k1b), "=&v"(v0), "=&v"(v1), "=&v"(v2),
-          "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6), "=&v"(v7)
-        : "v"(ka), "v"(va), "i"(TB), "i"(TB + 16), "i"(CB), "i"(2 * CB), "i"(3 * CB),
-          "i"(TB + CB), "i"(TB + 2 * CB), "i"(TB + 3 * CB)
-        : "memory");
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      d.k[0][i] = k0a[i]; d.k[0][4 + i] = k0b[i]; d.k[1][i] = k1a[i]; d.k[1][4 + i] = k1b[i];
-    }
     const u32x2 vv[8] = {v0, v1, v2, v3, v4, v5, v6, v7};
 #pragma unroll
     for (int T = 0; T < 2; T++)
 #pragma unroll
       for (int j = 0; j < 4; j++) { d.v[T][j][0] = vv[4 * T + j][0]; d.v[T][j][1] = vv[4 * T + j][1]; }
   }
-  // norms (K, then V two regions further); PACK 1 needs both tiles
-  const uint32_t na = base + noff;
-  if constexpr (PACK == 2) {
-    uint32_t nk, nv;
-    asm volatile(
-        "ds_read_u16 %0, %2\n\t"
-        "ds_read_u16 %1, %2 offset:%3\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(nk), "=&v"(nv)
-        : "v"(na), "i"(2 * TB)
-        : "memory");
-    d.nkv[0] = nk | (nv << 16);
-  } else {
-    uint32_t nk0, nv0, nk1, nv1;
-    asm volatile(
-        "ds_read_u16 %0, %4\n\t"
-        "ds_read_u16 %1, %4 offset:%5\n\t"
-        "ds_read_u16 %2, %4 offset:%6\n\t"
-        "ds_read_u16 %3, %4 offset:%7\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(nk0), "=&v"(nv0), "=&v"(nk1), "=&v"(nv1)
-        : "v"(na), "i"(2 * TB), "i"(TB), "i"(3 * TB)
-        : "memory");
-    d.nkv[0] = nk0 | (nv0 << 16);
-    d.nkv[1] = nk1 | (nv1 << 16);
-  }
+#else
+  (void)wslot; (void)voff; (void)noff; (void)d; nv[0] = nv[1] = 0;
 #endif
 }
 
@@ -473,17 +490,34 @@ __device__ __forceinline__ half4_t shl8(half4_t v) {
 // the one copy it depends on and leaves the later copies in flight.
 template <int PD, int PACK, bool QC, int SPW>
 __global__ __launch_bounds__(64 * DecodeGeom<PD>::MAXG * SPW)
-__attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : 4)))
+__attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : (PACK == 1 ? 3 : 4))))
 void decode_partials_kernel(DecodeParams p) {
   using Geo = DecodeGeom<PD>;
   constexpr int KD = Geo::KD;
   constexpr int NO = Geo::NO;
   constexpr int EBS = Geo::EBS;
-  constexpr int WB = Geo::WAVE_STEP;  // bytes of one staged step of one wave
+  constexpr int WB = 2 * kTile * EBS;  // bytes of one staged step (V, two tiles) of one wave
   constexpr int MG = Geo::MAXG;
-  __shared__ __attribute__((aligned(16))) uint8_t slot0[SPW * MG * WB];
-  __shared__ __attribute__((aligned(16))) uint8_t slot1[SPW * MG * WB];
+  // LDS: the K dequant table first (LDS address 0, which the table reads
+  // rely on), then two staging slots
+  struct __attribute__((aligned(16))) Lds {
+    uint32_t klut[256];
+    uint8_t slot0[SPW * MG * WB];
+    uint8_t slot1[SPW * MG * WB];
+  };
+  __shared__ Lds sm;
+  uint8_t* const slot0 = sm.slot0;
+  uint8_t* const slot1 = sm.slot1;
   constexpr int NSLOT = 2;  // LDS slots per wave: one step computed, one in flight
+
+  // K dequant table: code byte -> fp16 values of dims 2j (low half) and
+  // 2j + 1 (high half), built with the same table arithmetic as dq8
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+    uint32_t x[4];
+    dq8((uint32_t)i * 0x01010101u, x);
+    sm.klut[i] = (x[2] & 0xffffu) | (x[0] << 16);
+  }
+  __syncthreads();
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -606,23 +640,51 @@ void decode_partials_kernel(DecodeParams p) {
       goff[i] = (uint32_t)((c / CPT) * tokstride + (c % CPT) * CW);
     }
     const uint32_t gtail = (uint32_t)((lane >> 2) * tokstride + CB + (lane & 3) * 4);
-    // stage step k into this wave's region of one slot: regions K t0, K t1,
-    // V t0, V t1 of TB bytes each
+    // K of one step straight into registers: lane (token n, quarter q4)
+    // loads its PD/8 code bytes of each tile and the K norm of token
+    // 4*q4 + (lane & 3) of each tile (absent tiles read as zeros)
+    struct KRegs {
+      uint32_t k[2][KD];
+      uint32_t nk[2];
+    };
+    const uint32_t kcoff = (uint32_t)(n * tokstride + q4 * (PD / 8));
+    const uint32_t knoff = (uint32_t)((4 * q4 + (lane & 3)) * tokstride + CB);
+    // K codes and norms of step k into kr (absent tiles read as zeros)
+    auto stageK = [&](int k, KRegs& kr) {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+      for (int T = 0; T < 2; T++) {
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)tile_base(kslab, 2 * k + T), (short)0, tile_ok(2 * k + T) ? rec : 0,
+            0x00020000);
+        if constexpr (PD == 64) {
+          const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rk, kcoff, 0, 0);
+          kr.k[T][0] = v[0];
+          kr.k[T][1] = v[1];
+        } else {
+#pragma unroll
+          for (int h = 0; h < KD / 4; h++) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rk, kcoff + 16 * h, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) kr.k[T][4 * h + i] = v[i];
+          }
+        }
+        kr.nk[T] = __builtin_amdgcn_raw_buffer_load_b16(rk, knoff, 0, 0);
+      }
+#else
+      (void)k;
+      (void)kr;
+#endif
+    };
+    // V copies of step k into this wave's region of one slot (regions V t0,
+    // V t1 of TB bytes each)
     auto stage = [&](int k, uint8_t* dst) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the LDS-copy builtin has no host form
-      const bool ok0 = tile_ok(2 * k), ok1 = tile_ok(2 * k + 1);
-      // absent tiles get an empty range: their bytes read as zeros
-      const __amdgpu_buffer_rsrc_t rk0 = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)tile_base(kslab, 2 * k), (short)0, ok0 ? rec : 0, 0x00020000);
-      const __amdgpu_buffer_rsrc_t rk1 = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)tile_base(kslab, 2 * k + 1), (short)0, ok1 ? rec : 0, 0x00020000);
-      const __amdgpu_buffer_rsrc_t rv0 = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)tile_base(vslab, 2 * k), (short)0, ok0 ? rec : 0, 0x00020000);
-      const __amdgpu_buffer_rsrc_t rv1 = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)tile_base(vslab, 2 * k + 1), (short)0, ok1 ? rec : 0, 0x00020000);
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const __amdgpu_buffer_rsrc_t rs = r == 0 ? rk0 : (r == 1 ? rk1 : (r == 2 ? rv0 : rv1));
+      for (int r = 0; r < 2; r++) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)tile_base(vslab, 2 * k + r), (short)0, tile_ok(2 * k + r) ? rec : 0,
+            0x00020000);
 #pragma unroll
         for (int i = 0; i < CI; i++)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void*)(dst + r * TB + i * 64 * CW), CW,
@@ -637,29 +699,32 @@ void decode_partials_kernel(DecodeParams p) {
     };
 
     // per-lane LDS offsets inside a staged step of this wave
-    const uint32_t koff = (uint32_t)(n * CB + q4 * (PD / 8));
     const uint32_t voff = (uint32_t)((4 * q4) * CB + n * (PD / 32));
     const int slot = 16 / PACK;    // lanes per packed tile slot
     const int ptile = n / slot;    // tile of this lane's packed scores
     const int head = n % slot;     // head of this lane's packed scores
     const uint32_t noff = (uint32_t)(ptile * TB + kTile * CB + (4 * q4 + (lane & 3)) * 16);
 
-    // math of one step from registers
-    auto compute = [&](int k, const StepData<PD>& d) {
+    // math of one step; `kr` holds this step's K on entry and receives the
+    // next step's K (loads issued once the scores no longer need it)
+    auto compute = [&](int k, const StepData<PD>& d, KRegs& kr, bool knext) {
       const bool okT[2] = {tile_ok(2 * k), tile_ok(2 * k + 1)};
       // scores of both tiles (scheduling barriers keep the two tiles'
       // dequant temporaries from being live at the same time)
       float4_t acc[2];
-      acc[0] = tile_scores<PD, QC>(d.k[0], qb, ql);
+      acc[0] = tile_scores<PD, QC>(kr.k[0], qb, ql);
       __builtin_amdgcn_sched_barrier(0);
-      acc[1] = tile_scores<PD, QC>(d.k[1], qb, ql);
+      acc[1] = tile_scores<PD, QC>(kr.k[1], qb, ql);
       __builtin_amdgcn_sched_barrier(0);
+      const uint32_t nk01[2] = {kr.nk[0], kr.nk[1]};
+      if (knext) stageK(k + 1, kr);
       constexpr int NV = 4 * (2 / PACK);  // score values per lane
       float sc[NV], nk[NV], nv[NV];
       bool valid[NV];
 #pragma unroll
       for (int g = 0; g < 2 / PACK; g++) {
-        const uint32_t nkv = d.nkv[g];
+        const uint32_t nkv =
+            (PACK == 2 ? (ptile ? nk01[1] : nk01[0]) : nk01[g]) | (d.nkv[g] << 16);
         const uint32_t nr[4] = {quad_bcast<0>(nkv), quad_bcast<1>(nkv), quad_bcast<2>(nkv),
                                 quad_bcast<3>(nkv)};
 #pragma unroll
@@ -700,18 +765,21 @@ void decode_partials_kernel(DecodeParams p) {
     // one step: wait until its copy has landed (`later` = copy instructions
     // issued after it, which may stay in flight), read this wave's region of
     // `src` into registers, then the math
-    constexpr int NCOPY = 4 * (CI + 1);  // copy instructions per step
-    auto run = [&](int k, const uint8_t* src, int later) {
-      if (later >= 3 * NCOPY) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * NCOPY));
-      else if (later >= 2 * NCOPY) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NCOPY));
-      else if (later >= NCOPY) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NCOPY));
+    // V copies per step; the K loads of step k + 1 are issued inside step
+    // k, so when step k + 1 runs only the V copies of step k + 2 may still be
+    // in flight behind it
+    constexpr int NVCOPY = 2 * (CI + 1);
+    KRegs kr;
+    auto run = [&](int k, const uint8_t* src, int wend) {
+      if (k + 1 <= wend) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NVCOPY));
       else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       StepData<PD> d;
-      read_step_asm<PD, PACK>(src, koff, voff, noff, d);
-      compute(k, d);
+      uint32_t nv[2];
+      read_v_asm<PD, PACK>(src, voff, noff, d, nv);
+      d.nkv[0] = nv[0];
+      d.nkv[1] = nv[1];
+      compute(k, d, kr, k + 1 <= wend);
     };
-    // copies issued after step k's (those of steps k+1 .. min(k+NSLOT-1, wend))
-    auto later_of = [&](int k, int wend) { return NCOPY * max(0, min(NSLOT - 1, wend - k)); };
 
     const size_t wofs = (size_t)w * WB;
     auto open_window = [&](int wstep) {
@@ -731,6 +799,7 @@ void decode_partials_kernel(DecodeParams p) {
     uint8_t* const sB = slot0 + wofs;
     open_window(step0);
     stage(step0, sA);
+    stageK(step0, kr);
     // with q' formed in registers, slot0 is free: the second copy goes too
     bool staged1 = false;
     if (qreg && step0 + 1 <= min(step0 + 31, step1)) {
@@ -741,7 +810,10 @@ void decode_partials_kernel(DecodeParams p) {
     // fp16 hi + lo parts (q' = hi + lo to ~22 bits, so the scores keep
     // fp32-level accuracy even for heavy-tailed keys), in the MFMA B layout.
     const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
-    constexpr int ord[8] = {1, 3, 5, 7, 0, 2, 4, 6};
+    // element order of the K operand: dims 8c + e for the table, dq8's
+    // {1,3,5,7,0,2,4,6} otherwise
+    constexpr int ord[8] = {kKLut ? 0 : 1, kKLut ? 1 : 3, kKLut ? 2 : 5, kKLut ? 3 : 7,
+                            kKLut ? 4 : 0, kKLut ? 5 : 2, kKLut ? 6 : 4, kKLut ? 7 : 6};
     const int hq = QC ? (n & 7) : n;  // q head of this lane's B column
     if (qreg) {
       // in registers: butterflies h = 1, 2, 4 inside a lane, h >= 8 between
@@ -884,10 +956,10 @@ void decode_partials_kernel(DecodeParams p) {
       if (wstep + 1 <= wend && !staged1) stage(wstep + 1, sB);
       staged1 = false;
       for (int k = wstep; k <= wend; k += NSLOT) {
-        run(k, sA, later_of(k, wend));
+        run(k, sA, wend);
         if (k + NSLOT <= wend) stage(k + NSLOT, sA);
         if (k + 1 > wend) break;
-        run(k + 1, sB, later_of(k + 1, wend));
+        run(k + 1, sB, wend);
         if (k + 1 + NSLOT <= wend) stage(k + 1 + NSLOT, sB);
       }
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // drain before the next window's page ids
@@ -895,6 +967,7 @@ void decode_partials_kernel(DecodeParams p) {
       if (wstep > step1) break;
       open_window(wstep);
       stage(wstep, sA);
+      stageK(wstep, kr);
     }
   }
 
@@ -1075,7 +1148,7 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   // heads (waves) per workgroup: a divisor of num_kv_heads up to MAXG whose
   // q scratch fits the first slot
   const int maxg = pd == 256 ? 4 : 8;
-  const size_t slot_bytes = (size_t)maxg * 2 * 2 * kTile * ebs_expected;
+  const size_t slot_bytes = (size_t)maxg * 2 * kTile * ebs_expected;
   int G = 0;
   for (int g = maxg; g >= 1; g--)
     if (num_kv_heads % g == 0 && (size_t)g * ratio * pd * sizeof(float) <= slot_bytes) {

@@ -71,7 +71,7 @@ def decode_workgroup_shape(num_qo_heads: int, num_kv_heads: int, pd: int) -> tup
     pd 256) whose rotated-q scratch fits the first LDS slot)."""
     ebs = entry_bytes(pd)[2]
     maxg = 4 if pd == 256 else 8
-    slot_bytes = maxg * 2 * 2 * 16 * ebs
+    slot_bytes = maxg * 2 * 16 * ebs  # V of one two-tile step for each of maxg waves
     ratio = max(1, num_qo_heads // max(1, num_kv_heads))
     G = 1
     for g in range(maxg, 0, -1):
@@ -79,7 +79,7 @@ def decode_workgroup_shape(num_qo_heads: int, num_kv_heads: int, pd: int) -> tup
             G = g
             break
     spw = decode_splits_per_workgroup(num_qo_heads, num_kv_heads, pd)
-    by_lds = LDS_BYTES_PER_CU // (2 * slot_bytes * spw)
+    by_lds = LDS_BYTES_PER_CU // (2 * slot_bytes * spw + 1024)  # + the K table
     by_waves = 4 * _WAVES_PER_SIMD.get(pd, 2) // (G * spw)
     return G, spw * max(1, min(by_lds, by_waves))
 
