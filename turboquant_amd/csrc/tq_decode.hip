@@ -650,26 +650,41 @@ void decode_partials_kernel(DecodeParams p) {
     const uint32_t kcoff = (uint32_t)(n * tokstride + q4 * (PD / 8));
     const uint32_t knoff = (uint32_t)((4 * q4 + (lane & 3)) * tokstride + CB);
     // K codes and norms of step k into kr (absent tiles read as zeros)
+    // The loads are inline assembly: the compiler does not track them, so it
+    // inserts no wait of its own; run() waits for them explicitly (vmcnt) and
+    // then passes the registers through an empty asm so that no use can move
+    // above that wait.
     auto stageK = [&](int k, KRegs& kr) {
 #if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
       for (int T = 0; T < 2; T++) {
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)tile_base(kslab, 2 * k + T), (short)0, tile_ok(2 * k + T) ? rec : 0,
-            0x00020000);
+        const uint64_t base = (uint64_t)tile_base(kslab, 2 * k + T);
+        const u32x4 rk = {(uint32_t)base, (uint32_t)(base >> 32) & 0xffffu,
+                          (uint32_t)(tile_ok(2 * k + T) ? rec : 0), 0x00020000u};
         if constexpr (PD == 64) {
-          const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rk, kcoff, 0, 0);
+          u32x2 v;
+          asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen"
+                       : "=v"(v)
+                       : "v"(kcoff), "s"(rk)
+                       : "memory");
           kr.k[T][0] = v[0];
           kr.k[T][1] = v[1];
         } else {
 #pragma unroll
           for (int h = 0; h < KD / 4; h++) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rk, kcoff + 16 * h, 0, 0);
+            u32x4 v;
+            asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
+                         : "=v"(v)
+                         : "v"(kcoff), "s"(rk), "i"(16 * h)
+                         : "memory");
 #pragma unroll
             for (int i = 0; i < 4; i++) kr.k[T][4 * h + i] = v[i];
           }
         }
-        kr.nk[T] = __builtin_amdgcn_raw_buffer_load_b16(rk, knoff, 0, 0);
+        asm volatile("buffer_load_ushort %0, %1, %2, 0 offen"
+                     : "=v"(kr.nk[T])
+                     : "v"(knoff), "s"(rk)
+                     : "memory");
       }
 #else
       (void)k;
@@ -773,6 +788,14 @@ void decode_partials_kernel(DecodeParams p) {
     auto run = [&](int k, const uint8_t* src, int wend) {
       if (k + 1 <= wend) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NVCOPY));
       else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+      for (int T = 0; T < 2; T++) {
+#pragma unroll
+        for (int i = 0; i < KD; i++) asm volatile("" : "+v"(kr.k[T][i]));
+        asm volatile("" : "+v"(kr.nk[T]));
+      }
+#endif
       StepData<PD> d;
       uint32_t nv[2];
       read_v_asm<PD, PACK>(src, voff, noff, d, nv);
