@@ -994,12 +994,48 @@ void decode_partials_kernel(DecodeParams p) {
     }
   }
 
+  // ---- two splits per workgroup: the second group hands its state to the
+  // first through LDS (the staging slots are drained), the first merges it
+  // and writes one partial for the pair; the second split's row is marked
+  // empty.  Any partition of the tokens merges to the same attention.
+  if constexpr (SPW == 2) {
+    constexpr int NF = 4 * NO + 2;  // floats of state per lane
+    float* const xs = reinterpret_cast<float*>(slot0) + (size_t)hw * 64 * NF;
+    __syncthreads();  // every wave is past its last LDS read
+    if (sub == 1) {
+#pragma unroll
+      for (int i = 0; i < NO; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) xs[(4 * i + r) * 64 + lane] = st.O[i][r];
+      xs[4 * NO * 64 + lane] = st.mb;
+      xs[(4 * NO + 1) * 64 + lane] = st.lsum;
+    }
+    __syncthreads();
+    if (sub == 0) {
+      const float mb1 = xs[4 * NO * 64 + lane];
+      const float l1 = xs[(4 * NO + 1) * 64 + lane];
+      const float mm = fmaxf(st.mb, mb1);
+      const float a0 = st.mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.mb - mm);
+      const float a1 = mb1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb1 - mm);
+#pragma unroll
+      for (int i = 0; i < NO; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          st.O[i][r] = a0 * st.O[i][r] + a1 * xs[(4 * i + r) * 64 + lane];
+      st.lsum = a0 * st.lsum + a1 * l1;
+      st.mb = mm;
+    }
+  }
+
   // ---- finish: O[i][r] = o[h = n][dim (4*q4 + r)*NO + i]
   float lt = st.lsum;
   if constexpr (PACK == 2) lt = lt + __int_as_float(__builtin_amdgcn_mov_dpp(
                                          __float_as_int(lt), 0x128, 0xf, 0xf, false));
   lt = xor32_sum(xor16_sum(lt));
-  if (n < ratio && s < p.S) {
+  if (SPW == 2 && sub == 1) {
+    if (n < ratio && q4 == 0 && s < p.S)
+      p.plse[((int64_t)b * p.S + s) * p.Hq + kvh * ratio + n] = -INFINITY;
+  } else if (n < ratio && s < p.S) {
     // o = pv_scale * O / lsum' (p' = p * pv_scale in both O and lsum')
     const float inv = lt > 0.f ? p.pv_scale / lt : 0.0f;
     const int64_t orow = ((int64_t)b * p.S + s) * p.Hq + kvh * ratio + n;
@@ -1025,51 +1061,85 @@ void decode_partials_kernel(DecodeParams p) {
 // FWHT across its 64 lanes.
 template <int PD>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ po,
-                                                      const float* __restrict__ plse, int S,
+                                                      const float* __restrict__ plse, int S_rows, int step,
                                                       int Hq, const float* __restrict__ signs,
                                                       float inv_sqrt_pd, _Float16* __restrict__ o) {
   constexpr int C = PD / 4;        // float4 columns
   constexpr int NG = 256 / C;      // split groups
   constexpr int V = PD / 64;       // dims per lane in the FWHT
-  extern __shared__ float sm[];    // [S] weights, then [NG][PD] partial sums
+  extern __shared__ float sm[];    // [S] weights or group maxima, then [NG][PD] sums + [NG] denominators
   __shared__ float red[8];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int b = blockIdx.x / Hq, h = blockIdx.x % Hq;
-  const int64_t row0 = (int64_t)b * S * Hq + h;  // row of split s: row0 + s*Hq
+  // split j of sequence b is row row0 + j * rs (rows of the splits a partials
+  // workgroup merged into its first row are skipped with step > 1)
+  const int64_t row0 = (int64_t)b * S_rows * Hq + h;
+  const int64_t rs = (int64_t)step * Hq;
+  const int S = (S_rows + step - 1) / step;
 
-  float mx = -INFINITY;
-  for (int s = tid; s < S; s += 256) mx = fmaxf(mx, plse[row0 + (int64_t)s * Hq]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-  if (lane == 0) red[wv] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  float den = 0.f;
-  for (int s = tid; s < S; s += 256) {
-    const float l = plse[row0 + (int64_t)s * Hq];
-    const float wgt = (l > -INFINITY && mx > -INFINITY) ? __expf(l - mx) : 0.0f;
-    sm[s] = wgt;
-    den += wgt;
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off);
-  __syncthreads();  // red[] reads done, weights visible
-  if (lane == 0) red[4 + wv] = den;
-  float4_t acc = {0.f, 0.f, 0.f, 0.f};
   const int col = tid % C, grp = tid / C;
-  for (int s = grp; s < S; s += NG) {
-    const float wgt = sm[s];
-    if (wgt != 0.0f) {
-      const float4_t v = *reinterpret_cast<const float4_t*>(po + (row0 + (int64_t)s * Hq) * PD + col * 4);
-      acc += wgt * v;
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  float den = 0.f;
+  constexpr int R = 16;  // splits per thread held in registers on the fast path
+  if (S <= NG * R) {
+    // one round trip: the LSEs and partial rows of this thread's splits
+    // (grp, grp + NG, ...) are all loaded before any is used
+    float l[R];
+    float4_t v[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+      const int s = grp + NG * j;
+      l[j] = -INFINITY;
+      v[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+      if (s < S) {
+        l[j] = plse[row0 + (int64_t)s * rs];
+        v[j] = *reinterpret_cast<const float4_t*>(po + (row0 + (int64_t)s * rs) * PD + col * 4);
+      }
     }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < R; j++) mx = fmaxf(mx, l[j]);
+    // the groups hold disjoint splits: max over the groups through LDS
+    if (col == 0) sm[grp] = mx;
+    __syncthreads();
+    mx = -INFINITY;
+    for (int g = 0; g < NG; g++) mx = fmaxf(mx, sm[g]);
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+      const float wgt = (l[j] > -INFINITY && mx > -INFINITY) ? __expf(l[j] - mx) : 0.0f;
+      den += wgt;
+      acc += wgt != 0.0f ? wgt * v[j] : float4_t{0.f, 0.f, 0.f, 0.f};  // skipped rows may hold any bits
+    }
+    __syncthreads();  // the group maxima are read; LDS is reused below
+  } else {
+    float mx = -INFINITY;
+    for (int s = tid; s < S; s += 256) mx = fmaxf(mx, plse[row0 + (int64_t)s * rs]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) red[wv] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int s = tid; s < S; s += 256) {
+      const float l = plse[row0 + (int64_t)s * rs];
+      sm[s] = (l > -INFINITY && mx > -INFINITY) ? __expf(l - mx) : 0.0f;
+    }
+    __syncthreads();  // weights visible
+    for (int s = grp; s < S; s += NG) {
+      const float wgt = sm[s];
+      den += wgt;
+      if (wgt != 0.0f)
+        acc += wgt * *reinterpret_cast<const float4_t*>(po + (row0 + (int64_t)s * rs) * PD + col * 4);
+    }
+    __syncthreads();  // weights no longer needed; reuse LDS for group sums
   }
-  __syncthreads();  // weights no longer needed; reuse LDS for group sums
+  // den: each group summed its own splits (identical in all C lanes of the group)
   float* part = sm;
   *reinterpret_cast<float4_t*>(part + grp * PD + col * 4) = acc;
+  if (col == 0) part[NG * PD + grp] = den;
   __syncthreads();
   if (wv == 0) {
-    den = (red[4] + red[5]) + (red[6] + red[7]);
+    den = 0.f;
+    for (int g = 0; g < NG; g++) den += part[NG * PD + g];
     const float inv = den > 0.f ? 1.0f / den : 0.0f;
     float x[V];
 #pragma unroll
@@ -1104,6 +1174,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     for (int i = 0; i < V; i++) dst[i] = (_Float16)x[i];
   }
 }
+
+// Splits one partials workgroup serves: two (one 16-wave workgroup per CU)
+// when q' is formed in registers (ratio * pd <= 1024) and pd >= 128, which
+// keeps the workgroup free of barriers; head size 64 keeps three 8-wave
+// workgroups per CU instead.  The pair's state is merged into the first
+// split's row and the second row is marked empty.
+int splits_per_workgroup(int ratio, int pd) { return (ratio * pd <= 1024 && pd >= 128) ? 2 : 1; }
 
 int check_geometry(int pd, int hq, int hkv, int bs, int ebs, const char* who) {
   if (pd != 64 && pd != 128 && pd != 256) {
@@ -1211,10 +1288,7 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   // measured on MI355X at configs[2]: the first (older) group of a
   // two-split workgroup sustains ~3/4 of the pair's work in the same time
   p.share0 = 184;
-  // two splits per workgroup (one workgroup per CU) when q' can be formed in
-  // registers, which keeps the workgroup free of barriers; head size 64
-  // keeps three 8-wave workgroups per CU instead
-  const int spw = (ratio * pd <= 1024 && pd >= 128) ? 2 : 1;
+  const int spw = splits_per_workgroup(ratio, pd);
   const int64_t blocks = (int64_t)batch * ((num_splits + spw - 1) / spw) * p.HG;
   if (blocks > 0x7fffffffLL) {
     set_error("decode: grid too large");
@@ -1256,11 +1330,11 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   return 0;
 }
 
-extern "C" int tq_combine_splits(const float* partition_o, const float* partition_lse,
+namespace tq {
+static int combine_splits(const float* partition_o, const float* partition_lse, int step,
                                  int32_t batch, int32_t num_splits, int32_t num_qo_heads,
                                  int32_t padded_dim, const float* signs, void* o,
                                  tq_stream_t stream) {
-  using namespace tq;
   const int pd = padded_dim;
   if (pd != 64 && pd != 128 && pd != 256) {
     set_error("combine: padded_dim must be 64, 128 or 256, got %d", pd);
@@ -1284,7 +1358,8 @@ extern "C" int tq_combine_splits(const float* partition_o, const float* partitio
   const float isq = 1.0f / sqrtf((float)pd);
   _Float16* out = static_cast<_Float16*>(o);
   // LDS: split weights, later reused for the group partial sums (256*4 floats)
-  const size_t lds = sizeof(float) * (size_t)(num_splits > 1024 ? num_splits : 1024);
+  // weights of the splits, or the group sums [NG][pd] plus the group denominators
+  const size_t lds = sizeof(float) * (size_t)(num_splits > 1024 + 64 ? num_splits : 1024 + 64);
   if (lds > 60 * 1024) {
     set_error("combine: num_splits %d too large", num_splits);
     return kEinval;
@@ -1293,15 +1368,15 @@ extern "C" int tq_combine_splits(const float* partition_o, const float* partitio
   switch (pd) {
     case 64:
       hipLaunchKernelGGL(combine_kernel<64>, grid, block, lds, st, partition_o, partition_lse,
-                         num_splits, num_qo_heads, signs, isq, out);
+                         num_splits, step, num_qo_heads, signs, isq, out);
       break;
     case 128:
       hipLaunchKernelGGL(combine_kernel<128>, grid, block, lds, st, partition_o, partition_lse,
-                         num_splits, num_qo_heads, signs, isq, out);
+                         num_splits, step, num_qo_heads, signs, isq, out);
       break;
     default:
       hipLaunchKernelGGL(combine_kernel<256>, grid, block, lds, st, partition_o, partition_lse,
-                         num_splits, num_qo_heads, signs, isq, out);
+                         num_splits, step, num_qo_heads, signs, isq, out);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -1309,6 +1384,16 @@ extern "C" int tq_combine_splits(const float* partition_o, const float* partitio
     return (int)e;
   }
   return 0;
+}
+
+}  // namespace tq
+
+extern "C" int tq_combine_splits(const float* partition_o, const float* partition_lse,
+                                 int32_t batch, int32_t num_splits, int32_t num_qo_heads,
+                                 int32_t padded_dim, const float* signs, void* o,
+                                 tq_stream_t stream) {
+  return tq::combine_splits(partition_o, partition_lse, 1, batch, num_splits, num_qo_heads,
+                            padded_dim, signs, o, stream);
 }
 
 extern "C" int tq_decode_paged_splitkv(const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -1331,6 +1416,8 @@ extern "C" int tq_decode_paged_splitkv(const void* q, int64_t q_stride_b, int64_
                               block_size, ebs, num_blocks, sm_scale, signs, num_splits,
                               kv_chunk_size, partition_o, partition_lse, stream);
   if (rc) return rc;
-  return tq_combine_splits(partition_o, partition_lse, batch, num_splits, num_qo_heads,
-                           padded_dim, signs, o, stream);
+  // rows the partials kernel merged away are skipped
+  return tq::combine_splits(partition_o, partition_lse,
+                            tq::splits_per_workgroup(num_qo_heads / num_kv_heads, padded_dim),
+                            batch, num_splits, num_qo_heads, padded_dim, signs, o, stream);
 }
