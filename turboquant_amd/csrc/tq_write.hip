@@ -12,6 +12,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "tq_common.h"
 
 namespace tq {
@@ -72,6 +74,31 @@ __device__ __forceinline__ uint32_t bucketize(float v, const int32_t* bbits) {
   return pos ? 8u + k : 7u - k;
 }
 
+// Value of lane (lane ^ D) within each 32-lane half, without the LDS
+// crossbar: DPP quad permutes for D = 1, 2, two masked row shifts for D = 4,
+// a row rotate for D = 8 and the row swap of v_permlane16_swap for D = 16.
+template <int D>
+__device__ __forceinline__ float xor_lane(float x) {
+  const int xi = __float_as_int(x);
+  if constexpr (D == 1) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(xi, 0xb1, 0xf, 0xf, false));  // [1,0,3,2]
+  } else if constexpr (D == 2) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(xi, 0x4e, 0xf, 0xf, false));  // [2,3,0,1]
+  } else if constexpr (D == 4) {
+    // banks 0, 2 (lanes 0-3, 8-11 of a row) take lane + 4; banks 1, 3 take lane - 4
+    int r = __builtin_amdgcn_update_dpp(xi, xi, 0x104, 0xf, 0x5, false);  // row_shl:4
+    r = __builtin_amdgcn_update_dpp(r, xi, 0x114, 0xf, 0xa, false);       // row_shr:4
+    return __int_as_float(r);
+  } else if constexpr (D == 8) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(xi, 0x128, 0xf, 0xf, false));  // row_ror:8
+  } else {
+    static_assert(D == 16, "xor distance");
+    const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)xi, (uint32_t)xi, false, false);
+    const bool odd_row = (threadIdx.x & 16) != 0;
+    return __uint_as_float(odd_row ? r[0] : r[1]);
+  }
+}
+
 template <int PD, bool VEC_OK>
 __global__ __launch_bounds__(256) void write_kernel(
     uint8_t* __restrict__ k_slab, uint8_t* __restrict__ v_slab,
@@ -106,8 +133,11 @@ __global__ __launch_bounds__(256) void write_kernel(
   for (int i = 0; i < VEC; i++) ss = __builtin_fmaf(v[i], v[i], ss);
   // 2. 32-lane butterfly; every lane ends with the bits lane 0 of the
   //    reference's shfl_down tree (16,8,4,2,1) holds
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) ss = ss + __shfl_xor(ss, off, 32);
+  ss = ss + xor_lane<16>(ss);
+  ss = ss + xor_lane<8>(ss);
+  ss = ss + xor_lane<4>(ss);
+  ss = ss + xor_lane<2>(ss);
+  ss = ss + xor_lane<1>(ss);
   // 3. IEEE sqrt and reciprocal
   const float l2 = __builtin_sqrtf(ss);
   const float inv = (l2 > 1e-8f) ? (1.0f / l2) : 0.0f;
@@ -129,14 +159,19 @@ __global__ __launch_bounds__(256) void write_kernel(
       }
     }
   }
-#pragma unroll
-  for (int delta = 1; delta < 32; delta <<= 1) {
+  auto cross = [&](auto dist) {
+    constexpr int D = decltype(dist)::value;
 #pragma unroll
     for (int i = 0; i < VEC; i++) {
-      float partner = __shfl_xor(v[i], delta, 32);
-      v[i] = (lane & delta) ? (partner - v[i]) : (v[i] + partner);
+      const float partner = xor_lane<D>(v[i]);
+      v[i] = (lane & D) ? (partner - v[i]) : (v[i] + partner);
     }
-  }
+  };
+  cross(std::integral_constant<int, 1>{});
+  cross(std::integral_constant<int, 2>{});
+  cross(std::integral_constant<int, 4>{});
+  cross(std::integral_constant<int, 8>{});
+  cross(std::integral_constant<int, 16>{});
 #pragma unroll
   for (int i = 0; i < VEC; i++) v[i] = v[i] * scale;
 
