@@ -159,13 +159,13 @@ __global__ __launch_bounds__(256) void write_kernel(
       }
     }
   }
+  // butterfly partner + sign * own value: fma(+-1, v, p) rounds once, to the
+  // same bits as v + p (lower lane) or p - v (upper lane)
   auto cross = [&](auto dist) {
     constexpr int D = decltype(dist)::value;
+    const float sg = (lane & D) ? -1.0f : 1.0f;
 #pragma unroll
-    for (int i = 0; i < VEC; i++) {
-      const float partner = xor_lane<D>(v[i]);
-      v[i] = (lane & D) ? (partner - v[i]) : (v[i] + partner);
-    }
+    for (int i = 0; i < VEC; i++) v[i] = __builtin_fmaf(sg, v[i], xor_lane<D>(v[i]));
   };
   cross(std::integral_constant<int, 1>{});
   cross(std::integral_constant<int, 2>{});
