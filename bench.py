@@ -29,7 +29,7 @@ HBM_PEAK_GBS = 8000.0
 # from rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), each scale taken from a
 # 256 MiB device copy (profiles/decode_partials_cfg3_hbm_traffic.md); keyed by
 # (num_splits, kv_chunk_size) so an overridden layout reports null.
-PROFILED_TRAFFIC = {(64, 512): 403502855}
+PROFILED_TRAFFIC = {(64, 512): 420120318}
 
 
 def log(msg):
@@ -247,7 +247,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": PROFILED_TRAFFIC.get((S, w["cs"])),
-                     "kernel": "decode_partials_kernel<128, 2, 2>",
+                     "kernel": "decode_partials_kernel<128, 2, true, 2>",
                      "kernel_us": round(ms_k * 1e3, 2), "alg_bytes": nbytes},
         "cpu_baseline": cpu,
         "write_kernel": wr,
