@@ -1301,25 +1301,23 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   const bool pack2 = ratio <= 8 && pd <= 128;
   // q hi/lo parts share one B operand when the GQA ratio leaves 8 columns free
   const bool qc = ratio <= 8;
-#define TQ_LAUNCH(PDV, PK, QCV)                                                        \
-  do {                                                                                 \
-    if (spw == 2)                                                                      \
-      hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, QCV, 2>), grid, block, 0, st, p); \
-    else                                                                               \
-      hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, QCV, 1>), grid, block, 0, st, p); \
-  } while (0)
+  // only the (head size, packing, split pairing) combinations these rules
+  // reach are instantiated
+#define TQ_LAUNCH(PDV, PK, QCV, SPWV) \
+  hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, QCV, SPWV>), grid, block, 0, st, p)
   switch (pd) {
-    case 64:
-      if (pack2) TQ_LAUNCH(64, 2, true);
-      else TQ_LAUNCH(64, 1, false);
+    case 64:  // spw == 1
+      if (pack2) TQ_LAUNCH(64, 2, true, 1);
+      else TQ_LAUNCH(64, 1, false, 1);
       break;
-    case 128:
-      if (pack2) TQ_LAUNCH(128, 2, true);
-      else TQ_LAUNCH(128, 1, false);
+    case 128:  // pack2 exactly when spw == 2
+      if (pack2) TQ_LAUNCH(128, 2, true, 2);
+      else TQ_LAUNCH(128, 1, false, 1);
       break;
-    default:
-      if (qc) TQ_LAUNCH(256, 1, true);
-      else TQ_LAUNCH(256, 1, false);
+    default:  // spw == 2 only when ratio <= 4
+      if (spw == 2) TQ_LAUNCH(256, 1, true, 2);
+      else if (qc) TQ_LAUNCH(256, 1, true, 1);
+      else TQ_LAUNCH(256, 1, false, 1);
   }
 #undef TQ_LAUNCH
   hipError_t e = hipGetLastError();
