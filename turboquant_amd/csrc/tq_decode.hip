@@ -192,73 +192,76 @@ struct SoftmaxState {
   float m, mb, lsum;
 };
 
+// LDS byte address of dequant-table entry `byte k of w` for this lane.  The
+// table sits at LDS address 0 with LREP copies of each entry side by side
+// (entry e, copy r at dword e * LREP + r).  With 64 copies lane l reads
+// copy l, so a table read never has a bank conflict, and the address is one
+// byte permute: byte 0 = 4 l (lane4), byte 1 = the code byte.
+template <int LREP>
+__device__ __forceinline__ uint32_t lut_addr(uint32_t w, int k, uint32_t lane4) {
+  if constexpr (LREP == 64) {
+    return perm(w, lane4, 0x0c0c0000u | ((4u + (uint32_t)k) << 8));
+  } else {
+    static_assert(LREP == 1, "table copies: 1 or 64");
+    (void)lane4;
+    return ((w >> (8 * k)) & 0xffu) << 2;
+  }
+}
+
+// Eight table reads and one wait (inline assembly: the compiler does not
+// see them, so it adds no conservative wait for the copies in flight).
+__device__ __forceinline__ void lut_read8(const uint32_t* a, uint32_t* x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile(
+      "ds_read_b32 %0, %8\n\t"
+      "ds_read_b32 %1, %9\n\t"
+      "ds_read_b32 %2, %10\n\t"
+      "ds_read_b32 %3, %11\n\t"
+      "ds_read_b32 %4, %12\n\t"
+      "ds_read_b32 %5, %13\n\t"
+      "ds_read_b32 %6, %14\n\t"
+      "ds_read_b32 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]),
+        "=&v"(x[6]), "=&v"(x[7])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]),
+        "v"(a[7])
+      : "memory");
+#else
+  for (int i = 0; i < 8; i++) x[i] = a[i];
+#endif
+}
+
 // Scores of one tile, S[t = 4*q4 + r][h = l%16]: the K codes this lane
 // holds (token l%16, dims of quarter q4; byte j of dword c = dims 8c + 2j,
-// 8c + 2j + 1) are dequantized through the 256-entry LDS table at LDS
-// address 0 (code byte -> two fp16 codebook values, one ds_read each), then
-// the QK MFMAs run against q' (pre-scaled to log2 units) as fp16 hi + lo
-// parts.  QC: the B operand holds the hi parts in columns 0..7 and the lo
-// parts in columns 8..15 (GQA ratio <= 8), one MFMA per K block, and the
-// two halves are added across lanes n and n+8 (both end up with the sum);
-// otherwise qb/ql are separate hi/lo operands, two MFMAs per K block.
-#ifndef TQ_K_LUT
-#define TQ_K_LUT 1
-#endif
-constexpr bool kKLut = TQ_K_LUT;
-template <int PD, bool QC>
+// 8c + 2j + 1) are dequantized through the LDS table (code byte -> fp16
+// values of its high and low nibble, one ds_read each), then the QK MFMAs
+// run against q' (pre-scaled to log2 units) as fp16 hi + lo parts.  QC: the
+// B operand holds the hi parts in columns 0..7 and the lo parts in columns
+// 8..15 (GQA ratio <= 8), one MFMA per K block, and the two halves are added
+// across lanes n and n+8 (both end up with the sum); otherwise qb/ql are
+// separate hi/lo operands, two MFMAs per K block.
+template <int PD, bool QC, int LREP>
 __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_t* qb,
-                                                const half8_t* ql) {
+                                                const half8_t* ql, uint32_t lane4) {
   constexpr int KD = PD / 32;
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (!kKLut) {
-#pragma unroll
-    for (int c = 0; c < KD; c++) {
-      uint32_t x[4];
-      dq8(kw[c], x);
-      const half8_t kv8 = as_half8(x[0], x[1], x[2], x[3]);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qb[c], acc, 0, 0, 0);
-      if constexpr (!QC) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, ql[c], acc, 0, 0, 0);
-    }
-  } else {
 #pragma unroll
   for (int c = 0; c < KD; c += 2) {
     // two K blocks per batch of 8 table reads and one wait
-    uint32_t x[2][4];
-#if defined(__HIP_DEVICE_COMPILE__)
-    uint32_t a[2][4];
+    uint32_t a[8], x[8];
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) a[4 * u + j] = lut_addr<LREP>(kw[c + u], j, lane4);
+    lut_read8(a, x);
 #pragma unroll
     for (int u = 0; u < 2; u++) {
-      a[u][0] = (kw[c + u] & 0xffu) << 2;
-      a[u][1] = ((kw[c + u] >> 8) & 0xffu) << 2;
-      a[u][2] = ((kw[c + u] >> 16) & 0xffu) << 2;
-      a[u][3] = (kw[c + u] >> 24) << 2;
-    }
-    asm volatile(
-        "ds_read_b32 %0, %8\n\t"
-        "ds_read_b32 %1, %9\n\t"
-        "ds_read_b32 %2, %10\n\t"
-        "ds_read_b32 %3, %11\n\t"
-        "ds_read_b32 %4, %12\n\t"
-        "ds_read_b32 %5, %13\n\t"
-        "ds_read_b32 %6, %14\n\t"
-        "ds_read_b32 %7, %15\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(x[0][0]), "=&v"(x[0][1]), "=&v"(x[0][2]), "=&v"(x[0][3]), "=&v"(x[1][0]),
-          "=&v"(x[1][1]), "=&v"(x[1][2]), "=&v"(x[1][3])
-        : "v"(a[0][0]), "v"(a[0][1]), "v"(a[0][2]), "v"(a[0][3]), "v"(a[1][0]), "v"(a[1][1]),
-          "v"(a[1][2]), "v"(a[1][3])
-        : "memory");
-#else
-    for (int u = 0; u < 2; u++) x[u][0] = x[u][1] = x[u][2] = x[u][3] = kw[c + u];
-#endif
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const half8_t kv8 = as_half8(x[u][0], x[u][1], x[u][2], x[u][3]);
+      const half8_t kv8 = as_half8(x[4 * u], x[4 * u + 1], x[4 * u + 2], x[4 * u + 3]);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, qb[c + u], acc, 0, 0, 0);
       if constexpr (!QC)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, ql[c + u], acc, 0, 0, 0);
     }
-  }
   }
   if constexpr (QC) {
 #pragma unroll
@@ -267,44 +270,52 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
   return acc;
 }
 
-// This lane's V codes of one tile, transposed so that dword k holds code
-// byte k of tokens 4*q4 + 0..3 (byte j = token j).  v[j] = the lane's V
-// code bytes [n*VB, (n+1)*VB) of token 4*q4 + j.
-template <int PD>
-__device__ __forceinline__ void tile_v_columns(const uint32_t (*v)[(PD / 32) >= 4 ? PD / 128 : 1],
-                                               uint32_t* e) {
-  if constexpr (PD == 64) {
-    const uint32_t p01 = v[0][0] | (v[1][0] << 16);
-    const uint32_t p23 = v[2][0] | (v[3][0] << 16);
-    e[0] = perm(p23, p01, 0x06040200u);
-    e[1] = perm(p23, p01, 0x07050301u);
-  } else if constexpr (PD == 128) {
-    transpose4(v[0][0], v[1][0], v[2][0], v[3][0], e);
-  } else {
-    transpose4(v[0][0], v[1][0], v[2][0], v[3][0], e);
-    transpose4(v[0][1], v[1][1], v[2][1], v[3][1], e + 4);
-  }
-}
-
 // O[h][dim slot] += V^T P^T over the 32 tokens of one step with
 // v_mfma_f32_16x16x32_f16: the 8 k-values of a lane are tokens 4*q4 + 0..3
 // of tile 0 followed by the same tokens of tile 1, in both A (dequantized
 // V^T, row = dim slot) and B (probabilities p * nv, column = head).
-template <int PD>
+// v0 / v1[j] = this lane's V code bytes of token 4*q4 + j of tile 0 / 1
+// (dword w = bytes 4w..4w+3 of the lane's PD/32).  The A operand needs
+// fp16 pairs of one dim over two tokens, so the table index of a pair is
+// built from the two tokens' nibbles of one code byte (first token's
+// nibble high): the table maps it to (value of the first, value of the
+// second).  Byte k's low nibbles give dim slot 2k + 1, its high nibbles
+// dim slot 2k.
+template <int PD, int LREP>
 __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD / 128 : 1],
                                         const uint32_t (*v1)[(PD / 32) >= 4 ? PD / 128 : 1],
-                                        half8_t p, SoftmaxState<PD>& st) {
+                                        half8_t p, SoftmaxState<PD>& st, uint32_t lane4) {
   constexpr int VB = PD / 32;
-  uint32_t e0[VB], e1[VB];
-  tile_v_columns<PD>(v0, e0);
-  tile_v_columns<PD>(v1, e1);
+  constexpr int VW = VB >= 4 ? VB / 4 : 1;
+  // ix[T][pair][nibble][w]: pair 0 = tokens 0, 1; pair 1 = tokens 2, 3;
+  // nibble 0 = low nibbles, 1 = high nibbles
+  uint32_t ix[2][2][2][VW];
+#pragma unroll
+  for (int T = 0; T < 2; T++) {
+    const uint32_t (*v)[VW] = T ? v1 : v0;
+#pragma unroll
+    for (int pr = 0; pr < 2; pr++)
+#pragma unroll
+      for (int w = 0; w < VW; w++) {
+        const uint32_t a = v[2 * pr][w], b = v[2 * pr + 1][w];
+        ix[T][pr][0][w] = ((a << 4) & 0xf0f0f0f0u) | (b & 0x0f0f0f0fu);
+        ix[T][pr][1][w] = (a & 0xf0f0f0f0u) | ((b >> 4) & 0x0f0f0f0fu);
+      }
+  }
 #pragma unroll
   for (int k = 0; k < VB; k++) {
-    uint32_t x0[4], x1[4];
-    dq8(e0[k], x0);
-    dq8(e1[k], x1);
-    const half8_t lo8 = as_half8(x0[0], x0[1], x1[0], x1[1]);
-    const half8_t hi8 = as_half8(x0[2], x0[3], x1[2], x1[3]);
+    const int w = k / 4, j = k % 4;
+    uint32_t a[8], x[8];
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+      for (int T = 0; T < 2; T++)
+#pragma unroll
+        for (int pr = 0; pr < 2; pr++)
+          a[4 * nb + 2 * T + pr] = lut_addr<LREP>(ix[T][pr][nb][w], j, lane4);
+    lut_read8(a, x);
+    const half8_t lo8 = as_half8(x[0], x[1], x[2], x[3]);
+    const half8_t hi8 = as_half8(x[4], x[5], x[6], x[7]);
     st.O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo8, p, st.O[2 * k + 1], 0, 0, 0);
     st.O[2 * k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi8, p, st.O[2 * k], 0, 0, 0);
   }
@@ -498,10 +509,13 @@ void decode_partials_kernel(DecodeParams p) {
   constexpr int EBS = Geo::EBS;
   constexpr int WB = 2 * kTile * EBS;  // bytes of one staged step (V, two tiles) of one wave
   constexpr int MG = Geo::MAXG;
-  // LDS: the K dequant table first (LDS address 0, which the table reads
-  // rely on), then two staging slots
+  // dequant table copies: one per lane when two splits share the workgroup
+  // (which then has the CU's LDS to itself), else one
+  constexpr int LREP = SPW == 2 ? 64 : 1;
+  // LDS: the dequant table first (LDS address 0, which the table reads rely
+  // on), then two staging slots
   struct __attribute__((aligned(16))) Lds {
-    uint32_t klut[256];
+    uint32_t klut[256 * LREP];
     uint8_t slot0[SPW * MG * WB];
     uint8_t slot1[SPW * MG * WB];
   };
@@ -510,18 +524,28 @@ void decode_partials_kernel(DecodeParams p) {
   uint8_t* const slot1 = sm.slot1;
   constexpr int NSLOT = 2;  // LDS slots per wave: one step computed, one in flight
 
-  // K dequant table: code byte -> fp16 values of dims 2j (low half) and
-  // 2j + 1 (high half), built with the same table arithmetic as dq8
-  for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+  // dequant table: byte e -> fp16 values of its high nibble (low half) and
+  // its low nibble (high half), built with the same table arithmetic as
+  // dq8; LREP copies of each entry side by side (written 4 at a time)
+  auto lut_val = [](int e) {
     uint32_t x[4];
-    dq8((uint32_t)i * 0x01010101u, x);
-    sm.klut[i] = (x[2] & 0xffffu) | (x[0] << 16);
+    dq8((uint32_t)e * 0x01010101u, x);
+    return (x[2] & 0xffffu) | (x[0] << 16);
+  };
+  if constexpr (LREP == 1) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) sm.klut[i] = lut_val(i);
+  } else {
+    for (int i = threadIdx.x; i < 64 * LREP; i += blockDim.x) {
+      const uint32_t val = lut_val(i / (LREP / 4));
+      *reinterpret_cast<u32x4*>(&sm.klut[4 * i]) = u32x4{val, val, val, val};
+    }
   }
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int q4 = lane >> 4, n = lane & 15;
+  const uint32_t lane4 = (uint32_t)lane * 4;  // this lane's table copy (byte offset)
   // SPW splits per workgroup: waves [sub * G, (sub + 1) * G) serve split
   // SPW * (split group) + sub, so one workgroup fills a CU's wave slots and
   // its waves start together
@@ -727,9 +751,9 @@ void decode_partials_kernel(DecodeParams p) {
       // scores of both tiles (scheduling barriers keep the two tiles'
       // dequant temporaries from being live at the same time)
       float4_t acc[2];
-      acc[0] = tile_scores<PD, QC>(kr.k[0], qb, ql);
+      acc[0] = tile_scores<PD, QC, LREP>(kr.k[0], qb, ql, lane4);
       __builtin_amdgcn_sched_barrier(0);
-      acc[1] = tile_scores<PD, QC>(kr.k[1], qb, ql);
+      acc[1] = tile_scores<PD, QC, LREP>(kr.k[1], qb, ql, lane4);
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t nk01[2] = {kr.nk[0], kr.nk[1]};
       if (knext) stageK(k + 1, kr);
@@ -775,7 +799,7 @@ void decode_partials_kernel(DecodeParams p) {
       } else {
         p8 = half8_t{pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
       }
-      step_pv<PD>(d.v[0], d.v[1], p8, st);
+      step_pv<PD, LREP>(d.v[0], d.v[1], p8, st, lane4);
     };
     // one step: wait until its copy has landed (`later` = copy instructions
     // issued after it, which may stay in flight), read this wave's region of
@@ -833,10 +857,8 @@ void decode_partials_kernel(DecodeParams p) {
     // fp16 hi + lo parts (q' = hi + lo to ~22 bits, so the scores keep
     // fp32-level accuracy even for heavy-tailed keys), in the MFMA B layout.
     const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
-    // element order of the K operand: dims 8c + e for the table, dq8's
-    // {1,3,5,7,0,2,4,6} otherwise
-    constexpr int ord[8] = {kKLut ? 0 : 1, kKLut ? 1 : 3, kKLut ? 2 : 5, kKLut ? 3 : 7,
-                            kKLut ? 4 : 0, kKLut ? 5 : 2, kKLut ? 6 : 4, kKLut ? 7 : 6};
+    // element order of the K operand: the table yields dims 8c + e in order
+    constexpr int ord[8] = {0, 1, 2, 3, 4, 5, 6, 7};
     const int hq = QC ? (n & 7) : n;  // q head of this lane's B column
     if (qreg) {
       // in registers: butterflies h = 1, 2, 4 inside a lane, h >= 8 between

@@ -79,7 +79,8 @@ def decode_workgroup_shape(num_qo_heads: int, num_kv_heads: int, pd: int) -> tup
             G = g
             break
     spw = decode_splits_per_workgroup(num_qo_heads, num_kv_heads, pd)
-    by_lds = LDS_BYTES_PER_CU // (2 * slot_bytes * spw + 1024)  # + the K table
+    table = 65536 if spw == 2 else 1024  # the dequant table (64 copies with two splits)
+    by_lds = LDS_BYTES_PER_CU // (2 * slot_bytes * spw + table)
     by_waves = 4 * _WAVES_PER_SIMD.get(pd, 2) // (G * spw)
     return G, spw * max(1, min(by_lds, by_waves))
 
