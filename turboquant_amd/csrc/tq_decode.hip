@@ -34,6 +34,8 @@
 //    only moves when a tile exceeds it by more than 2^3), bounding p <= 8.
 #include <math.h>
 
+#include <type_traits>
+
 #include "tq_common.h"
 
 namespace tq {
@@ -119,7 +121,6 @@ struct DecodeParams {
   float qk_scale;     // sm_scale * log2(e) / (sqrt(pd) * kCbScale)
   float inv_sqrt_pd;  // 1/sqrt(pd)
   float pv_scale;     // 1/(sqrt(pd) * kCbScale)
-  int share0;         // two splits per workgroup: 256ths of the pair's tokens for the first
 };
 
 // 4x4 byte transpose: E_k byte j = byte k of D_j
@@ -157,6 +158,25 @@ __device__ __forceinline__ float xor32_sum(float x) {
 __device__ __forceinline__ float ror8(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
 }
+// value of lane l ^ m (m = 1, 2, 4, 8 without LDS: DPP quad_perm, row
+// half-mirror then quad reversal, row rotate by 8)
+__device__ __forceinline__ float xor_lane(float x, int m) {
+  const int v = __float_as_int(x);
+  switch (m) {
+    case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, false));
+    case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, false));
+    case 4: {
+      const int t = __builtin_amdgcn_mov_dpp(v, 0x141, 0xf, 0xf, false);
+      return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x1B, 0xf, 0xf, false));
+    }
+    case 8: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x128, 0xf, 0xf, false));
+    default: return __shfl_xor(x, m);
+  }
+}
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)ptr;
+}
 // fp16 value held in the low / high half of a dword
 __device__ __forceinline__ float lo_half(uint32_t v) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu));
@@ -165,18 +185,12 @@ __device__ __forceinline__ float hi_half(uint32_t v) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
 }
 
-// Static LDS geometry of the decode kernel.  A step is two 16-token tiles;
-// one staged step holds, for the workgroup's G heads, the K slab then the V
-// slab, each [32 token rows][G*ebs bytes].  ROW = the largest G*ebs a
-// workgroup may take for this head size.
+// Per-lane register geometry of the decode math for padded head size PD.
 template <int PD>
 struct DecodeGeom {
   static constexpr int KD = PD / 32;  // K dwords per lane per tile = QK MFMA pairs
   static constexpr int VB = PD / 32;  // V bytes per lane per token
   static constexpr int NO = PD / 16;  // PV MFMAs = output dim slots per lane
-  static constexpr int EBS = PD == 64 ? 48 : (PD == 128 ? 80 : 144);  // entry bytes
-  static constexpr int MAXG = PD == 256 ? 4 : 8;          // kv heads (waves) per workgroup
-  static constexpr int WAVE_STEP = 2 * 2 * kTile * EBS;  // one wave's staged step (K+V, 2 tiles)
 };
 
 // Online-softmax state of one wave.  O[i][r] = unnormalised o[h = l%16][dim
@@ -192,43 +206,45 @@ struct SoftmaxState {
   float m, mb, lsum;
 };
 
-// LDS byte address of dequant-table entry `byte k of w` for this lane.  The
-// table sits at LDS address 0 with LREP copies of each entry side by side
-// (entry e, copy r at dword e * LREP + r).  With 64 copies lane l reads
-// copy l, so a table read never has a bank conflict, and the address is one
-// byte permute: byte 0 = 4 l (lane4), byte 1 = the code byte.
-template <int LREP>
-__device__ __forceinline__ uint32_t lut_addr(uint32_t w, int k, uint32_t lane4) {
-  if constexpr (LREP == 64) {
-    return perm(w, lane4, 0x0c0c0000u | ((4u + (uint32_t)k) << 8));
-  } else {
-    static_assert(LREP == 1, "table copies: 1 or 64");
-    (void)lane4;
-    return ((w >> (8 * k)) & 0xffu) << 2;
+// LDS byte address of dequant-table entry `byte k of w`.  The table (256
+// dwords: entry e = fp16 values of the high and low nibble of code byte e)
+// sits at LDS address 0, so the address is the byte times 4: one SDWA shift
+// with a byte-select source operand.
+__device__ __forceinline__ uint32_t lut_addr(uint32_t w, int k) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  if (k == 0) {
+    uint32_t a;
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+        "src1_sel:BYTE_0"
+        : "=v"(a)
+        : "v"(2u), "v"(w));
+    return a;
   }
+#endif
+  return ((w >> (8 * k)) & 0xffu) << 2;
 }
 
-// Eight table reads and one wait (inline assembly: the compiler does not
-// see them, so it adds no conservative wait for the copies in flight).
-__device__ __forceinline__ void lut_read8(const uint32_t* a, uint32_t* x) {
+// Eight table reads in place (each address register receives its entry)
+// and one wait; inline assembly, so the compiler adds no conservative wait
+// for the copies in flight.
+__device__ __forceinline__ void lut_read8(uint32_t* a) {
 #if defined(__HIP_DEVICE_COMPILE__)
   asm volatile(
-      "ds_read_b32 %0, %8\n\t"
-      "ds_read_b32 %1, %9\n\t"
-      "ds_read_b32 %2, %10\n\t"
-      "ds_read_b32 %3, %11\n\t"
-      "ds_read_b32 %4, %12\n\t"
-      "ds_read_b32 %5, %13\n\t"
-      "ds_read_b32 %6, %14\n\t"
-      "ds_read_b32 %7, %15\n\t"
+      "ds_read_b32 %0, %0\n\t"
+      "ds_read_b32 %1, %1\n\t"
+      "ds_read_b32 %2, %2\n\t"
+      "ds_read_b32 %3, %3\n\t"
+      "ds_read_b32 %4, %4\n\t"
+      "ds_read_b32 %5, %5\n\t"
+      "ds_read_b32 %6, %6\n\t"
+      "ds_read_b32 %7, %7\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]),
-        "=&v"(x[6]), "=&v"(x[7])
-      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]),
-        "v"(a[7])
+      : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]),
+        "+v"(a[7])
+      :
       : "memory");
 #else
-  for (int i = 0; i < 8; i++) x[i] = a[i];
+  (void)a;
 #endif
 }
 
@@ -241,20 +257,20 @@ __device__ __forceinline__ void lut_read8(const uint32_t* a, uint32_t* x) {
 // 8..15 (GQA ratio <= 8), one MFMA per K block, and the two halves are added
 // across lanes n and n+8 (both end up with the sum); otherwise qb/ql are
 // separate hi/lo operands, two MFMAs per K block.
-template <int PD, bool QC, int LREP>
+template <int PD, bool QC>
 __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_t* qb,
-                                                const half8_t* ql, uint32_t lane4) {
+                                                const half8_t* ql) {
   constexpr int KD = PD / 32;
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < KD; c += 2) {
     // two K blocks per batch of 8 table reads and one wait
-    uint32_t a[8], x[8];
+    uint32_t x[8];
 #pragma unroll
     for (int u = 0; u < 2; u++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) a[4 * u + j] = lut_addr<LREP>(kw[c + u], j, lane4);
-    lut_read8(a, x);
+      for (int j = 0; j < 4; j++) x[4 * u + j] = lut_addr(kw[c + u], j);
+    lut_read8(x);
 #pragma unroll
     for (int u = 0; u < 2; u++) {
       const half8_t kv8 = as_half8(x[4 * u], x[4 * u + 1], x[4 * u + 2], x[4 * u + 3]);
@@ -281,10 +297,10 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
 // nibble high): the table maps it to (value of the first, value of the
 // second).  Byte k's low nibbles give dim slot 2k + 1, its high nibbles
 // dim slot 2k.
-template <int PD, int LREP>
+template <int PD>
 __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD / 128 : 1],
                                         const uint32_t (*v1)[(PD / 32) >= 4 ? PD / 128 : 1],
-                                        half8_t p, SoftmaxState<PD>& st, uint32_t lane4) {
+                                        half8_t p, SoftmaxState<PD>& st) {
   constexpr int VB = PD / 32;
   constexpr int VW = VB >= 4 ? VB / 4 : 1;
   // ix[T][pair][nibble][w]: pair 0 = tokens 0, 1; pair 1 = tokens 2, 3;
@@ -305,15 +321,14 @@ __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD
 #pragma unroll
   for (int k = 0; k < VB; k++) {
     const int w = k / 4, j = k % 4;
-    uint32_t a[8], x[8];
+    uint32_t x[8];
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
 #pragma unroll
       for (int T = 0; T < 2; T++)
 #pragma unroll
-        for (int pr = 0; pr < 2; pr++)
-          a[4 * nb + 2 * T + pr] = lut_addr<LREP>(ix[T][pr][nb][w], j, lane4);
-    lut_read8(a, x);
+        for (int pr = 0; pr < 2; pr++) x[4 * nb + 2 * T + pr] = lut_addr(ix[T][pr][nb][w], j);
+    lut_read8(x);
     const half8_t lo8 = as_half8(x[0], x[1], x[2], x[3]);
     const half8_t hi8 = as_half8(x[4], x[5], x[6], x[7]);
     st.O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo8, p, st.O[2 * k + 1], 0, 0, 0);
@@ -321,14 +336,14 @@ __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD
   }
 }
 
-// This wave's share of one staged step, read from LDS into registers.
+// This wave's share of one step (two tiles), read from LDS into registers.
 template <int PD>
 struct StepData {
   static constexpr int KD = PD / 32;
   static constexpr int VW = (PD / 32) >= 4 ? PD / 128 : 1;
-  uint32_t k[2][KD];     // K codes of tiles 0 and 1
-  uint32_t v[2][4][VW];  // V codes of tiles 0 and 1, tokens 4*q4 + j
-  uint32_t nkv[2];       // norms (K low, V high) of the packed tokens, per group
+  uint32_t k[2][KD];     // K codes of tiles 0 and 1: token l%16, dims of quarter q4
+  uint32_t v[2][4][VW];  // V codes of tiles 0 and 1, tokens 4*q4 + j, bytes of slot l%16
+  uint32_t nkv[2];       // norms (K low half, V high half) of the packed tokens, per group
 };
 
 // s_waitcnt immediate that waits until at most n vector-memory operations
@@ -338,97 +353,160 @@ __host__ __device__ constexpr int vmcnt_imm(int n) {
   return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14);
 }
 
-// LDS byte address of a pointer into __shared__ memory.
-__device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)ptr;
-}
+// LDS staging geometry of one workgroup (G kv heads of one split).  A tile
+// slot holds the 16 tokens of one tile for the workgroup's heads: the K slab
+// region, then the V slab region, each SLAB bytes.  A region holds the 16
+// token rows of CPT 16-byte chunks (G entries of EBS bytes) as copied from
+// the cache, at a row stride of RCH chunks: CPT rounded up to an odd count,
+// so that the 16 rows of one chunk column, and rows t and t + 4, fall into
+// distinct bank groups (the pad chunk of a row receives a second copy of
+// the row's last chunk).  NI 1 KB copies fill one region (the last may
+// spill past the rows into the region's slack).  Three slots form the ring.
+#ifndef TQ_RING_SLOTS
+#define TQ_RING_SLOTS 3
+#endif
+constexpr int kRingSlots = TQ_RING_SLOTS;  // tile slots in the LDS ring
 
-// This wave's V share of one staged step, read from LDS into registers, as
-// inline assembly ending in lgkmcnt(0): the compiler does not see these LDS
-// reads, so it adds no conservative wait for the copies in flight; the
-// caller waits for exactly the copy it reads (vmcnt).  Staged layout of one
-// step of one wave: regions V t0, V t1 of TB bytes; a region holds the 16
-// tokens' codes (CB bytes each, token-major) followed by their 16-byte entry
-// tails (norm copies and pad).  nv[T] = V norm bits of token
-// 4*q4 + (lane & 3) of tile T (PACK 2 reads only the lane's own tile).
-template <int PD, int PACK>
-__device__ __forceinline__ void read_v_asm(const uint8_t* wslot, uint32_t voff, uint32_t noff,
-                                           StepData<PD>& d, uint32_t* nv) {
-#if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the kernel stubs
-  constexpr int CB = PD / 2;            // code bytes per token
-  constexpr int TB = kTile * (CB + 16);  // one staged tile
-  constexpr int N1 = PACK == 2 ? 0 : TB;  // second norm: tile 1 (PACK 1 only)
-  const uint32_t base = lds_addr(wslot);
-  const uint32_t va = base + voff;
-  const uint32_t na = base + noff;
+template <int PD, int G>
+struct RingGeom {
+  static constexpr int EBS = PD == 64 ? 48 : (PD == 128 ? 80 : 144);  // entry bytes
+  static constexpr int ECH = EBS / 16;                       // chunks per entry
+  static constexpr int CPT = G * ECH;                         // chunks per token row
+  static constexpr int RCH = CPT | 1;                         // row stride in chunks
+  static constexpr int ROWB = RCH * 16;                       // row stride in bytes
+  static constexpr int NI = (kTile * RCH + 63) / 64;          // copies per region
+  static constexpr int SLAB = NI * 1024;                      // LDS bytes per region
+  static constexpr int TS = 2 * SLAB;                         // LDS bytes per tile slot
+  static constexpr int NIT = 2 * NI;                          // copies per tile
+  static constexpr int NW_HI = (NIT + G - 1) / G;             // copies per tile, waves < NIT % G
+  static constexpr int NW_LO = NIT / G;                       // copies per tile, other waves
+  static constexpr int RING = kRingSlots * TS;
+  static constexpr int LDS = 1024 + RING;                     // table + ring
+};
+
+// This wave's K codes, V codes and norms of the step's two tiles, read from
+// the ring slots S0 (tile 0) and S1 (tile 1) into registers: inline assembly
+// ending in lgkmcnt(0) (the compiler does not see these LDS reads, so it
+// adds no wait for the copies in flight; the caller has waited for exactly
+// the copies it reads).  oK / oV / oN: per-lane offsets inside a region of
+// the K code chunk(s), the V code bytes of token 4*q4 (token 4*q4 + j is j
+// rows further), and the entry tail (first norm copy) of token
+// 4*q4 + (lane & 3); PACK 2 reads the norms
+// of the lane's packed tile only, at oN (which then already includes the
+// distance to that tile's slot from the lower of the two slots).
+template <int PD, int G, int PACK>
+__device__ __forceinline__ void read_step(const uint32_t* ka, uint32_t va, uint32_t vb,
+                                          uint32_t na, uint32_t nb, StepData<PD>& d) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  using RG = RingGeom<PD, G>;
+  constexpr int R = RG::ROWB;
+  constexpr int SL = RG::SLAB;
+  uint32_t n0 = 0, n1 = 0, n2 = 0, n3 = 0;
+// V codes of tokens 4*q4 + 0..3 of both tiles: rows R apart
+#define TQ_V8(OP)                                \
+  OP " %[a0], %[va]\n\t"                         \
+  OP " %[a1], %[va] offset:%[r1]\n\t"            \
+  OP " %[a2], %[va] offset:%[r2]\n\t"            \
+  OP " %[a3], %[va] offset:%[r3]\n\t"            \
+  OP " %[c0], %[vb]\n\t"                         \
+  OP " %[c1], %[vb] offset:%[r1]\n\t"            \
+  OP " %[c2], %[vb] offset:%[r2]\n\t"            \
+  OP " %[c3], %[vb] offset:%[r3]\n\t"
+#define TQ_VOUT                                                                          \
+  [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3), [c0] "=&v"(c0),        \
+  [c1] "=&v"(c1), [c2] "=&v"(c2), [c3] "=&v"(c3)
+#define TQ_VIN [va] "v"(va), [vb] "v"(vb), [r1] "i"(R), [r2] "i"(2 * R), [r3] "i"(3 * R)
+// norms: PACK 2 the lane's packed tile (K at na, V one region further); PACK 1
+// both tiles (K t0 at na, K t1 at nb, V t0, V t1 one region further)
+#define TQ_N2                                      \
+  "ds_read_u16 %[n0], %[na]\n\t"                   \
+  "ds_read_u16 %[n1], %[na] offset:%[sl]\n\t"
+#define TQ_N1                                      \
+  "ds_read_u16 %[n0], %[na]\n\t"                   \
+  "ds_read_u16 %[n1], %[nb]\n\t"                   \
+  "ds_read_u16 %[n2], %[na] offset:%[sl]\n\t"      \
+  "ds_read_u16 %[n3], %[nb] offset:%[sl]\n\t"
   if constexpr (PD == 128 || PD == 64) {
-    uint32_t v0, v1, v2, v3, v4, v5, v6, v7;
-    if constexpr (PD == 128) {
-      asm volatile(
-          "ds_read_b32 %0, %10\n\t"
-          "ds_read_b32 %1, %10 offset:%12\n\t"
-          "ds_read_b32 %2, %10 offset:%13\n\t"
-          "ds_read_b32 %3, %10 offset:%14\n\t"
-          "ds_read_b32 %4, %10 offset:%15\n\t"
-          "ds_read_b32 %5, %10 offset:%16\n\t"
-          "ds_read_b32 %6, %10 offset:%17\n\t"
-          "ds_read_b32 %7, %10 offset:%18\n\t"
-          "ds_read_u16 %8, %11\n\t"
-          "ds_read_u16 %9, %11 offset:%19\n\t"
-          "s_waitcnt lgkmcnt(0)"
-          : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6),
-            "=&v"(v7), "=&v"(nv[0]), "=&v"(nv[1])
-          : "v"(va), "v"(na), "i"(CB), "i"(2 * CB), "i"(3 * CB), "i"(TB), "i"(TB + CB),
-            "i"(TB + 2 * CB), "i"(TB + 3 * CB), "i"(N1)
-          : "memory");
+    typedef typename std::conditional<PD == 128, u32x4, u32x2>::type KT;
+    KT k0, k1;
+    uint32_t a0, a1, a2, a3, c0, c1, c2, c3;
+    if constexpr (PD == 128 && PACK == 2) {
+      asm volatile("ds_read_b128 %[k0], %[ka0]\n\t"
+                   "ds_read_b128 %[k1], %[ka1]\n\t"
+                   TQ_V8("ds_read_b32") TQ_N2 "s_waitcnt lgkmcnt(0)"
+                   : [k0] "=&v"(k0), [k1] "=&v"(k1), TQ_VOUT, [n0] "=&v"(n0), [n1] "=&v"(n1)
+                   : [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), TQ_VIN, [na] "v"(na), [sl] "i"(SL)
+                   : "memory");
+    } else if constexpr (PD == 128) {
+      asm volatile("ds_read_b128 %[k0], %[ka0]\n\t"
+                   "ds_read_b128 %[k1], %[ka1]\n\t"
+                   TQ_V8("ds_read_b32") TQ_N1 "s_waitcnt lgkmcnt(0)"
+                   : [k0] "=&v"(k0), [k1] "=&v"(k1), TQ_VOUT, [n0] "=&v"(n0), [n1] "=&v"(n1),
+                     [n2] "=&v"(n2), [n3] "=&v"(n3)
+                   : [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), TQ_VIN, [na] "v"(na), [nb] "v"(nb),
+                     [sl] "i"(SL)
+                   : "memory");
+    } else if constexpr (PACK == 2) {
+      asm volatile("ds_read_b64 %[k0], %[ka0]\n\t"
+                   "ds_read_b64 %[k1], %[ka1]\n\t"
+                   TQ_V8("ds_read_u16") TQ_N2 "s_waitcnt lgkmcnt(0)"
+                   : [k0] "=&v"(k0), [k1] "=&v"(k1), TQ_VOUT, [n0] "=&v"(n0), [n1] "=&v"(n1)
+                   : [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), TQ_VIN, [na] "v"(na), [sl] "i"(SL)
+                   : "memory");
     } else {
-      asm volatile(
-          "ds_read_u16 %0, %10\n\t"
-          "ds_read_u16 %1, %10 offset:%12\n\t"
-          "ds_read_u16 %2, %10 offset:%13\n\t"
-          "ds_read_u16 %3, %10 offset:%14\n\t"
-          "ds_read_u16 %4, %10 offset:%15\n\t"
-          "ds_read_u16 %5, %10 offset:%16\n\t"
-          "ds_read_u16 %6, %10 offset:%17\n\t"
-          "ds_read_u16 %7, %10 offset:%18\n\t"
-          "ds_read_u16 %8, %11\n\t"
-          "ds_read_u16 %9, %11 offset:%19\n\t"
-          "s_waitcnt lgkmcnt(0)"
-          : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6),
-            "=&v"(v7), "=&v"(nv[0]), "=&v"(nv[1])
-          : "v"(va), "v"(na), "i"(CB), "i"(2 * CB), "i"(3 * CB), "i"(TB), "i"(TB + CB),
-            "i"(TB + 2 * CB), "i"(TB + 3 * CB), "i"(N1)
-          : "memory");
+      asm volatile("ds_read_b64 %[k0], %[ka0]\n\t"
+                   "ds_read_b64 %[k1], %[ka1]\n\t"
+                   TQ_V8("ds_read_u16") TQ_N1 "s_waitcnt lgkmcnt(0)"
+                   : [k0] "=&v"(k0), [k1] "=&v"(k1), TQ_VOUT, [n0] "=&v"(n0), [n1] "=&v"(n1),
+                     [n2] "=&v"(n2), [n3] "=&v"(n3)
+                   : [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), TQ_VIN, [na] "v"(na), [nb] "v"(nb),
+                     [sl] "i"(SL)
+                   : "memory");
     }
-    d.v[0][0][0] = v0; d.v[0][1][0] = v1; d.v[0][2][0] = v2; d.v[0][3][0] = v3;
-    d.v[1][0][0] = v4; d.v[1][1][0] = v5; d.v[1][2][0] = v6; d.v[1][3][0] = v7;
+#pragma unroll
+    for (int i = 0; i < PD / 32; i++) {
+      d.k[0][i] = k0[i];
+      d.k[1][i] = k1[i];
+    }
+    d.v[0][0][0] = a0; d.v[0][1][0] = a1; d.v[0][2][0] = a2; d.v[0][3][0] = a3;
+    d.v[1][0][0] = c0; d.v[1][1][0] = c1; d.v[1][2][0] = c2; d.v[1][3][0] = c3;
   } else {
-    u32x2 v0, v1, v2, v3, v4, v5, v6, v7;
-    asm volatile(
-        "ds_read_b64 %0, %10\n\t"
-        "ds_read_b64 %1, %10 offset:%12\n\t"
-        "ds_read_b64 %2, %10 offset:%13\n\t"
-        "ds_read_b64 %3, %10 offset:%14\n\t"
-        "ds_read_b64 %4, %10 offset:%15\n\t"
-        "ds_read_b64 %5, %10 offset:%16\n\t"
-        "ds_read_b64 %6, %10 offset:%17\n\t"
-        "ds_read_b64 %7, %10 offset:%18\n\t"
-        "ds_read_u16 %8, %11\n\t"
-        "ds_read_u16 %9, %11 offset:%19\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6),
-          "=&v"(v7), "=&v"(nv[0]), "=&v"(nv[1])
-        : "v"(va), "v"(na), "i"(CB), "i"(2 * CB), "i"(3 * CB), "i"(TB), "i"(TB + CB),
-          "i"(TB + 2 * CB), "i"(TB + 3 * CB), "i"(N1)
-        : "memory");
-    const u32x2 vv[8] = {v0, v1, v2, v3, v4, v5, v6, v7};
+    static_assert(PD == 256 && PACK == 1, "head size 256 keeps one tile per score set");
+    u32x4 k0, k1, k2, k3;
+    u32x2 a0, a1, a2, a3, c0, c1, c2, c3;
+    asm volatile("ds_read_b128 %[k0], %[ka0]\n\t"
+                 "ds_read_b128 %[k1], %[ka0] offset:16\n\t"
+                 "ds_read_b128 %[k2], %[ka1]\n\t"
+                 "ds_read_b128 %[k3], %[ka1] offset:16\n\t"
+                 TQ_V8("ds_read_b64") TQ_N1 "s_waitcnt lgkmcnt(0)"
+                 : [k0] "=&v"(k0), [k1] "=&v"(k1), [k2] "=&v"(k2), [k3] "=&v"(k3), TQ_VOUT,
+                   [n0] "=&v"(n0), [n1] "=&v"(n1), [n2] "=&v"(n2), [n3] "=&v"(n3)
+                 : [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), TQ_VIN, [na] "v"(na), [nb] "v"(nb),
+                   [sl] "i"(SL)
+                 : "memory");
 #pragma unroll
-    for (int T = 0; T < 2; T++)
+    for (int i = 0; i < 4; i++) {
+      d.k[0][i] = k0[i];
+      d.k[0][4 + i] = k1[i];
+      d.k[1][i] = k2[i];
+      d.k[1][4 + i] = k3[i];
+    }
+    const u32x2 vva[4] = {a0, a1, a2, a3}, vvc[4] = {c0, c1, c2, c3};
 #pragma unroll
-      for (int j = 0; j < 4; j++) { d.v[T][j][0] = vv[4 * T + j][0]; d.v[T][j][1] = vv[4 * T + j][1]; }
+    for (int j = 0; j < 4; j++) {
+      d.v[0][j][0] = vva[j][0]; d.v[0][j][1] = vva[j][1];
+      d.v[1][j][0] = vvc[j][0]; d.v[1][j][1] = vvc[j][1];
+    }
   }
+#undef TQ_V8
+#undef TQ_VOUT
+#undef TQ_VIN
+#undef TQ_N2
+#undef TQ_N1
+  d.nkv[0] = n0 | (PACK == 2 ? n1 : n2) << 16;
+  d.nkv[1] = n1 | n3 << 16;  // PACK 1: tile 1
 #else
-  (void)wslot; (void)voff; (void)noff; (void)d; nv[0] = nv[1] = 0;
+  (void)ka; (void)va; (void)vb; (void)na; (void)nb; (void)d;
 #endif
 }
 
@@ -493,75 +571,56 @@ __device__ __forceinline__ half4_t shl8(half4_t v) {
 }
 
 // Split-KV partials.  Workgroup = (sequence b, split s, group hg of G kv
-// heads), one wave per kv head.  Each wave streams its own head's cache
-// entries of each step (two 16-token tiles, K and V) into its own region of
-// NSLOT LDS slots with direct-to-LDS 16-byte loads, NSLOT - 1 steps ahead of
-// the step it computes.  Waves never wait on each other after the q setup:
-// the slots are distinct LDS arrays, so the compiler ties every LDS read to
-// the one copy it depends on and leaves the later copies in flight.
-template <int PD, int PACK, bool QC, int SPW>
-__global__ __launch_bounds__(64 * DecodeGeom<PD>::MAXG * SPW)
+// heads), one wave per kv head.  The workgroup streams its heads' cache rows
+// tile by tile (16 tokens x G entries of both slabs) into a ring of three
+// LDS tile slots with direct-to-LDS 16-byte copies: every copy instruction
+// reads 1 KB of consecutive row bytes, so each cache line is requested once
+// by one instruction.  A step is two tiles.  Per step: wait for this wave's
+// copies of the step's tiles (the next tile's copies stay in flight),
+// barrier, each wave reads its own head's codes and norms into registers,
+// barrier, then the copies of the two tiles after the next are issued into
+// the two slots just read, and the math runs while three tiles are in
+// flight.  The step loop is unrolled by three so every slot address is an
+// immediate.
+template <int PD, int G, int PACK, bool QC>
+__global__ __launch_bounds__(64 * G)
 __attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : (PACK == 1 ? 3 : 4))))
 void decode_partials_kernel(DecodeParams p) {
-  using Geo = DecodeGeom<PD>;
-  constexpr int KD = Geo::KD;
-  constexpr int NO = Geo::NO;
-  constexpr int EBS = Geo::EBS;
-  constexpr int WB = 2 * kTile * EBS;  // bytes of one staged step (V, two tiles) of one wave
-  constexpr int MG = Geo::MAXG;
-  // dequant table copies: one per lane when two splits share the workgroup
-  // (which then has the CU's LDS to itself), else one
-  constexpr int LREP = SPW == 2 ? 64 : 1;
-  // LDS: the dequant table first (LDS address 0, which the table reads rely
-  // on), then two staging slots
+  using RG = RingGeom<PD, G>;
+  constexpr int KD = PD / 32;
+  constexpr int NO = PD / 16;
+  constexpr int EBS = RG::EBS;
+  constexpr int ECH = RG::ECH;
+  constexpr int CPT = RG::CPT;
+  constexpr int NI = RG::NI;
+  // LDS: the dequant table at address 0 (the table reads rely on it), then
+  // the ring of three tile slots
   struct __attribute__((aligned(16))) Lds {
-    uint32_t klut[256 * LREP];
-    uint8_t slot0[SPW * MG * WB];
-    uint8_t slot1[SPW * MG * WB];
+    uint32_t klut[256];
+    uint8_t ring[RG::RING];
   };
   __shared__ Lds sm;
-  uint8_t* const slot0 = sm.slot0;
-  uint8_t* const slot1 = sm.slot1;
-  constexpr int NSLOT = 2;  // LDS slots per wave: one step computed, one in flight
 
   // dequant table: byte e -> fp16 values of its high nibble (low half) and
-  // its low nibble (high half), built with the same table arithmetic as
-  // dq8; LREP copies of each entry side by side (written 4 at a time)
-  auto lut_val = [](int e) {
+  // its low nibble (high half), built with the same table arithmetic as dq8
+  for (int i = threadIdx.x; i < 256; i += 64 * G) {
     uint32_t x[4];
-    dq8((uint32_t)e * 0x01010101u, x);
-    return (x[2] & 0xffffu) | (x[0] << 16);
-  };
-  if constexpr (LREP == 1) {
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) sm.klut[i] = lut_val(i);
-  } else {
-    for (int i = threadIdx.x; i < 64 * LREP; i += blockDim.x) {
-      const uint32_t val = lut_val(i / (LREP / 4));
-      *reinterpret_cast<u32x4*>(&sm.klut[4 * i]) = u32x4{val, val, val, val};
-    }
+    dq8((uint32_t)i * 0x01010101u, x);
+    sm.klut[i] = (x[2] & 0xffffu) | (x[0] << 16);
   }
-  __syncthreads();
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int q4 = lane >> 4, n = lane & 15;
-  const uint32_t lane4 = (uint32_t)lane * 4;  // this lane's table copy (byte offset)
-  // SPW splits per workgroup: waves [sub * G, (sub + 1) * G) serve split
-  // SPW * (split group) + sub, so one workgroup fills a CU's wave slots and
-  // its waves start together
-  const int G = p.G;
-  const int sub = SPW == 1 ? 0 : w / G;  // uniform
-  const int hw = w - sub * G;            // kv head within the group
-  const int nsg = (p.S + SPW - 1) / SPW;  // split groups per sequence
   int bid = blockIdx.x;
   const int hg = bid % p.HG;
   bid /= p.HG;
-  const int s = (bid % nsg) * SPW + sub;
-  const int b = bid / nsg;
-  const int kvh = hg * G + hw;
+  const int s = bid % p.S;
+  const int b = bid / p.S;
+  const int kvh = hg * G + w;
   const int ratio = p.ratio;
 
-  half8_t qb[KD], ql[QC ? 1 : KD];  // q' operands, filled once the first copy is in flight
+  half8_t qb[KD], ql[QC ? 1 : KD];  // q' operands
 
   // s * q of this wave's heads, loaded first so that its latency overlaps
   // the page-table loads and the first copies: in load j < NQL, lane l holds
@@ -605,165 +664,306 @@ void decode_partials_kernel(DecodeParams p) {
   st.lsum = 0.f;
   const float lpv = -__log2f(p.pv_scale);
 
-  const int L = s < p.S ? p.seq_lens[b] : 0;  // a split past the last one is empty
-  int c0 = s * p.cs;
-  int c1 = min(c0 + p.cs, L);
-  if (SPW == 2 && s - sub + 1 < p.S) {
-    // The two wave groups of a workgroup do not progress at the same rate
-    // (issue arbitration favours the older waves), so the token range of the
-    // split pair is divided unevenly: the first group takes share0/256 of it,
-    // rounded to whole 32-token steps.  Any partition merges to the same
-    // attention.
-    const int base = (s - sub) * p.cs;
-    const int end = min(base + 2 * p.cs, p.seq_lens[b]);
-    const int mid = min(end, base + ((max(end - base, 0) * p.share0 / 256 + 31) & ~31));
-    c0 = sub ? mid : base;
-    c1 = sub ? end : mid;
-  }
+  const int L = p.seq_lens[b];
+  const int c0 = s * p.cs;
+  const int c1 = min(c0 + p.cs, L);
+  // the table is written (an LDS-only wait, so the q loads stay in flight)
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
+  __builtin_amdgcn_s_barrier();
   if (c0 < c1) {  // uniform over the workgroup
     constexpr int STEP = 2 * kTile;
-    constexpr int TB = kTile * EBS;                // one tile of one slab (LDS)
     const int step0 = c0 / STEP, step1 = (c1 - 1) / STEP;
     const int tpp = p.block_size / kTile;  // tiles per page
     const int64_t tokstride = (int64_t)p.Hkv * EBS;
     const int ip = p.indptr[b];
-    const uint8_t* kslab = p.ks + (int64_t)kvh * EBS;
-    const uint8_t* vslab = p.vs + (int64_t)kvh * EBS;
+    const uint8_t* const kslab = p.ks;
+    const uint8_t* const vslab = p.vs;
     const int tile_last = (c1 - 1) / kTile;
-    const int rec = (int)((kTile - 1) * tokstride + EBS);
+    const int tile_end = 2 * step1 + 1;  // last tile any step of this split reads
+    const int rec = (int)(kTile * tokstride);
 
-    // tile offsets: lane i holds the byte offset inside a slab of tile
+    // Tile window: lane i holds the byte offset inside a slab of tile
     // wtile + i (64 bit, as lo/hi halves) and tmask bit i says whether that
-    // tile is present (within the split and on a page inside the cache).  A
-    // window covers 32 steps (64 tiles) and is rebuilt between windows with
-    // the copies drained.
+    // tile is present (within the split and on a page inside the cache).
+    // When the copies reach the end of the window it slides by 32 tiles;
+    // the page ids of the next 32 tiles are loaded one slide ahead (npg,
+    // lanes 32..63).
     uint32_t tlo = 0, thi = 0;
     uint64_t tmask = 0;
     int wtile = 2 * step0;
+    int npg = -1;
+    auto page_of = [&](int t) -> int {
+      return t <= tile_last ? p.indices[ip + t / tpp] : -1;
+    };
+    auto set_tile = [&](int t, int pg, bool& ok, uint32_t& lo, uint32_t& hi) {
+      ok = pg >= 0 && pg < p.num_blocks;
+      const int64_t off =
+          ok ? ((int64_t)pg * p.block_size + (t % tpp) * kTile) * tokstride : 0;
+      lo = (uint32_t)off;
+      hi = (uint32_t)((uint64_t)off >> 32);
+    };
     auto tile_ok = [&](int t) -> bool { return (tmask >> ((t - wtile) & 63)) & 1; };
-    auto tile_base = [&](const uint8_t* slab, int t) -> const uint8_t* {
-      const int j = (t - wtile) & 63;
-      const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)tlo, j);
-      const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)thi, j);
-      return slab + (int64_t)((hi << 32) | lo);
+    auto prefetch_pages = [&]() {
+      npg = lane >= 32 ? page_of(wtile + 32 + lane) : -1;
+    };
+    {
+      bool ok;
+      set_tile(wtile + lane, page_of(wtile + lane), ok, tlo, thi);
+      tmask = __ballot(ok);
+      prefetch_pages();
+    }
+    auto slide = [&]() {
+      bool ok;
+      uint32_t lo, hi;
+      set_tile(wtile + 32 + lane, npg, ok, lo, hi);
+      const uint32_t lo_up = (uint32_t)__shfl((int)tlo, (lane + 32) & 63);
+      const uint32_t hi_up = (uint32_t)__shfl((int)thi, (lane + 32) & 63);
+      tlo = lane < 32 ? lo_up : lo;
+      thi = lane < 32 ? hi_up : hi;
+      tmask = (tmask >> 32) | (__ballot(ok && lane >= 32) & 0xffffffff00000000ull);
+      wtile += 32;
+      prefetch_pages();
     };
 
-    // Copies of one region (16 tokens of one slab): the codes as CI
-    // instructions of CW bytes per lane (lane-contiguous in LDS, token-major
-    // with CB bytes per token), then the 16-byte entry tails (norm copies and
-    // pad) as one 4-byte-per-lane instruction.  Every lane of every copy is
-    // active, so the copies never sit under divergent control flow.
-    constexpr int CB = PD / 2;                // code bytes per token
-    constexpr int CW = PD == 64 ? 4 : 16;     // bytes per lane of a code copy
-    constexpr int CI = kTile * CB / (64 * CW);  // code copies per region
-    constexpr int CPT = CB / CW;              // lanes per token in a code copy
-    uint32_t goff[CI];
+    // Copies: copy j of a tile (j < NI: K region, else V region; jj = j mod
+    // NI) fills LDS chunks jj*64 + lane of the region.  Wave w issues copies
+    // j = w, w + G, ...  Per-lane source offsets inside the tile's slab
+    // (rows of tokstride bytes, the group's entries at hg*G*EBS):
+    constexpr int NWMAX = RG::NW_HI;
+    const int nmine = RG::NW_LO + (w < RG::NIT % G ? 1 : 0);  // uniform
+    uint32_t goff[NWMAX];
 #pragma unroll
-    for (int i = 0; i < CI; i++) {
-      const int c = 64 * i + lane;
-      goff[i] = (uint32_t)((c / CPT) * tokstride + (c % CPT) * CW);
+    for (int i = 0; i < NWMAX; i++) {
+      const int jj = (w + G * i) % NI;
+      int pos = jj * 64 + lane;
+      if (pos >= kTile * RG::RCH) pos = kTile * RG::RCH - 1;  // spill lanes reload a chunk
+      const int t = pos / RG::RCH;
+      const int c = min(pos % RG::RCH, CPT - 1);  // the pad chunk reloads the row's last
+      goff[i] = (uint32_t)(t * tokstride + (int64_t)hg * G * EBS + c * 16);
     }
-    const uint32_t gtail = (uint32_t)((lane >> 2) * tokstride + CB + (lane & 3) * 4);
-    // K of one step straight into registers: lane (token n, quarter q4)
-    // loads its PD/8 code bytes of each tile and the K norm of token
-    // 4*q4 + (lane & 3) of each tile (absent tiles read as zeros)
-    struct KRegs {
-      uint32_t k[2][KD];
-      uint32_t nk[2];
+    auto issue = [&](int t, int slot) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the LDS-copy builtin has no host form
+      const int jw = (t - wtile) & 63;
+      const uint64_t off = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)thi, jw) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)tlo, jw);
+      const int nrec = tile_ok(t) ? rec : 0;
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(kslab + off), (short)0, nrec, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rv =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(vslab + off), (short)0, nrec, 0x00020000);
+      uint8_t* const dst = sm.ring + slot * RG::TS;
+#pragma unroll
+      for (int i = 0; i < NWMAX; i++) {
+        if (i < nmine) {
+          const int j = w + G * i;
+          const bool isv = j >= NI;
+          const int jj = isv ? j - NI : j;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(isv ? rv : rk,
+                                                   (void*)(dst + (isv ? RG::SLAB : 0) + jj * 1024),
+                                                   16, goff[i], 0, 0, 0);
+        }
+      }
+#else
+      (void)t;
+      (void)slot;
+#endif
     };
-    const uint32_t kcoff = (uint32_t)(n * tokstride + q4 * (PD / 8));
-    const uint32_t knoff = (uint32_t)((4 * q4 + (lane & 3)) * tokstride + CB);
-    // K codes and norms of step k into kr (absent tiles read as zeros)
-    // The loads are inline assembly: the compiler does not track them, so it
-    // inserts no wait of its own; run() waits for them explicitly (vmcnt) and
-    // then passes the registers through an empty asm so that no use can move
-    // above that wait.
-    auto stageK = [&](int k, KRegs& kr) {
-#if defined(__HIP_DEVICE_COMPILE__)
+    // wait until this wave's copies of every tile but the last `later`
+    // issued ones have landed
+    auto wait_copies = [&](int later) {
+      const int nw = (RG::NW_HI != RG::NW_LO && w < RG::NIT % G) ? RG::NW_HI : RG::NW_LO;
+      switch (later * nw) {
+        case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(1)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2)); break;
+        case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3)); break;
+        case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4)); break;
+        case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5)); break;
+        case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6)); break;
+        case 7: __builtin_amdgcn_s_waitcnt(vmcnt_imm(7)); break;
+        case 8: __builtin_amdgcn_s_waitcnt(vmcnt_imm(8)); break;
+        case 9: __builtin_amdgcn_s_waitcnt(vmcnt_imm(9)); break;
+        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(10)); break;
+      }
+    };
+
+    // per-lane LDS read offsets inside a region (see read_step)
+    constexpr int ROWB = RG::ROWB;
+    const int hb = w * ECH;  // first chunk of this wave's entry in a row
+    uint32_t oK[1];
+    if constexpr (PD == 128) {
+      oK[0] = n * ROWB + (hb + q4) * 16;
+    } else if constexpr (PD == 64) {
+      oK[0] = n * ROWB + (hb + q4 / 2) * 16 + (q4 & 1) * 8;
+    } else {
+      oK[0] = n * ROWB + (hb + 2 * q4) * 16;  // two chunks: the second 16 bytes further
+    }
+    constexpr int VBY = PD / 32;  // V code bytes per lane per token
+    const uint32_t oV = 4 * q4 * ROWB + hb * 16 + n * VBY;
+    const int slotw = 16 / PACK;   // lanes per packed tile
+    const int ptile = n / slotw;   // tile of this lane's packed scores
+    const int head = n % slotw;    // head of this lane's packed scores
+    const uint32_t oN = (4 * q4 + (lane & 3)) * ROWB + (hb + PD / 32) * 16;
+
+    // (q' in registers: the tiles whose slots do not hold the q' scratch)
+    const int qfirst = G * 4096 <= (kRingSlots - 1) * RG::TS ? 1 : 0;  // tiles before the q setup
+    const uint32_t qscr = (uint32_t)(qfirst * RG::TS);  // q' scratch: ring offset
+    if (qreg && qfirst) issue(2 * step0, 0);
+
+    // ---- q' = FWHT(s*q)/sqrt(pd), scaled to log2 units and split into
+    // fp16 hi + lo parts (q' = hi + lo to ~22 bits, so the scores keep
+    // fp32-level accuracy even for heavy-tailed keys), in the MFMA B layout.
+    const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
+    const int hq = QC ? (n & 7) : n;  // q head of this lane's B column
+    if (qreg) {
+      // in registers: butterflies h = 1, 2, 4 inside a lane, h >= 8 between
+      // lanes l and l ^ (h / 8) (DPP, one fma with a lane sign each)
+      if (p.signs) {
 #pragma unroll
-      for (int T = 0; T < 2; T++) {
-        const uint64_t base = (uint64_t)tile_base(kslab, 2 * k + T);
-        const u32x4 rk = {(uint32_t)base, (uint32_t)(base >> 32) & 0xffffu,
-                          (uint32_t)(tile_ok(2 * k + T) ? rec : 0), 0x00020000u};
-        if constexpr (PD == 64) {
-          u32x2 v;
-          asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen"
-                       : "=v"(v)
-                       : "v"(kcoff), "s"(rk)
-                       : "memory");
-          kr.k[T][0] = v[0];
-          kr.k[T][1] = v[1];
-        } else {
+        for (int j = 0; j < NQL; j++) {
 #pragma unroll
-          for (int h = 0; h < KD / 4; h++) {
-            u32x4 v;
-            asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
-                         : "=v"(v)
-                         : "v"(kcoff), "s"(rk), "i"(16 * h)
-                         : "memory");
+          for (int h = 1; h < 8; h <<= 1)
 #pragma unroll
-            for (int i = 0; i < 4; i++) kr.k[T][4 * h + i] = v[i];
+            for (int k = 0; k < 8; k++)
+              if (!(k & h)) {
+                const float a = qx[j][k], c = qx[j][k + h];
+                qx[j][k] = a + c;
+                qx[j][k + h] = a - c;
+              }
+#pragma unroll
+          for (int h = 8; h < PD; h <<= 1) {
+            const float sgn = (lane & (h / 8)) ? -1.0f : 1.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) qx[j][k] = fmaf(sgn, qx[j][k], xor_lane(qx[j][k], h / 8));
           }
         }
-        asm volatile("buffer_load_ushort %0, %1, %2, 0 offen"
-                     : "=v"(kr.nk[T])
-                     : "v"(knoff), "s"(rk)
+      }
+      // fp16 hi / lo parts through a per-wave LDS scratch (hi then lo, 1024
+      // elements each) to the B layout: column n takes head hq, dims
+      // q4 * PD/4 + 8c + 0..7.  Inline assembly: the scratch shares the ring
+      // with the copy in flight, and the compiler would otherwise wait for it.
+#if defined(__HIP_DEVICE_COMPILE__)
+      const uint32_t qsb = lds_addr(sm.ring) + qscr + (uint32_t)w * 4096u;
+#pragma unroll
+      for (int j = 0; j < NQL; j++) {
+        u32x4 vh, vl;
+#pragma unroll
+        for (int wd = 0; wd < 4; wd++) {
+          const float x0 = qx[j][2 * wd] * qsc, x1 = qx[j][2 * wd + 1] * qsc;
+          const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+          const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+          vh[wd] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+          vl[wd] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        }
+        const uint32_t a = qsb + (uint32_t)(512 * j + 8 * lane) * 2u;
+        asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:2048"
+                     :
+                     : "v"(a), "v"(vh), "v"(vl)
                      : "memory");
       }
-#else
-      (void)k;
-      (void)kr;
-#endif
-    };
-    // V copies of step k into this wave's region of one slot (regions V t0,
-    // V t1 of TB bytes each)
-    auto stage = [&](int k, uint8_t* dst) {
-#if defined(__HIP_DEVICE_COMPILE__)  // the LDS-copy builtin has no host form
 #pragma unroll
-      for (int r = 0; r < 2; r++) {
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)tile_base(vslab, 2 * k + r), (short)0, tile_ok(2 * k + r) ? rec : 0,
-            0x00020000);
-#pragma unroll
-        for (int i = 0; i < CI; i++)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void*)(dst + r * TB + i * 64 * CW), CW,
-                                                   goff[i], 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void*)(dst + r * TB + kTile * CB), 4, gtail,
-                                                 0, 0, 0);
+      for (int c = 0; c < KD; c++) {
+        const uint32_t e = (uint32_t)(hq * PD + q4 * (PD / 4) + 8 * c);
+        u32x4 vh, vl;
+        if constexpr (QC) {
+          asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                       : "=v"(vh)
+                       : "v"(qsb + e * 2u + (n < 8 ? 0u : 2048u))
+                       : "memory");
+          if (hq >= ratio) vh = u32x4{0u, 0u, 0u, 0u};
+          qb[c] = __builtin_bit_cast(half8_t, vh);
+        } else {
+          asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:2048\n\t"
+                       "s_waitcnt lgkmcnt(0)"
+                       : "=&v"(vh), "=&v"(vl)
+                       : "v"(qsb + e * 2u)
+                       : "memory");
+          if (hq >= ratio) vh = vl = u32x4{0u, 0u, 0u, 0u};
+          qb[c] = __builtin_bit_cast(half8_t, vh);
+          ql[c] = __builtin_bit_cast(half8_t, vl);
+        }
       }
-#else
-      (void)k;
-      (void)dst;
 #endif
-    };
+      // once every wave has read its scratch, the rest of the first tiles go
+      // out (their copies overwrite the scratch)
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < kRingSlots; r++)
+        if (r >= qfirst && 2 * step0 + r <= tile_end) issue(2 * step0 + r, r);
+    } else {
+      // ---- q' = FWHT(s*q)/sqrt(pd) for this wave's `ratio` heads on an LDS
+      // scratch in the ring (each wave its own region; the launcher keeps
+      // G * ratio * PD floats within the ring), before any copy is issued.
+      // LDS operations of one wave complete in order, so a wave barrier
+      // orders the butterfly stages.
+      float* const qs = reinterpret_cast<float*>(sm.ring) + (size_t)w * ratio * PD;
+      auto qsync = [&]() {
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+      };
+      for (int i = lane; i < ratio * PD; i += 64) {
+        const int r = i / PD, d = i - r * PD;
+        float x = (float)p.q[b * p.q_sb + (int64_t)(kvh * ratio + r) * p.q_sh + d];
+        if (p.signs) x = x * p.signs[d];
+        qs[i] = x;
+      }
+      qsync();
+      if (p.signs) {
+        for (int h = 1; h < PD; h <<= 1) {
+          for (int i = lane; i < ratio * PD / 2; i += 64) {
+            const int r = i / (PD / 2), j = i - r * (PD / 2);
+            const int lo = r * PD + (j / h) * 2 * h + (j % h);
+            const float a = qs[lo], c = qs[lo + h];
+            qs[lo] = a + c;
+            qs[lo + h] = a - c;
+          }
+          qsync();
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < KD; c++) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int d = q4 * (PD / 4) + 8 * c + e;
+          const float x = (hq < ratio) ? qs[hq * PD + d] * qsc : 0.0f;
+          const _Float16 hi = (_Float16)x;
+          const _Float16 lo = (_Float16)(x - (float)hi);
+          if constexpr (QC) {
+            qb[c][e] = n < 8 ? hi : lo;
+          } else {
+            qb[c][e] = hi;
+            ql[c][e] = lo;
+          }
+        }
+      }
+      __syncthreads();  // every wave is done with its scratch: the copies may start
+#pragma unroll
+      for (int r = 0; r < kRingSlots; r++)
+        if (2 * step0 + r <= tile_end) issue(2 * step0 + r, r);
+    }
 
-    // per-lane LDS offsets inside a staged step of this wave
-    const uint32_t voff = (uint32_t)((4 * q4) * CB + n * (PD / 32));
-    const int slot = 16 / PACK;    // lanes per packed tile slot
-    const int ptile = n / slot;    // tile of this lane's packed scores
-    const int head = n % slot;     // head of this lane's packed scores
-    const uint32_t noff = (uint32_t)(ptile * TB + kTile * CB + (4 * q4 + (lane & 3)) * 16);
-
-    // math of one step; `kr` holds this step's K on entry and receives the
-    // next step's K (loads issued once the scores no longer need it)
-    auto compute = [&](int k, const StepData<PD>& d, KRegs& kr, bool knext) {
+    // math of one step (tiles 2k, 2k + 1) from the registers in d
+    auto compute = [&](int k, const StepData<PD>& d) {
       const bool okT[2] = {tile_ok(2 * k), tile_ok(2 * k + 1)};
       // scores of both tiles (scheduling barriers keep the two tiles'
       // dequant temporaries from being live at the same time)
       float4_t acc[2];
-      acc[0] = tile_scores<PD, QC, LREP>(kr.k[0], qb, ql, lane4);
+      acc[0] = tile_scores<PD, QC>(d.k[0], qb, ql);
       __builtin_amdgcn_sched_barrier(0);
-      acc[1] = tile_scores<PD, QC, LREP>(kr.k[1], qb, ql, lane4);
+      acc[1] = tile_scores<PD, QC>(d.k[1], qb, ql);
       __builtin_amdgcn_sched_barrier(0);
-      const uint32_t nk01[2] = {kr.nk[0], kr.nk[1]};
-      if (knext) stageK(k + 1, kr);
       constexpr int NV = 4 * (2 / PACK);  // score values per lane
       float sc[NV], nk[NV], nv[NV];
       bool valid[NV];
 #pragma unroll
       for (int g = 0; g < 2 / PACK; g++) {
-        const uint32_t nkv =
-            (PACK == 2 ? (ptile ? nk01[1] : nk01[0]) : nk01[g]) | (d.nkv[g] << 16);
+        const uint32_t nkv = d.nkv[g];
         const uint32_t nr[4] = {quad_bcast<0>(nkv), quad_bcast<1>(nkv), quad_bcast<2>(nkv),
                                 quad_bcast<3>(nkv)};
 #pragma unroll
@@ -799,253 +999,38 @@ void decode_partials_kernel(DecodeParams p) {
       } else {
         p8 = half8_t{pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
       }
-      step_pv<PD, LREP>(d.v[0], d.v[1], p8, st, lane4);
+      step_pv<PD>(d.v[0], d.v[1], p8, st);
     };
-    // one step: wait until its copy has landed (`later` = copy instructions
-    // issued after it, which may stay in flight), read this wave's region of
-    // `src` into registers, then the math
-    // V copies per step; the K loads of step k + 1 are issued inside step
-    // k, so when step k + 1 runs only the V copies of step k + 2 may still be
-    // in flight behind it
-    constexpr int NVCOPY = 2 * (CI + 1);
-    KRegs kr;
-    auto run = [&](int k, const uint8_t* src, int wend) {
-      if (k + 1 <= wend) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NVCOPY));
-      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-#if defined(__HIP_DEVICE_COMPILE__)
-#pragma unroll
-      for (int T = 0; T < 2; T++) {
-#pragma unroll
-        for (int i = 0; i < KD; i++) asm volatile("" : "+v"(kr.k[T][i]));
-        asm volatile("" : "+v"(kr.nk[T]));
-      }
-#endif
+
+    // one step: tiles 2k, 2k + 1 in ring slots s0, s1
+    auto run = [&](int k, int s0, int s1) {
+      // the tiles after 2k + 1 already issued may stay in flight
+      wait_copies(max(0, min(kRingSlots - 2, tile_end - (2 * k + 1))));
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();  // every wave's copies of tiles 2k, 2k + 1 have landed
+      __builtin_amdgcn_sched_barrier(0);
       StepData<PD> d;
-      uint32_t nv[2];
-      read_v_asm<PD, PACK>(src, voff, noff, d, nv);
-      d.nkv[0] = nv[0];
-      d.nkv[1] = nv[1];
-      compute(k, d, kr, k + 1 <= wend);
-    };
-
-    const size_t wofs = (size_t)w * WB;
-    auto open_window = [&](int wstep) {
-      wtile = 2 * wstep;
-      const int t = wtile + lane;
-      const int pg = (t <= tile_last) ? p.indices[ip + t / tpp] : -1;
-      const bool ok = pg >= 0 && pg < p.num_blocks;
-      const int64_t off = ok ? ((int64_t)pg * p.block_size + (t % tpp) * kTile) * tokstride : 0;
-      tlo = (uint32_t)off;
-      thi = (uint32_t)((uint64_t)off >> 32);
-      tmask = __ballot(ok);
-    };
-    // steps wstep + 2j live in slot A (slot1), wstep + 2j + 1 in slot B
-    // (slot0); one step is in flight while the other is computed.  The first
-    // copy is issued before the q setup, which may use slot0 as scratch.
-    uint8_t* const sA = slot1 + wofs;
-    uint8_t* const sB = slot0 + wofs;
-    open_window(step0);
-    stage(step0, sA);
-    stageK(step0, kr);
-    // with q' formed in registers, slot0 is free: the second copy goes too
-    bool staged1 = false;
-    if (qreg && step0 + 1 <= min(step0 + 31, step1)) {
-      stage(step0 + 1, sB);
-      staged1 = true;
-    }
-    // ---- q' = FWHT(s*q)/sqrt(pd), scaled to log2 units and split into
-    // fp16 hi + lo parts (q' = hi + lo to ~22 bits, so the scores keep
-    // fp32-level accuracy even for heavy-tailed keys), in the MFMA B layout.
-    const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
-    // element order of the K operand: the table yields dims 8c + e in order
-    constexpr int ord[8] = {0, 1, 2, 3, 4, 5, 6, 7};
-    const int hq = QC ? (n & 7) : n;  // q head of this lane's B column
-    if (qreg) {
-      // in registers: butterflies h = 1, 2, 4 inside a lane, h >= 8 between
-      // lanes l and l ^ (h / 8); no LDS, no barrier
-      if (p.signs) {
-#pragma unroll
-        for (int j = 0; j < NQL; j++) {
-#pragma unroll
-          for (int h = 1; h < 8; h <<= 1)
-#pragma unroll
-            for (int k = 0; k < 8; k++)
-              if (!(k & h)) {
-                const float a = qx[j][k], c = qx[j][k + h];
-                qx[j][k] = a + c;
-                qx[j][k + h] = a - c;
-              }
-#pragma unroll
-          for (int h = 8; h < PD; h <<= 1) {
-            const bool upper = lane & (h / 8);
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-              const float pt = __shfl_xor(qx[j][k], h / 8);
-              qx[j][k] = upper ? pt - qx[j][k] : qx[j][k] + pt;
-            }
-          }
-        }
-      }
-      // packed fp16 hi / lo pairs in MFMA element order
-      uint32_t ph[NQL][4], pl[NQL][4];
-#pragma unroll
-      for (int j = 0; j < NQL; j++)
-#pragma unroll
-        for (int wd = 0; wd < 4; wd++) {
-          const float x0 = qx[j][ord[2 * wd]] * qsc, x1 = qx[j][ord[2 * wd + 1]] * qsc;
-          const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
-          const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
-          ph[j][wd] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
-                      ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-          pl[j][wd] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
-                      ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-        }
-      // B operand: column n takes head hq, dims q4 * PD/4 + 8c + ord[.] from
-      // the lane holding those 8 elements
-#pragma unroll
-      for (int c = 0; c < KD; c++) {
-        const int e = hq * PD + q4 * (PD / 4) + 8 * c;
-        const int src = (e % 512) / 8, jsel = e / 512;
-        u32x4 vh, vl;
-#pragma unroll
-        for (int wd = 0; wd < 4; wd++) {
-          uint32_t h = (uint32_t)__shfl((int)ph[0][wd], src);
-          uint32_t l = (uint32_t)__shfl((int)pl[0][wd], src);
-#pragma unroll
-          for (int j = 1; j < NQL; j++) {
-            const uint32_t hj = (uint32_t)__shfl((int)ph[j][wd], src);
-            const uint32_t lj = (uint32_t)__shfl((int)pl[j][wd], src);
-            h = jsel == j ? hj : h;
-            l = jsel == j ? lj : l;
-          }
-          if (hq >= ratio) h = l = 0u;
-          vh[wd] = h;
-          vl[wd] = l;
-        }
-        if constexpr (QC) {
-          qb[c] = __builtin_bit_cast(half8_t, n < 8 ? vh : vl);
-        } else {
-          qb[c] = __builtin_bit_cast(half8_t, vh);
-          ql[c] = __builtin_bit_cast(half8_t, vl);
-        }
-      }
-    } else {
-      // ---- q' = FWHT(s*q)/sqrt(pd) for this wave's `ratio` heads, on an LDS
-      // scratch in slot0.  When it fits, the scratch is this wave's own region
-      // of slot0: only this wave touches it and LDS operations of one wave
-      // complete in order, so no workgroup barrier is needed.  Otherwise the
-      // waves' scratches span slot0 and the workgroup synchronises.
-      const bool qlocal = ratio * PD * 4 <= WB;  // uniform
-      auto qsync = [&]() {
-        if (qlocal) {
-          __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-          __builtin_amdgcn_wave_barrier();
-        } else {
-          __syncthreads();
-        }
-      };
-      float* const qs =
-          reinterpret_cast<float*>(slot0 + (qlocal ? wofs : (size_t)w * ratio * PD * 4));
-      for (int i = lane; i < ratio * PD; i += 64) {
-        const int r = i / PD, d = i - r * PD;
-        float x = (float)p.q[b * p.q_sb + (int64_t)(kvh * ratio + r) * p.q_sh + d];
-        if (p.signs) x = x * p.signs[d];
-        qs[i] = x;
-      }
-      qsync();
-      if (p.signs) {
-        for (int h = 1; h < PD; h <<= 1) {
-          for (int i = lane; i < ratio * PD / 2; i += 64) {
-            const int r = i / (PD / 2), j = i - r * (PD / 2);
-            const int lo = r * PD + (j / h) * 2 * h + (j % h);
-            const float a = qs[lo], c = qs[lo + h];
-            qs[lo] = a + c;
-            qs[lo + h] = a - c;
-          }
-          qsync();
-        }
-      }
-      // q' (pre-scaled to log2 units) split into fp16 high and low parts
-      // (q' = hi + lo to ~22 bits), so the scores keep fp32-level accuracy
-      // even for heavy-tailed keys.
       {
-#pragma unroll
-        for (int c = 0; c < KD; c++) {
-#pragma unroll
-          for (int e = 0; e < 8; e++) {
-            const int d = q4 * (PD / 4) + 8 * c + ord[e];
-            const float x = (hq < ratio) ? qs[hq * PD + d] * qsc : 0.0f;
-            const _Float16 hi = (_Float16)x;
-            const _Float16 lo = (_Float16)(x - (float)hi);
-            if constexpr (QC) {
-              qb[c][e] = n < 8 ? hi : lo;
-            } else {
-              qb[c][e] = hi;
-              ql[c][e] = lo;
-            }
-          }
-        }
+        const uint32_t b0 = 1024 + s0 * RG::TS, b1 = 1024 + s1 * RG::TS;  // K regions
+        const uint32_t ka[2] = {oK[0] + b0, oK[0] + b1};
+        const uint32_t na = oN + (PACK == 2 && ptile ? b1 : b0);
+        read_step<PD, G, PACK>(ka, oV + b0 + RG::SLAB, oV + b1 + RG::SLAB, na, oN + b1, d);
       }
-      // the scratch is overwritten by the copies into slot0 below
-      if (qlocal) {
-#if defined(__HIP_DEVICE_COMPILE__)
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#endif
-      } else {
-        __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();  // every wave has read the two slots
+      __builtin_amdgcn_sched_barrier(0);
+      // the next copies go into the two slots just read
+      if (2 * k + kRingSlots <= tile_end) {
+        if (2 * k + kRingSlots + 1 >= wtile + 64) slide();
+        issue(2 * k + kRingSlots, s0);
+        if (2 * k + kRingSlots + 1 <= tile_end) issue(2 * k + kRingSlots + 1, s1);
       }
-    }
-
-    for (int wstep = step0;;) {
-      const int wend = min(wstep + 31, step1);
-      if (wstep + 1 <= wend && !staged1) stage(wstep + 1, sB);
-      staged1 = false;
-      for (int k = wstep; k <= wend; k += NSLOT) {
-        run(k, sA, wend);
-        if (k + NSLOT <= wend) stage(k + NSLOT, sA);
-        if (k + 1 > wend) break;
-        run(k + 1, sB, wend);
-        if (k + 1 + NSLOT <= wend) stage(k + 1 + NSLOT, sB);
-      }
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // drain before the next window's page ids
-      wstep += 32;
-      if (wstep > step1) break;
-      open_window(wstep);
-      stage(wstep, sA);
-      stageK(wstep, kr);
-    }
-  }
-
-  // ---- two splits per workgroup: the second group hands its state to the
-  // first through LDS (the staging slots are drained), the first merges it
-  // and writes one partial for the pair; the second split's row is marked
-  // empty.  Any partition of the tokens merges to the same attention.
-  if constexpr (SPW == 2) {
-    constexpr int NF = 4 * NO + 2;  // floats of state per lane
-    float* const xs = reinterpret_cast<float*>(slot0) + (size_t)hw * 64 * NF;
-    __syncthreads();  // every wave is past its last LDS read
-    if (sub == 1) {
-#pragma unroll
-      for (int i = 0; i < NO; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) xs[(4 * i + r) * 64 + lane] = st.O[i][r];
-      xs[4 * NO * 64 + lane] = st.mb;
-      xs[(4 * NO + 1) * 64 + lane] = st.lsum;
-    }
-    __syncthreads();
-    if (sub == 0) {
-      const float mb1 = xs[4 * NO * 64 + lane];
-      const float l1 = xs[(4 * NO + 1) * 64 + lane];
-      const float mm = fmaxf(st.mb, mb1);
-      const float a0 = st.mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.mb - mm);
-      const float a1 = mb1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb1 - mm);
-#pragma unroll
-      for (int i = 0; i < NO; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-          st.O[i][r] = a0 * st.O[i][r] + a1 * xs[(4 * i + r) * 64 + lane];
-      st.lsum = a0 * st.lsum + a1 * l1;
-      st.mb = mm;
+      compute(k, d);
+    };
+    for (int k = step0, s0 = 0, s1 = 1; k <= step1; k++) {
+      run(k, s0, s1);
+      s0 = s0 + 2 >= kRingSlots ? s0 + 2 - kRingSlots : s0 + 2;  // tile t sits in slot
+      s1 = s1 + 2 >= kRingSlots ? s1 + 2 - kRingSlots : s1 + 2;  // (t - 2 step0) mod slots
     }
   }
 
@@ -1054,10 +1039,7 @@ void decode_partials_kernel(DecodeParams p) {
   if constexpr (PACK == 2) lt = lt + __int_as_float(__builtin_amdgcn_mov_dpp(
                                          __float_as_int(lt), 0x128, 0xf, 0xf, false));
   lt = xor32_sum(xor16_sum(lt));
-  if (SPW == 2 && sub == 1) {
-    if (n < ratio && q4 == 0 && s < p.S)
-      p.plse[((int64_t)b * p.S + s) * p.Hq + kvh * ratio + n] = -INFINITY;
-  } else if (n < ratio && s < p.S) {
+  if (n < ratio) {
     // o = pv_scale * O / lsum' (p' = p * pv_scale in both O and lsum')
     const float inv = lt > 0.f ? p.pv_scale / lt : 0.0f;
     const int64_t orow = ((int64_t)b * p.S + s) * p.Hq + kvh * ratio + n;
@@ -1197,12 +1179,25 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   }
 }
 
-// Splits one partials workgroup serves: two (one 16-wave workgroup per CU)
-// when q' is formed in registers (ratio * pd <= 1024) and pd >= 128, which
-// keeps the workgroup free of barriers; head size 64 keeps three 8-wave
-// workgroups per CU instead.  The pair's state is merged into the first
-// split's row and the second row is marked empty.
-int splits_per_workgroup(int ratio, int pd) { return (ratio * pd <= 1024 && pd >= 128) ? 2 : 1; }
+// LDS bytes of a partials workgroup of g kv heads (mirrors RingGeom).
+int ring_lds_bytes(int pd, int g) {
+  const int ech = (pd == 64 ? 48 : (pd == 128 ? 80 : 144)) / 16;
+  const int rch = (g * ech) | 1;
+  const int ni = (kTile * rch + 63) / 64;
+  return 1024 + kRingSlots * 2 * ni * 1024;
+}
+
+// Heads (waves) per partials workgroup: the largest of 8, 4, 2, 1 (at most 4
+// for head size 256) that divides num_kv_heads and, when q' is formed in LDS
+// (ratio * pd > 1024), whose q scratch fits the ring.
+int decode_group_size(int pd, int hkv, int ratio) {
+  const int maxg = pd == 256 ? 4 : 8;
+  for (int g = maxg; g >= 1; g >>= 1)
+    if (hkv % g == 0 &&
+        (ratio * pd <= 1024 || (size_t)g * ratio * pd * 4 <= (size_t)ring_lds_bytes(pd, g) - 1024))
+      return g;
+  return 0;
+}
 
 int check_geometry(int pd, int hq, int hkv, int bs, int ebs, const char* who) {
   if (pd != 64 && pd != 128 && pd != 256) {
@@ -1260,23 +1255,12 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   }
   const int pd = padded_dim;
   const int ratio = num_qo_heads / num_kv_heads;
-  // heads per workgroup: a divisor of num_kv_heads whose staged rows fit the
-  // static LDS buffers (G*ebs <= ROW) and whose q scratch fits one buffer
   const int ebs_expected = pd == 64 ? 48 : (pd == 128 ? 80 : 144);
   if (ebs != ebs_expected) {
     set_error("decode: ebs %d does not match padded_dim %d (expected %d)", ebs, pd, ebs_expected);
     return kEinval;
   }
-  // heads (waves) per workgroup: a divisor of num_kv_heads up to MAXG whose
-  // q scratch fits the first slot
-  const int maxg = pd == 256 ? 4 : 8;
-  const size_t slot_bytes = (size_t)maxg * 2 * kTile * ebs_expected;
-  int G = 0;
-  for (int g = maxg; g >= 1; g--)
-    if (num_kv_heads % g == 0 && (size_t)g * ratio * pd * sizeof(float) <= slot_bytes) {
-      G = g;
-      break;
-    }
+  const int G = decode_group_size(pd, num_kv_heads, ratio);
   if (G == 0) {
     set_error("decode: no workgroup shape for %d kv heads, ratio %d", num_kv_heads, ratio);
     return kEinval;
@@ -1307,40 +1291,38 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   p.inv_sqrt_pd = 1.0f / sqrtf((float)pd);
   p.qk_scale = sm_scale * 1.4426950408889634f * p.inv_sqrt_pd / kCbScale;
   p.pv_scale = p.inv_sqrt_pd / kCbScale;
-  // measured on MI355X at configs[2]: the first (older) group of a
-  // two-split workgroup sustains ~3/4 of the pair's work in the same time
-  p.share0 = 184;
-  const int spw = splits_per_workgroup(ratio, pd);
-  const int64_t blocks = (int64_t)batch * ((num_splits + spw - 1) / spw) * p.HG;
+  const int64_t blocks = (int64_t)batch * num_splits * p.HG;
   if (blocks > 0x7fffffffLL) {
     set_error("decode: grid too large");
     return kEinval;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  dim3 grid((unsigned)blocks), block(64 * G * spw);
+  dim3 grid((unsigned)blocks), block(64 * G);
   // scores of two tiles share one register set when ratio <= 8 (head size
-  // 256 keeps one tile per set: two would exceed the register file)
+  // 256 keeps one tile per set: two would exceed the register file); q hi/lo
+  // parts share one B operand when the GQA ratio leaves 8 columns free
   const bool pack2 = ratio <= 8 && pd <= 128;
-  // q hi/lo parts share one B operand when the GQA ratio leaves 8 columns free
   const bool qc = ratio <= 8;
-  // only the (head size, packing, split pairing) combinations these rules
-  // reach are instantiated
-#define TQ_LAUNCH(PDV, PK, QCV, SPWV) \
-  hipLaunchKernelGGL((decode_partials_kernel<PDV, PK, QCV, SPWV>), grid, block, 0, st, p)
-  switch (pd) {
-    case 64:  // spw == 1
-      if (pack2) TQ_LAUNCH(64, 2, true, 1);
-      else TQ_LAUNCH(64, 1, false, 1);
-      break;
-    case 128:  // pack2 exactly when spw == 2
-      if (pack2) TQ_LAUNCH(128, 2, true, 2);
-      else TQ_LAUNCH(128, 1, false, 1);
-      break;
-    default:  // spw == 2 only when ratio <= 4
-      if (spw == 2) TQ_LAUNCH(256, 1, true, 2);
-      else if (qc) TQ_LAUNCH(256, 1, true, 1);
-      else TQ_LAUNCH(256, 1, false, 1);
+#define TQ_LAUNCH(PDV, GV, PK, QCV) \
+  hipLaunchKernelGGL((decode_partials_kernel<PDV, GV, PK, QCV>), grid, block, 0, st, p)
+#define TQ_LAUNCH_G(PDV, PK, QCV)   \
+  switch (G) {                      \
+    case 8: TQ_LAUNCH(PDV, (PDV == 256 ? 4 : 8), PK, QCV); break; \
+    case 4: TQ_LAUNCH(PDV, 4, PK, QCV); break; \
+    case 2: TQ_LAUNCH(PDV, 2, PK, QCV); break; \
+    default: TQ_LAUNCH(PDV, 1, PK, QCV); \
   }
+  switch (pd) {
+    case 64:
+      if (pack2) { TQ_LAUNCH_G(64, 2, true) } else { TQ_LAUNCH_G(64, 1, false) }
+      break;
+    case 128:
+      if (pack2) { TQ_LAUNCH_G(128, 2, true) } else { TQ_LAUNCH_G(128, 1, false) }
+      break;
+    default:
+      if (qc) { TQ_LAUNCH_G(256, 1, true) } else { TQ_LAUNCH_G(256, 1, false) }
+  }
+#undef TQ_LAUNCH_G
 #undef TQ_LAUNCH
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -1437,7 +1419,6 @@ extern "C" int tq_decode_paged_splitkv(const void* q, int64_t q_stride_b, int64_
                               kv_chunk_size, partition_o, partition_lse, stream);
   if (rc) return rc;
   // rows the partials kernel merged away are skipped
-  return tq::combine_splits(partition_o, partition_lse,
-                            tq::splits_per_workgroup(num_qo_heads / num_kv_heads, padded_dim),
-                            batch, num_splits, num_qo_heads, padded_dim, signs, o, stream);
+  return tq::combine_splits(partition_o, partition_lse, 1, batch, num_splits, num_qo_heads,
+                            padded_dim, signs, o, stream);
 }

@@ -51,46 +51,57 @@ def hadamard_signs(pd: int, device="cpu"):
 
 
 # Decode split heuristic for MI355X.  A workgroup serves (sequence, split,
-# group of G kv heads) with one wave per kv head, and holds a double-buffered
-# LDS staging area sized for the largest G of its head size.  The split count
-# is chosen so the grid fills the workgroup slots of all CUs once: a second,
-# partial round of workgroups would leave most CUs idle at the end.  Each
-# split keeps at least MIN_CHUNK_TOKENS tokens to amortise the per-workgroup
-# q rotation and the LSE merge.
+# group of G kv heads) with one wave per kv head, and holds the 1 KB dequant
+# table plus a ring of three LDS tile slots (16 token rows of the group's
+# entries, K and V).  The split count is chosen so the grid fills the
+# workgroup slots of all CUs once: a second, partial round of workgroups
+# would leave most CUs idle at the end.  Each split keeps at least
+# MIN_CHUNK_TOKENS tokens to amortise the per-workgroup q rotation and the
+# LSE merge.
 MIN_CHUNK_TOKENS = 256
 CHUNK_ALIGN = 16
 MI355X_CUS = 256
 LDS_BYTES_PER_CU = 160 * 1024
-# waves per SIMD the decode kernel's register use allows, by padded head size
-_WAVES_PER_SIMD = {64: 6, 128: 4, 256: 2}
+
+
+def _waves_per_simd(pd: int, ratio: int) -> int:
+    """Occupancy the decode kernel is compiled for (amdgpu_waves_per_eu)."""
+    if pd == 256:
+        return 2
+    return 4 if ratio <= 8 else 3
+
+
+def ring_lds_bytes(pd: int, g: int) -> int:
+    """LDS bytes of one decode workgroup of g kv heads (tq_decode.hip
+    RingGeom): table + 3 slots x 2 regions of NI 1 KB copies, rows padded
+    to an odd number of 16-byte chunks."""
+    ech = entry_bytes(pd)[2] // 16
+    rch = (g * ech) | 1
+    ni = (16 * rch + 63) // 64
+    return 1024 + 3 * 2 * ni * 1024
+
+
+def decode_group_size(pd: int, num_kv_heads: int, ratio: int) -> int:
+    """Heads (waves) per decode workgroup, as the launcher picks them: the
+    largest of 8, 4, 2, 1 (at most 4 for pd 256) dividing num_kv_heads whose
+    q scratch fits the ring when q' is formed in LDS (ratio * pd > 1024)."""
+    maxg = 4 if pd == 256 else 8
+    g = maxg
+    while g >= 1:
+        if num_kv_heads % g == 0 and (ratio * pd <= 1024 or
+                                      g * ratio * pd * 4 <= ring_lds_bytes(pd, g) - 1024):
+            return g
+        g //= 2
+    return 0
 
 
 def decode_workgroup_shape(num_qo_heads: int, num_kv_heads: int, pd: int) -> tuple[int, int]:
-    """(G, splits resident per CU) of the decode kernel; G mirrors the
-    launcher in tq_decode.hip (largest divisor of num_kv_heads up to 8 (4 for
-    pd 256) whose rotated-q scratch fits the first LDS slot)."""
-    ebs = entry_bytes(pd)[2]
-    maxg = 4 if pd == 256 else 8
-    slot_bytes = maxg * 2 * 16 * ebs  # V of one two-tile step for each of maxg waves
+    """(G, workgroups resident per CU) of the decode kernel."""
     ratio = max(1, num_qo_heads // max(1, num_kv_heads))
-    G = 1
-    for g in range(maxg, 0, -1):
-        if num_kv_heads % g == 0 and g * ratio * pd * 4 <= slot_bytes:
-            G = g
-            break
-    spw = decode_splits_per_workgroup(num_qo_heads, num_kv_heads, pd)
-    table = 65536 if spw == 2 else 1024  # the dequant table (64 copies with two splits)
-    by_lds = LDS_BYTES_PER_CU // (2 * slot_bytes * spw + table)
-    by_waves = 4 * _WAVES_PER_SIMD.get(pd, 2) // (G * spw)
-    return G, spw * max(1, min(by_lds, by_waves))
-
-
-def decode_splits_per_workgroup(num_qo_heads: int, num_kv_heads: int, pd: int) -> int:
-    """Splits one decode workgroup serves: 2 (one 16-wave workgroup per CU)
-    when q' fits the register path and pd >= 128, else 1 (mirrors the
-    launcher in tq_decode.hip)."""
-    ratio = max(1, num_qo_heads // max(1, num_kv_heads))
-    return 2 if (ratio * pd <= 1024 and pd >= 128) else 1
+    G = max(1, decode_group_size(pd, num_kv_heads, ratio))
+    by_lds = LDS_BYTES_PER_CU // ring_lds_bytes(pd, G)
+    by_waves = 4 * _waves_per_simd(pd, ratio) // G
+    return G, max(1, min(by_lds, by_waves))
 
 
 def choose_splits(batch: int, max_len: int, num_kv_heads: int, num_qo_heads: int | None = None,
