@@ -206,22 +206,18 @@ struct SoftmaxState {
   float m, mb, lsum;
 };
 
-// LDS byte address of dequant-table entry `byte k of w`.  The table (256
-// dwords: entry e = fp16 values of the high and low nibble of code byte e)
-// sits at LDS address 0, so the address is the byte times 4: one SDWA shift
-// with a byte-select source operand.
-__device__ __forceinline__ uint32_t lut_addr(uint32_t w, int k) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  if (k == 0) {
-    uint32_t a;
-    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
-        "src1_sel:BYTE_0"
-        : "=v"(a)
-        : "v"(2u), "v"(w));
-    return a;
-  }
-#endif
-  return ((w >> (8 * k)) & 0xffu) << 2;
+// The dequant table: 256 entries (entry e = fp16 values of the high and low
+// nibble of code byte e), each held in kLutCopies copies side by side at the
+// start of LDS (entry e, copy c at dword e * kLutCopies + c).  Lane l reads
+// copy l mod 32, so the 32 lanes the LDS serves per cycle always hit 32
+// distinct banks, whatever the codes: a lookup never has a bank conflict.
+constexpr int kLutCopies = 32;
+constexpr int kLutBytes = 256 * 4 * kLutCopies;
+
+// LDS byte address of the table entry `byte k of w` for this lane (lanec =
+// 4 * (lane mod 32)).
+__device__ __forceinline__ uint32_t lut_addr(uint32_t w, int k, uint32_t lanec) {
+  return (((w >> (8 * k)) & 0xffu) << 7) | lanec;
 }
 
 // Eight table reads in place (each address register receives its entry)
@@ -259,7 +255,7 @@ __device__ __forceinline__ void lut_read8(uint32_t* a) {
 // separate hi/lo operands, two MFMAs per K block.
 template <int PD, bool QC>
 __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_t* qb,
-                                                const half8_t* ql) {
+                                                const half8_t* ql, uint32_t lanec) {
   constexpr int KD = PD / 32;
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -269,7 +265,7 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
 #pragma unroll
     for (int u = 0; u < 2; u++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) x[4 * u + j] = lut_addr(kw[c + u], j);
+      for (int j = 0; j < 4; j++) x[4 * u + j] = lut_addr(kw[c + u], j, lanec);
     lut_read8(x);
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -300,7 +296,7 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
 template <int PD>
 __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD / 128 : 1],
                                         const uint32_t (*v1)[(PD / 32) >= 4 ? PD / 128 : 1],
-                                        half8_t p, SoftmaxState<PD>& st) {
+                                        half8_t p, SoftmaxState<PD>& st, uint32_t lanec) {
   constexpr int VB = PD / 32;
   constexpr int VW = VB >= 4 ? VB / 4 : 1;
   // ix[T][pair][nibble][w]: pair 0 = tokens 0, 1; pair 1 = tokens 2, 3;
@@ -327,7 +323,8 @@ __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD
 #pragma unroll
       for (int T = 0; T < 2; T++)
 #pragma unroll
-        for (int pr = 0; pr < 2; pr++) x[4 * nb + 2 * T + pr] = lut_addr(ix[T][pr][nb][w], j);
+        for (int pr = 0; pr < 2; pr++)
+          x[4 * nb + 2 * T + pr] = lut_addr(ix[T][pr][nb][w], j, lanec);
     lut_read8(x);
     const half8_t lo8 = as_half8(x[0], x[1], x[2], x[3]);
     const half8_t hi8 = as_half8(x[4], x[5], x[6], x[7]);
@@ -363,7 +360,7 @@ __host__ __device__ constexpr int vmcnt_imm(int n) {
 // the row's last chunk).  NI 1 KB copies fill one region (the last may
 // spill past the rows into the region's slack).  Three slots form the ring.
 #ifndef TQ_RING_SLOTS
-#define TQ_RING_SLOTS 3
+#define TQ_RING_SLOTS 2
 #endif
 constexpr int kRingSlots = TQ_RING_SLOTS;  // tile slots in the LDS ring
 
@@ -381,7 +378,7 @@ struct RingGeom {
   static constexpr int NW_HI = (NIT + G - 1) / G;             // copies per tile, waves < NIT % G
   static constexpr int NW_LO = NIT / G;                       // copies per tile, other waves
   static constexpr int RING = kRingSlots * TS;
-  static constexpr int LDS = 1024 + RING;                     // table + ring
+  static constexpr int LDS = kLutBytes + RING;               // table + ring
 };
 
 // This wave's K codes, V codes and norms of the step's two tiles, read from
@@ -596,22 +593,26 @@ void decode_partials_kernel(DecodeParams p) {
   // LDS: the dequant table at address 0 (the table reads rely on it), then
   // the ring of three tile slots
   struct __attribute__((aligned(16))) Lds {
-    uint32_t klut[256];
+    uint32_t klut[256 * kLutCopies];
     uint8_t ring[RG::RING];
   };
   __shared__ Lds sm;
 
   // dequant table: byte e -> fp16 values of its high nibble (low half) and
-  // its low nibble (high half), built with the same table arithmetic as dq8
-  for (int i = threadIdx.x; i < 256; i += 64 * G) {
+  // its low nibble (high half), built with the same table arithmetic as dq8,
+  // in kLutCopies copies (written four at a time)
+  for (int i = threadIdx.x; i < 64 * kLutCopies; i += 64 * G) {
+    const int e = i / (kLutCopies / 4);
     uint32_t x[4];
-    dq8((uint32_t)i * 0x01010101u, x);
-    sm.klut[i] = (x[2] & 0xffffu) | (x[0] << 16);
+    dq8((uint32_t)e * 0x01010101u, x);
+    const uint32_t val = (x[2] & 0xffffu) | (x[0] << 16);
+    *reinterpret_cast<u32x4*>(&sm.klut[4 * i]) = u32x4{val, val, val, val};
   }
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int q4 = lane >> 4, n = lane & 15;
+  const uint32_t lanec = (uint32_t)(lane & 31) * 4u;  // this lane's table copy
   int bid = blockIdx.x;
   const int hg = bid % p.HG;
   bid /= p.HG;
@@ -954,9 +955,9 @@ void decode_partials_kernel(DecodeParams p) {
       // scores of both tiles (scheduling barriers keep the two tiles'
       // dequant temporaries from being live at the same time)
       float4_t acc[2];
-      acc[0] = tile_scores<PD, QC>(d.k[0], qb, ql);
+      acc[0] = tile_scores<PD, QC>(d.k[0], qb, ql, lanec);
       __builtin_amdgcn_sched_barrier(0);
-      acc[1] = tile_scores<PD, QC>(d.k[1], qb, ql);
+      acc[1] = tile_scores<PD, QC>(d.k[1], qb, ql, lanec);
       __builtin_amdgcn_sched_barrier(0);
       constexpr int NV = 4 * (2 / PACK);  // score values per lane
       float sc[NV], nk[NV], nv[NV];
@@ -999,7 +1000,7 @@ void decode_partials_kernel(DecodeParams p) {
       } else {
         p8 = half8_t{pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
       }
-      step_pv<PD>(d.v[0], d.v[1], p8, st);
+      step_pv<PD>(d.v[0], d.v[1], p8, st, lanec);
     };
 
     // one step: tiles 2k, 2k + 1 in ring slots s0, s1
@@ -1011,7 +1012,7 @@ void decode_partials_kernel(DecodeParams p) {
       __builtin_amdgcn_sched_barrier(0);
       StepData<PD> d;
       {
-        const uint32_t b0 = 1024 + s0 * RG::TS, b1 = 1024 + s1 * RG::TS;  // K regions
+        const uint32_t b0 = kLutBytes + s0 * RG::TS, b1 = kLutBytes + s1 * RG::TS;  // K regions
         const uint32_t ka[2] = {oK[0] + b0, oK[0] + b1};
         const uint32_t na = oN + (PACK == 2 && ptile ? b1 : b0);
         read_step<PD, G, PACK>(ka, oV + b0 + RG::SLAB, oV + b1 + RG::SLAB, na, oN + b1, d);
@@ -1184,7 +1185,7 @@ int ring_lds_bytes(int pd, int g) {
   const int ech = (pd == 64 ? 48 : (pd == 128 ? 80 : 144)) / 16;
   const int rch = (g * ech) | 1;
   const int ni = (kTile * rch + 63) / 64;
-  return 1024 + kRingSlots * 2 * ni * 1024;
+  return kLutBytes + kRingSlots * 2 * ni * 1024;
 }
 
 // Heads (waves) per partials workgroup: the largest of 8, 4, 2, 1 (at most 4
@@ -1194,7 +1195,7 @@ int decode_group_size(int pd, int hkv, int ratio) {
   const int maxg = pd == 256 ? 4 : 8;
   for (int g = maxg; g >= 1; g >>= 1)
     if (hkv % g == 0 &&
-        (ratio * pd <= 1024 || (size_t)g * ratio * pd * 4 <= (size_t)ring_lds_bytes(pd, g) - 1024))
+        (ratio * pd <= 1024 || (size_t)g * ratio * pd * 4 <= (size_t)(ring_lds_bytes(pd, g) - kLutBytes)))
       return g;
   return 0;
 }

@@ -71,14 +71,18 @@ def _waves_per_simd(pd: int, ratio: int) -> int:
     return 4 if ratio <= 8 else 3
 
 
+LUT_BYTES = 256 * 4 * 32  # dequant table: 256 entries x 32 bank-spread copies
+RING_SLOTS = 2
+
+
 def ring_lds_bytes(pd: int, g: int) -> int:
     """LDS bytes of one decode workgroup of g kv heads (tq_decode.hip
-    RingGeom): table + 3 slots x 2 regions of NI 1 KB copies, rows padded
-    to an odd number of 16-byte chunks."""
+    RingGeom::LDS): the table + RING_SLOTS tile slots x 2 regions of NI 1 KB
+    copies, rows padded to an odd number of 16-byte chunks."""
     ech = entry_bytes(pd)[2] // 16
     rch = (g * ech) | 1
     ni = (16 * rch + 63) // 64
-    return 1024 + 3 * 2 * ni * 1024
+    return LUT_BYTES + RING_SLOTS * 2 * ni * 1024
 
 
 def decode_group_size(pd: int, num_kv_heads: int, ratio: int) -> int:
@@ -89,7 +93,7 @@ def decode_group_size(pd: int, num_kv_heads: int, ratio: int) -> int:
     g = maxg
     while g >= 1:
         if num_kv_heads % g == 0 and (ratio * pd <= 1024 or
-                                      g * ratio * pd * 4 <= ring_lds_bytes(pd, g) - 1024):
+                                      g * ratio * pd * 4 <= ring_lds_bytes(pd, g) - LUT_BYTES):
             return g
         g //= 2
     return 0
