@@ -600,14 +600,23 @@ void decode_partials_kernel(DecodeParams p) {
 
   // dequant table: byte e -> fp16 values of its high nibble (low half) and
   // its low nibble (high half), built with the same table arithmetic as dq8,
-  // in kLutCopies copies (written four at a time)
-  for (int i = threadIdx.x; i < 64 * kLutCopies; i += 64 * G) {
-    const int e = i / (kLutCopies / 4);
-    uint32_t x[4];
-    dq8((uint32_t)e * 0x01010101u, x);
-    const uint32_t val = (x[2] & 0xffffu) | (x[0] << 16);
-    *reinterpret_cast<u32x4*>(&sm.klut[4 * i]) = u32x4{val, val, val, val};
-  }
+  // in kLutCopies copies (written four at a time, as inline assembly: the
+  // copies in flight into the ring do not touch it, which the compiler
+  // cannot tell)
+  auto init_table = [&]() {
+    for (int i = threadIdx.x; i < 64 * kLutCopies; i += 64 * G) {
+      const int e = i / (kLutCopies / 4);
+      uint32_t x[4];
+      dq8((uint32_t)e * 0x01010101u, x);
+      const uint32_t val = (x[2] & 0xffffu) | (x[0] << 16);
+#if defined(__HIP_DEVICE_COMPILE__)
+      asm volatile("ds_write_b128 %0, %1" : : "v"(lds_addr(&sm.klut[4 * i])), "v"(u32x4{val, val, val, val}) : "memory");
+#endif
+    }
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
+  };
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -620,6 +629,10 @@ void decode_partials_kernel(DecodeParams p) {
   const int b = bid / p.S;
   const int kvh = hg * G + w;
   const int ratio = p.ratio;
+  // sequence length and page-table start, loaded before anything else: the
+  // first copies depend on them
+  const int L = p.seq_lens[b];
+  const int ip = p.indptr[b];
 
   half8_t qb[KD], ql[QC ? 1 : KD];  // q' operands
 
@@ -657,6 +670,13 @@ void decode_partials_kernel(DecodeParams p) {
   }
 #endif
 
+#if defined(__HIP_DEVICE_COMPILE__)
+  // both scalar loads complete here, in one round trip with the q loads in
+  // flight (the compiler would otherwise sink the page-table start below the
+  // branch on the split range and pay a second round trip)
+  asm volatile("" : : "s"(L), "s"(ip));
+#endif
+
   SoftmaxState<PD> st;
 #pragma unroll
   for (int i = 0; i < NO; i++) st.O[i] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -665,20 +685,13 @@ void decode_partials_kernel(DecodeParams p) {
   st.lsum = 0.f;
   const float lpv = -__log2f(p.pv_scale);
 
-  const int L = p.seq_lens[b];
   const int c0 = s * p.cs;
   const int c1 = min(c0 + p.cs, L);
-  // the table is written (an LDS-only wait, so the q loads stay in flight)
-#if defined(__HIP_DEVICE_COMPILE__)
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#endif
-  __builtin_amdgcn_s_barrier();
   if (c0 < c1) {  // uniform over the workgroup
     constexpr int STEP = 2 * kTile;
     const int step0 = c0 / STEP, step1 = (c1 - 1) / STEP;
     const int tpp = p.block_size / kTile;  // tiles per page
     const int64_t tokstride = (int64_t)p.Hkv * EBS;
-    const int ip = p.indptr[b];
     const uint8_t* const kslab = p.ks;
     const uint8_t* const vslab = p.vs;
     const int tile_last = (c1 - 1) / kTile;
@@ -808,10 +821,14 @@ void decode_partials_kernel(DecodeParams p) {
     const int head = n % slotw;    // head of this lane's packed scores
     const uint32_t oN = (4 * q4 + (lane & 3)) * ROWB + (hb + PD / 32) * 16;
 
-    // (q' in registers: the tiles whose slots do not hold the q' scratch)
-    const int qfirst = G * 4096 <= (kRingSlots - 1) * RG::TS ? 1 : 0;  // tiles before the q setup
-    const uint32_t qscr = (uint32_t)(qfirst * RG::TS);  // q' scratch: ring offset
-    if (qreg && qfirst) issue(2 * step0, 0);
+    // the q' scratch lives where the dequant table goes (the table is built
+    // after it); with q' formed in registers it fits there (4 KB a wave), so
+    // the first tiles go out before the q setup
+    if (qreg) {
+#pragma unroll
+      for (int r = 0; r < kRingSlots; r++)
+        if (2 * step0 + r <= tile_end) issue(2 * step0 + r, r);
+    }
 
     // ---- q' = FWHT(s*q)/sqrt(pd), scaled to log2 units and split into
     // fp16 hi + lo parts (q' = hi + lo to ~22 bits, so the scores keep
@@ -821,9 +838,12 @@ void decode_partials_kernel(DecodeParams p) {
     if (qreg) {
       // in registers: butterflies h = 1, 2, 4 inside a lane, h >= 8 between
       // lanes l and l ^ (h / 8) (DPP, one fma with a lane sign each)
+      // the second 512 elements only exist when ratio * PD > 512
+      const bool q2 = ratio * PD > 512;  // uniform
       if (p.signs) {
 #pragma unroll
         for (int j = 0; j < NQL; j++) {
+          if (j > 0 && !q2) break;
 #pragma unroll
           for (int h = 1; h < 8; h <<= 1)
 #pragma unroll
@@ -846,9 +866,10 @@ void decode_partials_kernel(DecodeParams p) {
       // q4 * PD/4 + 8c + 0..7.  Inline assembly: the scratch shares the ring
       // with the copy in flight, and the compiler would otherwise wait for it.
 #if defined(__HIP_DEVICE_COMPILE__)
-      const uint32_t qsb = lds_addr(sm.ring) + qscr + (uint32_t)w * 4096u;
+      const uint32_t qsb = lds_addr(sm.klut) + (uint32_t)w * 4096u;
 #pragma unroll
       for (int j = 0; j < NQL; j++) {
+        if (j > 0 && !q2) break;  // those scratch elements are never read
         u32x4 vh, vl;
 #pragma unroll
         for (int wd = 0; wd < 4; wd++) {
@@ -871,6 +892,7 @@ void decode_partials_kernel(DecodeParams p) {
         const uint32_t e = (uint32_t)(hq * PD + q4 * (PD / 4) + 8 * c);
         u32x4 vh, vl;
         if constexpr (QC) {
+          // (columns of heads >= ratio read elements never written: zeroed)
           asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
                        : "=v"(vh)
                        : "v"(qsb + e * 2u + (n < 8 ? 0u : 2048u))
@@ -889,21 +911,19 @@ void decode_partials_kernel(DecodeParams p) {
         }
       }
 #endif
-      // once every wave has read its scratch, the rest of the first tiles go
-      // out (their copies overwrite the scratch)
+      // once every wave has read its scratch, the table overwrites it
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int r = 0; r < kRingSlots; r++)
-        if (r >= qfirst && 2 * step0 + r <= tile_end) issue(2 * step0 + r, r);
+      init_table();
     } else {
       // ---- q' = FWHT(s*q)/sqrt(pd) for this wave's `ratio` heads on an LDS
-      // scratch in the ring (each wave its own region; the launcher keeps
-      // G * ratio * PD floats within the ring), before any copy is issued.
+      // scratch from the table's place on (each wave its own region; the
+      // launcher keeps G * ratio * PD floats within the table and the ring),
+      // before any copy is issued.
       // LDS operations of one wave complete in order, so a wave barrier
       // orders the butterfly stages.
-      float* const qs = reinterpret_cast<float*>(sm.ring) + (size_t)w * ratio * PD;
+      float* const qs = reinterpret_cast<float*>(sm.klut) + (size_t)w * ratio * PD;
       auto qsync = [&]() {
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -947,6 +967,7 @@ void decode_partials_kernel(DecodeParams p) {
 #pragma unroll
       for (int r = 0; r < kRingSlots; r++)
         if (2 * step0 + r <= tile_end) issue(2 * step0 + r, r);
+      init_table();
     }
 
     // math of one step (tiles 2k, 2k + 1) from the registers in d
@@ -1195,7 +1216,7 @@ int decode_group_size(int pd, int hkv, int ratio) {
   const int maxg = pd == 256 ? 4 : 8;
   for (int g = maxg; g >= 1; g >>= 1)
     if (hkv % g == 0 &&
-        (ratio * pd <= 1024 || (size_t)g * ratio * pd * 4 <= (size_t)(ring_lds_bytes(pd, g) - kLutBytes)))
+        (ratio * pd <= 1024 || (size_t)g * ratio * pd * 4 <= (size_t)ring_lds_bytes(pd, g)))
       return g;
   return 0;
 }

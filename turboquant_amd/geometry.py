@@ -88,12 +88,12 @@ def ring_lds_bytes(pd: int, g: int) -> int:
 def decode_group_size(pd: int, num_kv_heads: int, ratio: int) -> int:
     """Heads (waves) per decode workgroup, as the launcher picks them: the
     largest of 8, 4, 2, 1 (at most 4 for pd 256) dividing num_kv_heads whose
-    q scratch fits the ring when q' is formed in LDS (ratio * pd > 1024)."""
+    q scratch fits the table and ring when q' is formed in LDS (ratio * pd > 1024)."""
     maxg = 4 if pd == 256 else 8
     g = maxg
     while g >= 1:
         if num_kv_heads % g == 0 and (ratio * pd <= 1024 or
-                                      g * ratio * pd * 4 <= ring_lds_bytes(pd, g) - LUT_BYTES):
+                                      g * ratio * pd * 4 <= ring_lds_bytes(pd, g)):
             return g
         g //= 2
     return 0
