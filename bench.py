@@ -168,8 +168,8 @@ def bench_write(torch, steps, warmup):
     v = torch.from_numpy(c["v"]).to(dev)
     slots = torch.from_numpy(c["slots"]).to(dev)
     signs = hadamard_signs(pd, dev)
-    ms = time_launches(torch, lambda: ops.quantize_write_kv_cache(cache, k, v, signs, slots,
-                                                                  128, pd), steps, warmup)
+    ms = time_graph(torch, lambda: ops.quantize_write_kv_cache(cache, k, v, signs, slots,
+                                                               128, pd), steps, warmup)
     nbytes = W.algorithmic_write_bytes(8192, 8, 128)
     return {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "alg_bytes": nbytes, "config": "8192 tok x 8 heads x 128, K+V fp16, outliers x20, "

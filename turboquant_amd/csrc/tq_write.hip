@@ -1,14 +1,15 @@
 // tq_write.hip -- quantize-and-scatter of K/V rows into the packed paged cache.
 //
 // Same numbers as the reference scatter kernel
-// (csrc/include/turboquant/quantize_write_kernel.cuh:332-431): every vector is
-// handled by 32 lanes holding VEC = pd/32 consecutive dims each, so the
-// fp32 sum of squares, its reduction tree, sqrt, reciprocal, sign flip,
-// FWHT butterflies and the 1/sqrt(pd) scale happen in the same order and
-// give the same bits.  MI355X layout: a wave64 carries two vectors (one per
-// 32-lane half), a 256-thread workgroup carries 8 consecutive (token, head)
-// vectors, so the 8 heads of one token (8 x ebs contiguous bytes) are
-// written by one workgroup.  One launch covers K and V.
+// (csrc/include/turboquant/quantize_write_kernel.cuh:332-431), which gives
+// every vector 32 lanes of VEC = pd/32 consecutive dims: the fp32 sum of
+// squares, its reduction tree, sqrt, reciprocal, sign flip, FWHT butterflies
+// and the 1/sqrt(pd) scale happen in the same order and give the same bits.
+// MI355X layout: 16 lanes per vector, each holding the dims of two of the
+// reference's lanes (p and p + 16), so a wave64 carries four vectors and the
+// per-vector work (index math, reduction, sqrt, divide, norm store) is
+// shared by twice the dims; a 256-thread workgroup writes 16 consecutive
+// (token, head) entries, i.e. whole cache rows.  One launch covers K and V.
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -99,41 +100,58 @@ __device__ __forceinline__ float xor_lane(float x) {
   }
 }
 
+// Quantize-and-scatter: 16 lanes per vector, 4 vectors per wave64, 16
+// consecutive vectors (kv, token, head; head fastest, so the entries of one
+// token's heads are written together) per 256-thread workgroup.  Physical
+// lane p of a vector holds the dims of two lanes of the reference's 32-lane
+// layout (quantize_write_kernel.cuh:332-431): lane p (dims VEC p .. +VEC) in
+// x0 and lane p + 16 in x1.  The arithmetic is the reference's, in its
+// order: per-lane FMA sums, the shfl_down tree 16, 8, 4, 2, 1 (its first
+// level pairs x0 and x1 of one physical lane), IEEE sqrt and reciprocal,
+// sign flip, FWHT stages h = 1 .. pd/2 in ascending order (the last one,
+// between lanes p and p + 16, again inside one physical lane), 1/sqrt(pd),
+// bucketize, pack.
 template <int PD, bool VEC_OK>
 __global__ __launch_bounds__(256) void write_kernel(
     uint8_t* __restrict__ k_slab, uint8_t* __restrict__ v_slab,
     const void* __restrict__ key, const void* __restrict__ value, int dtype,
     int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh,
     const float* __restrict__ signs, const int32_t* __restrict__ slots,
-    int64_t num_tokens, int H, int head_dim, int block_size, int ebs, int64_t nslots,
+    uint32_t per_kv, int H, uint32_t hmul, int head_dim, int ebs, int64_t nslots,
     float scale) {
 #pragma clang fp contract(off)
   constexpr int VEC = PD / 32;
-  const int lane = threadIdx.x & 31;
-  const int64_t per_kv = num_tokens * H;
-  const int64_t g = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
-  if (g >= 2 * per_kv) return;
+  const int lane = threadIdx.x & 15;
+  const uint32_t g = blockIdx.x * 16u + (threadIdx.x >> 4);
+  if (g >= 2 * per_kv) return;  // a whole 16-lane group (one DPP row) leaves
   const int kv = g >= per_kv ? 1 : 0;
-  const int64_t rem = g - kv * per_kv;
-  const int64_t t = rem / H;
-  const int h = (int)(rem - t * H);
+  const uint32_t rem = g - (kv ? per_kv : 0u);
+  // t = rem / H by multiply-high (hmul = ceil(2^32 / H), exact for rem < 2^32 / H)
+  const uint32_t t = H == 1 ? rem : __umulhi(rem, hmul);
+  const int h = (int)(rem - t * (uint32_t)H);
+
+  float x0[VEC], x1[VEC];
+  const int da = lane * VEC, db = (lane + 16) * VEC;
+  if (kv == 0) {
+    load_row<VEC>(key, (int64_t)t * k_st + h * k_sh, dtype, da, head_dim, VEC_OK, x0);
+    load_row<VEC>(key, (int64_t)t * k_st + h * k_sh, dtype, db, head_dim, VEC_OK, x1);
+  } else {
+    load_row<VEC>(value, (int64_t)t * v_st + h * v_sh, dtype, da, head_dim, VEC_OK, x0);
+    load_row<VEC>(value, (int64_t)t * v_st + h * v_sh, dtype, db, head_dim, VEC_OK, x1);
+  }
   const int32_t slot = slots[t];
-  if (slot < 0 || (int64_t)slot >= nslots) return;  // whole 32-lane group leaves together
+  if (slot < 0 || (int64_t)slot >= nslots) return;  // whole 16-lane group together
 
-  float v[VEC];
-  const int d0 = lane * VEC;
-  if (kv == 0)
-    load_row<VEC>(key, t * k_st + h * k_sh, dtype, d0, head_dim, VEC_OK, v);
-  else
-    load_row<VEC>(value, t * v_st + h * v_sh, dtype, d0, head_dim, VEC_OK, v);
-
-  // 1. per-lane sum of squares, FMA-accumulated in dim order
-  float ss = 0.0f;
+  // 1. per-lane sums of squares, FMA-accumulated in dim order
+  float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-  for (int i = 0; i < VEC; i++) ss = __builtin_fmaf(v[i], v[i], ss);
-  // 2. 32-lane butterfly; every lane ends with the bits lane 0 of the
-  //    reference's shfl_down tree (16,8,4,2,1) holds
-  ss = ss + xor_lane<16>(ss);
+  for (int i = 0; i < VEC; i++) {
+    s0 = __builtin_fmaf(x0[i], x0[i], s0);
+    s1 = __builtin_fmaf(x1[i], x1[i], s1);
+  }
+  // 2. the tree: level 16 in-lane, then 8, 4, 2, 1 across the 16 lanes;
+  //    every lane ends with the bits the reference's lane 0 holds
+  float ss = s0 + s1;
   ss = ss + xor_lane<8>(ss);
   ss = ss + xor_lane<4>(ss);
   ss = ss + xor_lane<2>(ss);
@@ -143,19 +161,30 @@ __global__ __launch_bounds__(256) void write_kernel(
   const float inv = (l2 > 1e-8f) ? (1.0f / l2) : 0.0f;
   // 4. normalise, flip signs
 #pragma unroll
-  for (int i = 0; i < VEC; i++) v[i] = v[i] * inv;
+  for (int i = 0; i < VEC; i++) {
+    x0[i] = x0[i] * inv;
+    x1[i] = x1[i] * inv;
+  }
 #pragma unroll
-  for (int i = 0; i < VEC; i++) v[i] = v[i] * signs[d0 + i];
-  // 5. FWHT: in-lane stages, then cross-lane stages
+  for (int i = 0; i < VEC; i++) {
+    x0[i] = x0[i] * signs[da + i];
+    x1[i] = x1[i] * signs[db + i];
+  }
+  // 5. FWHT: in-lane stages h < VEC, cross-lane stages (lane xor 1..8), then
+  //    the stage between lanes p and p + 16
 #pragma unroll
   for (int hh = 1; hh < VEC; hh <<= 1) {
 #pragma unroll
     for (int i = 0; i < VEC; i += 2 * hh) {
 #pragma unroll
       for (int k = 0; k < hh; k++) {
-        float a = v[i + k], b = v[i + k + hh];
-        v[i + k] = a + b;
-        v[i + k + hh] = a - b;
+        float a = x0[i + k], b = x0[i + k + hh];
+        x0[i + k] = a + b;
+        x0[i + k + hh] = a - b;
+        a = x1[i + k];
+        b = x1[i + k + hh];
+        x1[i + k] = a + b;
+        x1[i + k + hh] = a - b;
       }
     }
   }
@@ -165,15 +194,21 @@ __global__ __launch_bounds__(256) void write_kernel(
     constexpr int D = decltype(dist)::value;
     const float sg = (lane & D) ? -1.0f : 1.0f;
 #pragma unroll
-    for (int i = 0; i < VEC; i++) v[i] = __builtin_fmaf(sg, v[i], xor_lane<D>(v[i]));
+    for (int i = 0; i < VEC; i++) {
+      x0[i] = __builtin_fmaf(sg, x0[i], xor_lane<D>(x0[i]));
+      x1[i] = __builtin_fmaf(sg, x1[i], xor_lane<D>(x1[i]));
+    }
   };
   cross(std::integral_constant<int, 1>{});
   cross(std::integral_constant<int, 2>{});
   cross(std::integral_constant<int, 4>{});
   cross(std::integral_constant<int, 8>{});
-  cross(std::integral_constant<int, 16>{});
 #pragma unroll
-  for (int i = 0; i < VEC; i++) v[i] = v[i] * scale;
+  for (int i = 0; i < VEC; i++) {
+    const float a = x0[i], b = x1[i];
+    x0[i] = (a + b) * scale;
+    x1[i] = (a - b) * scale;
+  }
 
   // 6. bucketize against b_j * scale (fp32 products, as the reference forms them)
   int32_t bbits[7];
@@ -183,19 +218,23 @@ __global__ __launch_bounds__(256) void write_kernel(
   uint8_t* entry = (kv == 0 ? k_slab : v_slab) +
                    ((int64_t)slot * H + h) * (int64_t)ebs;  // slot*H == (block*bs+entry)*H
   // 7. pack: byte k = code[2k] << 4 | code[2k+1]
-  uint32_t packed = 0;
+  uint32_t p0 = 0, p1 = 0;
 #pragma unroll
   for (int i = 0; i < VEC; i += 2) {
-    uint32_t c0 = bucketize(v[i], bbits), c1 = bucketize(v[i + 1], bbits);
-    packed |= ((c0 << 4) | c1) << (4 * i);  // byte i/2
+    p0 |= ((bucketize(x0[i], bbits) << 4) | bucketize(x0[i + 1], bbits)) << (4 * i);
+    p1 |= ((bucketize(x1[i], bbits) << 4) | bucketize(x1[i + 1], bbits)) << (4 * i);
   }
-  uint8_t* dst = entry + lane * (VEC / 2);
+  uint8_t* d0p = entry + lane * (VEC / 2);
+  uint8_t* d1p = entry + (lane + 16) * (VEC / 2);
   if constexpr (VEC == 2) {
-    *dst = (uint8_t)packed;
+    *d0p = (uint8_t)p0;
+    *d1p = (uint8_t)p1;
   } else if constexpr (VEC == 4) {
-    *reinterpret_cast<uint16_t*>(dst) = (uint16_t)packed;
+    *reinterpret_cast<uint16_t*>(d0p) = (uint16_t)p0;
+    *reinterpret_cast<uint16_t*>(d1p) = (uint16_t)p1;
   } else {
-    *reinterpret_cast<uint32_t*>(dst) = packed;
+    *reinterpret_cast<uint32_t*>(d0p) = p0;
+    *reinterpret_cast<uint32_t*>(d1p) = p1;
   }
   // 8. fp16(l2), round to nearest even, repeated pd/64 times after the codes
   if (lane == 0) {
@@ -219,16 +258,16 @@ template <int PD>
 hipError_t launch_write(bool vec_ok, dim3 grid, hipStream_t stream, uint8_t* ks, uint8_t* vs,
                         const void* key, const void* value, int dtype, int64_t k_st,
                         int64_t k_sh, int64_t v_st, int64_t v_sh, const float* signs,
-                        const int32_t* slots, int64_t n, int H, int hd, int bs, int ebs,
-                        int64_t nslots, float scale) {
+                        const int32_t* slots, uint32_t per_kv, int H, uint32_t hmul, int hd,
+                        int ebs, int64_t nslots, float scale) {
   if (vec_ok)
     hipLaunchKernelGGL((write_kernel<PD, true>), grid, dim3(256), 0, stream, ks, vs, key, value,
-                       dtype, k_st, k_sh, v_st, v_sh, signs, slots, n, H, hd, bs, ebs, nslots,
-                       scale);
+                       dtype, k_st, k_sh, v_st, v_sh, signs, slots, per_kv, H, hmul, hd, ebs,
+                       nslots, scale);
   else
     hipLaunchKernelGGL((write_kernel<PD, false>), grid, dim3(256), 0, stream, ks, vs, key, value,
-                       dtype, k_st, k_sh, v_st, v_sh, signs, slots, n, H, hd, bs, ebs, nslots,
-                       scale);
+                       dtype, k_st, k_sh, v_st, v_sh, signs, slots, per_kv, H, hmul, hd, ebs,
+                       nslots, scale);
   return hipGetLastError();
 }
 
@@ -292,12 +331,17 @@ extern "C" int tq_quantize_write_kv_cache(void* k_slab, void* v_slab, const void
                 (k_stride_tok % vec == 0) && (k_stride_head % vec == 0) &&
                 (v_stride_tok % vec == 0) && (v_stride_head % vec == 0) &&
                 ((uintptr_t)key % (vec * esz) == 0) && ((uintptr_t)value % (vec * esz) == 0);
-  const int64_t vectors = 2 * num_tokens * (int64_t)num_kv_heads;
-  const int64_t blocks = (vectors + 7) / 8;
-  if (blocks > 0x7fffffffLL) {
-    set_error("quantize_write: too many tokens");
+  // 16 vectors per workgroup; token = rem / H by multiply-high, exact while
+  // num_tokens * H < 2^32 / H
+  const int64_t per_kv = num_tokens * (int64_t)num_kv_heads;
+  if (per_kv * num_kv_heads >= (int64_t)1 << 32 || 2 * per_kv >= (int64_t)1 << 32) {
+    set_error("quantize_write: too many tokens (%lld x %d heads)", (long long)num_tokens,
+              num_kv_heads);
     return kEinval;
   }
+  const uint32_t hmul =
+      num_kv_heads == 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + num_kv_heads - 1) / num_kv_heads);
+  const int64_t blocks = (2 * per_kv + 15) / 16;
   const float scale = 1.0f / sqrtf((float)pd);
   const int64_t nslots = num_blocks * (int64_t)block_size;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -309,17 +353,17 @@ extern "C" int tq_quantize_write_kv_cache(void* k_slab, void* v_slab, const void
     case 64:
       e = launch_write<64>(vec_ok, grid, s, ks, vs, key, value, in_dtype, k_stride_tok,
                            k_stride_head, v_stride_tok, v_stride_head, signs, slot_mapping,
-                           num_tokens, num_kv_heads, head_dim, block_size, ebs, nslots, scale);
+                           (uint32_t)per_kv, num_kv_heads, hmul, head_dim, ebs, nslots, scale);
       break;
     case 128:
       e = launch_write<128>(vec_ok, grid, s, ks, vs, key, value, in_dtype, k_stride_tok,
                             k_stride_head, v_stride_tok, v_stride_head, signs, slot_mapping,
-                            num_tokens, num_kv_heads, head_dim, block_size, ebs, nslots, scale);
+                            (uint32_t)per_kv, num_kv_heads, hmul, head_dim, ebs, nslots, scale);
       break;
     default:
       e = launch_write<256>(vec_ok, grid, s, ks, vs, key, value, in_dtype, k_stride_tok,
                             k_stride_head, v_stride_tok, v_stride_head, signs, slot_mapping,
-                            num_tokens, num_kv_heads, head_dim, block_size, ebs, nslots, scale);
+                            (uint32_t)per_kv, num_kv_heads, hmul, head_dim, ebs, nslots, scale);
   }
   if (e != hipSuccess) {
     set_error("quantize_write: launch failed: %s", hipGetErrorString(e));
