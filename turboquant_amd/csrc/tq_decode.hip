@@ -20,11 +20,14 @@
 //    (row 4*(l/16)+r = token, column l%16 = head) is exactly the B layout of
 //    the PV product v_mfma_f32_16x16x16_f16 (A = V^T: row = dim slot l%16,
 //    k = tokens 4*(l/16)..+3), so probabilities never leave registers.
-//  * 4-bit -> fp16 dequant without memory lookups: the codebook is odd
-//    (c[15-i] = -c[i]); codes are folded to (sign, 3-bit magnitude) with
-//    bit tricks on 8 nibbles at once, magnitudes come from two v_perm_b32
-//    byte tables (high and low byte of the fp16 value), the sign is OR-ed into
-//    the high byte, and v_perm interleaves the bytes into packed fp16 pairs.
+//  * 4-bit -> fp16 dequant through a 256-entry LDS table (code byte -> the
+//    fp16 values of its two nibbles), built once per workgroup from the odd
+//    codebook (c[15-i] = -c[i]) with bit tricks and v_perm_b32 byte tables,
+//    and held in 32 interleaved copies so that the lookups of a wave never
+//    conflict on an LDS bank.
+//  * The cache rows stream into LDS with direct-to-LDS 16-byte copies
+//    (buffer_load ... lds), one workgroup-wide contiguous copy per 1 KB of
+//    rows, through a ring of tile slots, so each cache line is requested once.
 //  * The K norm scales the score; the V norm and 1/sqrt(pd) fold into the
 //    probability, so dequantized operands are (scaled) codebook values.
 //  * Accuracy: q' and the probabilities enter the MFMAs as fp16 hi + lo
@@ -122,17 +125,6 @@ struct DecodeParams {
   float inv_sqrt_pd;  // 1/sqrt(pd)
   float pv_scale;     // 1/(sqrt(pd) * kCbScale)
 };
-
-// 4x4 byte transpose: E_k byte j = byte k of D_j
-__device__ __forceinline__ void transpose4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
-                                           uint32_t* e) {
-  const uint32_t a01 = perm(d1, d0, 0x05010400u), b01 = perm(d1, d0, 0x07030602u);
-  const uint32_t a23 = perm(d3, d2, 0x05010400u), b23 = perm(d3, d2, 0x07030602u);
-  e[0] = perm(a23, a01, 0x05040100u);
-  e[1] = perm(a23, a01, 0x07060302u);
-  e[2] = perm(b23, b01, 0x05040100u);
-  e[3] = perm(b23, b01, 0x07060302u);
-}
 
 __device__ __forceinline__ float xor16_max(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
@@ -358,7 +350,8 @@ __host__ __device__ constexpr int vmcnt_imm(int n) {
 // so that the 16 rows of one chunk column, and rows t and t + 4, fall into
 // distinct bank groups (the pad chunk of a row receives a second copy of
 // the row's last chunk).  NI 1 KB copies fill one region (the last may
-// spill past the rows into the region's slack).  Three slots form the ring.
+// spill past the rows into the region's slack).  kRingSlots slots (two by
+// default) form the ring.
 #ifndef TQ_RING_SLOTS
 #define TQ_RING_SLOTS 2
 #endif
@@ -569,16 +562,16 @@ __device__ __forceinline__ half4_t shl8(half4_t v) {
 
 // Split-KV partials.  Workgroup = (sequence b, split s, group hg of G kv
 // heads), one wave per kv head.  The workgroup streams its heads' cache rows
-// tile by tile (16 tokens x G entries of both slabs) into a ring of three
-// LDS tile slots with direct-to-LDS 16-byte copies: every copy instruction
-// reads 1 KB of consecutive row bytes, so each cache line is requested once
-// by one instruction.  A step is two tiles.  Per step: wait for this wave's
-// copies of the step's tiles (the next tile's copies stay in flight),
-// barrier, each wave reads its own head's codes and norms into registers,
-// barrier, then the copies of the two tiles after the next are issued into
-// the two slots just read, and the math runs while three tiles are in
-// flight.  The step loop is unrolled by three so every slot address is an
-// immediate.
+// tile by tile (16 tokens x G entries of both slabs) into a ring of
+// kRingSlots LDS tile slots with direct-to-LDS 16-byte copies: every copy
+// instruction reads 1 KB of consecutive row bytes, so each cache line is
+// requested once by one instruction.  A step is two tiles.  Per step: wait
+// for the copies of the step's tiles (the waves share the copies, so each
+// wave waits for its own and the barrier that follows makes all of them
+// visible), barrier, each wave reads its own head's codes and norms into
+// registers, barrier, then the copies of the tiles kRingSlots ahead are
+// issued into the two slots just read, and the math runs while they are in
+// flight.  Slot bases are runtime values (advanced by two slots per step).
 template <int PD, int G, int PACK, bool QC>
 __global__ __launch_bounds__(64 * G)
 __attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : (PACK == 1 ? 3 : 4))))
@@ -591,7 +584,7 @@ void decode_partials_kernel(DecodeParams p) {
   constexpr int CPT = RG::CPT;
   constexpr int NI = RG::NI;
   // LDS: the dequant table at address 0 (the table reads rely on it), then
-  // the ring of three tile slots
+  // the ring of tile slots
   struct __attribute__((aligned(16))) Lds {
     uint32_t klut[256 * kLutCopies];
     uint8_t ring[RG::RING];
