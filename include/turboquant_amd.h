@@ -94,10 +94,8 @@ int tq_decode_paged_splitkv(const void* q, int64_t q_stride_b, int64_t q_stride_
 /*
  * The first kernel of tq_decode_paged_splitkv alone (the reference's v5 split
  * kernel, v5_tc.cuh:106-795): writes partition_o (normalised, rotated domain)
- * and partition_lse (natural log; -inf for an empty split).  When
- * (num_qo_heads / num_kv_heads) * padded_dim <= 1024 and padded_dim >= 128,
- * one workgroup serves splits 2j and 2j+1 and writes their merged result to
- * row 2j; row 2j+1 gets lse = -inf (tq_combine_splits accepts either form).
+ * and partition_lse (natural log; -inf for an empty split) of split s =
+ * tokens [s * kv_chunk_size, min((s + 1) * kv_chunk_size, seq_len)).
  */
 int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                        const uint8_t* k_slab, const uint8_t* v_slab,
