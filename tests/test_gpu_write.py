@@ -154,3 +154,33 @@ def test_write_kat_vectors():
         got = _gpu_cache(shape, x[:, None, :], x[:, None, :], np.arange(n, dtype=np.int32), hd, pd)
         k_entries = got[0].reshape(-1, shape[-1])[:n, :e.shape[1]]
         assert np.array_equal(k_entries, e), f"hd {hd}: {_diff_report(k_entries, e)}"
+
+
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_write_nonfinite_and_extreme_rows(hd):
+    """Rows holding inf, -inf, NaN, fp16 max and subnormals: the codes match the
+    oracle bit for bit (NaN after the rotation -> code 0 everywhere); norms
+    match, or are both NaN."""
+    print(f"case: write non-finite rows hd={hd}", flush=True)
+    rng = np.random.default_rng(40 + hd)
+    n, h, nb = 32, 2, 4
+    k, v = W.write_inputs(rng, n, h, hd)
+    k[0, 0, 3] = np.inf
+    k[1, 1, 0] = -np.inf
+    k[2, 0, hd - 1] = np.nan
+    v[3, 0, :] = np.float16(65504.0)
+    v[4, 1, :] = np.float16(-65504.0)
+    v[5, 0, :] = np.float16(6e-8)
+    v[6, 1, ::2] = np.float16(-6e-8)
+    k[7, 0, :] = np.float16(-0.0)
+    slots = np.arange(n, dtype=np.int32)
+    shape, pd = W.cache_bytes(nb, h, hd)
+    ref = _oracle_cache(shape, k, v, slots, hd, pd)
+    got = _gpu_cache(shape, k, v, slots, hd, pd)
+    qb = pd // 2
+    assert np.array_equal(ref[..., :qb], got[..., :qb]), _diff_report(ref[..., :qb], got[..., :qb])
+    nr = ref[..., qb:qb + 2 * (pd // 64)].copy().view(np.float16)
+    ng = got[..., qb:qb + 2 * (pd // 64)].copy().view(np.float16)
+    same = (nr.view(np.uint16) == ng.view(np.uint16)) | (np.isnan(nr) & np.isnan(ng))
+    assert same.all()
+    assert (got[0].reshape(-1, h, shape[-1])[0, 0, :qb] == 0).all()  # the inf row
