@@ -29,7 +29,7 @@ HBM_PEAK_GBS = 8000.0
 # from rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), each scale taken from a
 # 256 MiB device copy (profiles/decode_partials_cfg3_hbm_traffic.md); keyed by
 # (num_splits, kv_chunk_size) so an overridden layout reports null.
-PROFILED_TRAFFIC = {(64, 512): 344753945}
+PROFILED_TRAFFIC = {(64, 512): 346478388}
 
 
 def log(msg):

