@@ -4,6 +4,10 @@
   csrc/src/quantize_write_binding.cu:285-286 (reference).
 * ``torch.ops.turboquant_v5.decode_v5_from_cache_paged_splitkv_ws`` — schema of
   csrc/src/decode_v5_tc_binding.cu:966-973 (reference).
+* ``torch.ops.turboquant_v5.decode_v5_from_cache_ws`` and
+  ``decode_v5_from_cache_splitkv_ws`` — schemas of decode_v5_tc_binding.cu:948-964,
+  the non-split (graph-safe) and gather-then-split ops the reference backend
+  and tests call; ``decode_v5_from_cache`` is the eager (allocating) form.
 
 Both launch on the current torch stream, allocate nothing and never sync, so
 they can be captured in a HIP graph.  They have a CUDA (= HIP on ROCm) kernel
@@ -160,6 +164,105 @@ def _reference_paged_splitkv(q, kv_cache, indices, indptr, last_page_len, seq_le
                                 o_ws, partition_o_ws, partition_lse_ws, int(num_splits), cs)
 
 
+def _check_gather_ws(q, num_kv_heads, max_len, qbytes, padded_dim, k_quant_ws, v_quant_ws,
+                     k_norms_ws, v_norms_ws, o_ws):
+    """The workspace checks of decode_v5_from_cache_ws
+    (decode_v5_tc_binding.cu:466-478), kept so that callers sized for the
+    reference are accepted or refused alike."""
+    b, hq = q.size(0), q.size(1)
+    dc = int(padded_dim) // 64
+    if int(max_len) <= 0:
+        raise RuntimeError("max_len must be positive")
+    if tuple(k_quant_ws.shape) != (b, int(num_kv_heads), int(max_len), int(qbytes)):
+        raise RuntimeError("k_quant_ws shape mismatch")
+    if tuple(v_quant_ws.shape) != tuple(k_quant_ws.shape):
+        raise RuntimeError("v_quant_ws shape mismatch")
+    if tuple(k_norms_ws.shape) != (b, int(num_kv_heads), int(max_len), dc):
+        raise RuntimeError("k_norms_ws shape mismatch")
+    if tuple(v_norms_ws.shape) != tuple(k_norms_ws.shape):
+        raise RuntimeError("v_norms_ws shape mismatch")
+    if tuple(o_ws.shape) != (b, hq, int(padded_dim)):
+        raise RuntimeError("o_ws shape mismatch")
+
+
+def _scratch_f32(t: torch.Tensor, n: int):
+    """n fp32 elements at the start of a contiguous caller-owned buffer, or None."""
+    if not t.is_contiguous() or t.numel() * t.element_size() < 4 * n or t.data_ptr() % 16:
+        return None
+    return t.view(-1).view(torch.uint8)[:4 * n].view(torch.float32)
+
+
+def _from_cache_ws(q, kv_cache, indices, indptr, last_page_len, seq_lens, num_kv_heads,
+                   page_size, head_dim, padded_dim, sm_scale, hadamard_signs, qbytes, nbytes,
+                   k_quant_ws, v_quant_ws, k_norms_ws, v_norms_ws, o_ws, max_len):
+    """decode_v5_from_cache_ws (decode_v5_tc_binding.cu:439-551): the reference
+    gathers the pages into contiguous K/V workspaces and runs one unsplit
+    kernel.  Here the paged kernel reads the pages directly, so the gather
+    workspaces are free; they hold the split partials instead (the op owns
+    their contents during the call, as the reference's gather does), which
+    keeps the split-KV layout without any allocation.  Tokens are read up to
+    min(seq_lens[b], num_splits * kv_chunk_size) with num_splits *
+    kv_chunk_size >= max_len."""
+    from .geometry import CHUNK_ALIGN, choose_splits
+    _check_gather_ws(q, num_kv_heads, max_len, qbytes, padded_dim, k_quant_ws, v_quant_ws,
+                     k_norms_ws, v_norms_ws, o_ws)
+    b, hq, pd = q.size(0), q.size(1), int(padded_dim)
+    splits, chunk = choose_splits(b, int(max_len), int(num_kv_heads), hq, pd)
+    while True:
+        po = _scratch_f32(k_quant_ws, b * splits * hq * pd)
+        pl = _scratch_f32(v_quant_ws, b * splits * hq)
+        if (po is not None and pl is not None) or splits == 1:
+            break
+        splits = max(1, splits // 2)
+        chunk = -(-int(max_len) // splits)
+        chunk = (chunk + CHUNK_ALIGN - 1) // CHUNK_ALIGN * CHUNK_ALIGN
+        splits = -(-int(max_len) // chunk)
+    if po is None or pl is None:
+        raise RuntimeError("decode_v5_from_cache_ws: workspaces too small for the partials")
+    return decode_paged_splitkv(q, kv_cache, indices, indptr, seq_lens, int(num_kv_heads),
+                                int(head_dim), pd, float(sm_scale), hadamard_signs, o_ws, po,
+                                pl, splits, chunk)
+
+
+def _from_cache_splitkv_ws(q, kv_cache, indices, indptr, last_page_len, seq_lens, num_kv_heads,
+                           page_size, head_dim, padded_dim, sm_scale, hadamard_signs, qbytes,
+                           nbytes, k_quant_ws, v_quant_ws, k_norms_ws, v_norms_ws, o_ws, max_len,
+                           partition_o_ws, partition_lse_ws, request_indices, kv_tile_indices,
+                           split_indptr, kv_chunk_size_t, num_splits):
+    """decode_v5_from_cache_splitkv_ws (decode_v5_tc_binding.cu:586-752): the
+    gather-then-split variant.  The paged kernel needs no gather, so this is
+    the paged split op with the caller's partition workspaces."""
+    _check_gather_ws(q, num_kv_heads, max_len, qbytes, padded_dim, k_quant_ws, v_quant_ws,
+                     k_norms_ws, v_norms_ws, o_ws)
+    return _reference_paged_splitkv(q, kv_cache, indices, indptr, last_page_len, seq_lens,
+                                    num_kv_heads, page_size, head_dim, padded_dim, sm_scale,
+                                    hadamard_signs, qbytes, nbytes, o_ws, max_len, partition_o_ws,
+                                    partition_lse_ws, request_indices, kv_tile_indices,
+                                    split_indptr, kv_chunk_size_t, num_splits)
+
+
+def decode_v5_from_cache(q, kv_cache, indices, indptr, last_page_len, seq_lens, num_kv_heads,
+                         page_size, head_dim, padded_dim, sm_scale, hadamard_signs, qbytes,
+                         nbytes):
+    """The eager decode_v5_from_cache (decode_v5_tc_binding.cu:324-423): it
+    allocates its own output and workspaces (not graph-capturable, as in the
+    reference); max_len is the page-table width times page_size."""
+    from .geometry import choose_splits
+    b, hq, pd = q.size(0), q.size(1), int(padded_dim)
+    if b and indptr.numel() > 1:
+        max_len = int(indptr[1] - indptr[0]) * int(page_size)
+    else:
+        max_len = int(page_size)
+    max_len = max(max_len, int(page_size))
+    splits, chunk = choose_splits(b, max_len, int(num_kv_heads), hq, pd)
+    o = torch.empty((b, hq, pd), dtype=torch.float16, device=q.device)
+    po = torch.empty((b * splits, hq, pd), dtype=torch.float32, device=q.device)
+    pl = torch.empty((b * splits, hq), dtype=torch.float32, device=q.device)
+    return decode_paged_splitkv(q, kv_cache, indices, indptr, seq_lens, int(num_kv_heads),
+                                int(head_dim), pd, float(sm_scale), hadamard_signs, o, po, pl,
+                                splits, chunk)
+
+
 def register_ops() -> None:
     """Define turboquant_write::* and turboquant_v5::* with the reference
     schemas and bind the HIP implementations to the CUDA dispatch key."""
@@ -181,5 +284,22 @@ def register_ops() -> None:
              "Tensor request_indices, Tensor kv_tile_indices, "
              "Tensor split_indptr, Tensor kv_chunk_size_t, int num_splits) -> Tensor")
     d.impl("decode_v5_from_cache_paged_splitkv_ws", _reference_paged_splitkv, "CUDA")
+    d.define("decode_v5_from_cache_ws(Tensor q, Tensor kv_cache, Tensor indices, "
+             "Tensor indptr, Tensor last_page_len, Tensor seq_lens, "
+             "int num_kv_heads, int page_size, int head_dim, int padded_dim, "
+             "float sm_scale, Tensor hadamard_signs, int qbytes, int nbytes, "
+             "Tensor k_quant_ws, Tensor v_quant_ws, Tensor k_norms_ws, "
+             "Tensor v_norms_ws, Tensor o_ws, int max_len) -> Tensor")
+    d.impl("decode_v5_from_cache_ws", _from_cache_ws, "CUDA")
+    d.define("decode_v5_from_cache_splitkv_ws(Tensor q, Tensor kv_cache, Tensor indices, "
+             "Tensor indptr, Tensor last_page_len, Tensor seq_lens, "
+             "int num_kv_heads, int page_size, int head_dim, int padded_dim, "
+             "float sm_scale, Tensor hadamard_signs, int qbytes, int nbytes, "
+             "Tensor k_quant_ws, Tensor v_quant_ws, Tensor k_norms_ws, "
+             "Tensor v_norms_ws, Tensor o_ws, int max_len, "
+             "Tensor partition_o_ws, Tensor partition_lse_ws, "
+             "Tensor request_indices, Tensor kv_tile_indices, "
+             "Tensor split_indptr, Tensor kv_chunk_size_t, int num_splits) -> Tensor")
+    d.impl("decode_v5_from_cache_splitkv_ws", _from_cache_splitkv_ws, "CUDA")
     _libs.extend([w, d])
     _registered = True
