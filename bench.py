@@ -176,6 +176,24 @@ def bench_write(torch, steps, warmup):
                                            "permuted slots (configs[1])"}
 
 
+def bench_dequant(torch, w, steps, warmup):
+    """tq_dequant_paged (the read-back of cached context for a prefill chunk)
+    over one configs[2] sequence: 32768 tokens x 8 heads of K and V back to
+    fp16 rows.  Algorithmic bytes: the entries' codes + norms read
+    (2 x 68 B per token and head) plus the fp16 rows written (2 x 256 B)."""
+    from turboquant_amd import ops
+    L, hkv, hd, pd = w["seq_len"], w["hkv"], w["hd"], w["pd"]
+    pages = w["bt"][0].contiguous()
+    ok = torch.empty((L, hkv, hd), dtype=torch.float16, device=w["q"].device)
+    ov = torch.empty_like(ok)
+    ms = time_graph(torch, lambda: ops.dequant_paged(w["cache"], pages, L, hkv, hd, pd,
+                                                     w["signs"], ok, ov), steps, warmup)
+    nbytes = L * hkv * 2 * (pd // 2 + 2 * (pd // 64)) + L * hkv * 2 * hd * 2 + (L // 16) * 4
+    return {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "alg_bytes": nbytes, "config": f"{L} cached tokens x {hkv} heads x {hd}, K+V "
+                                           "(one configs[2] sequence), fp16 rows out"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -252,6 +270,8 @@ def main():
     layout_bytes = b * w["seq_len"] * w["hkv"] * 2 * w["ebs"]
     wr = bench_write(torch, args.steps, args.warmup)
     log(f"write kernel {wr['us']} us -> {wr['GB/s']} GB/s")
+    dq = bench_dequant(torch, w, args.steps, args.warmup)
+    log(f"dequant kernel {dq['us']} us -> {dq['GB/s']} GB/s")
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle) ...")
@@ -287,6 +307,7 @@ def main():
                      "alg_bytes": nbytes},
         "cpu_baseline": cpu,
         "write_kernel": wr,
+        "dequant_kernel": dq,
     }
     print(json.dumps(line), flush=True)
 

@@ -119,6 +119,26 @@ int tq_combine_splits(const float* partition_o, const float* partition_lse,
                       int32_t padded_dim, const float* signs, void* o,
                       tq_stream_t stream);
 
+/*
+ * Read cached K/V back: the packed entries of tokens [0, num_tokens) of one
+ * sequence (token t = page pages[t / block_size], entry t % block_size) as fp16
+ * rows in the original domain, x = s * FWHT(c[code] * norm / sqrt(pd)) / sqrt(pd)
+ * (no rotation when signs == NULL).  out_k / out_v: fp16, element (t, h, d) at
+ * out + t * out_stride_tok + h * head_dim + d, d < head_dim.  Pages outside
+ * [0, num_blocks) give zeros.
+ *
+ * Serves the prefill of a chunk whose sequence has cached context; the
+ * reference's prefill (turboquant/vllm_backend_fused.py:335-371) attends the
+ * fresh chunk only and has no counterpart.  The dequantization is the one its
+ * decode reference applies (turboquant/triton_decode_ref.py:89-131).
+ */
+int tq_dequant_paged(const uint8_t* k_slab, const uint8_t* v_slab,
+                     const int32_t* pages, int64_t num_tokens, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t padded_dim, int32_t block_size,
+                     int32_t ebs, int64_t num_blocks, const float* signs,
+                     void* out_k, void* out_v, int64_t out_stride_tok,
+                     tq_stream_t stream);
+
 /* Message for the last non-zero return of a tq_* call on this thread. */
 const char* tq_last_error(void);
 

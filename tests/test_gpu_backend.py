@@ -77,3 +77,100 @@ def test_backend_prefill_fresh_attention():
             ref = torch.softmax(s, -1) @ vv
             got = out.float().cpu().view(n, hq, hd)[a:b, h]
             assert torch.allclose(got, ref, atol=2e-2), (a, h)
+
+
+@pytest.mark.parametrize("hq,hkv,hd", [(32, 8, 128), (8, 2, 64)])
+def test_backend_mixed_batch_with_cached_context(hq, hkv, hd):
+    """A max_query_len > 1 batch: a fresh prompt, two chunks of longer prompts
+    whose earlier tokens are already cached, and a decode row.  Chunks attend
+    the dequantized cached context plus their fresh K/V (causal); the decode
+    row attends the dequantized cache; the fresh prompt its own K/V.  All
+    against a float64 reference (tests/npref.py dequantization)."""
+    print(f"case: backend mixed batch {hq}/{hkv}/{hd}", flush=True)
+    import oracle
+    from tests import npref
+    from turboquant_amd.geometry import hadamard_signs, padded_dim
+    from turboquant_amd.vllm_backend_fused import TurboQuantBackend, TurboQuantFusedImpl
+    dev = G.DEV
+    rng = np.random.default_rng(hd + hq)
+    ctxs = [0, 300, 500, 16]
+    qls = [20, 37, 1, 5]
+    lens = [c + q for c, q in zip(ctxs, qls)]
+    bt, slots, nb = W.paged_layout(rng, lens)
+    n_all = int(sum(lens))
+    k_all, v_all = W.write_inputs(rng, n_all, hkv, hd)
+    q_new = rng.standard_normal((sum(qls), hq, hd)).astype(np.float16)
+    shape = TurboQuantBackend.get_kv_cache_shape(nb, W.BLOCK, hkv, hd, "fp8")
+    cache = torch.zeros(shape, dtype=torch.uint8, device=dev)
+    scale = 1.0 / np.sqrt(hd)
+    impl = TurboQuantFusedImpl(hq, hd, scale, hkv, None, None, "fp8")
+    impl.do_kv_cache_update(None, torch.from_numpy(k_all).to(dev), torch.from_numpy(v_all).to(dev),
+                            cache, torch.from_numpy(slots).to(dev))
+    # the batch's new tokens are the last qls[i] tokens of each request
+    starts = np.concatenate([[0], np.cumsum(lens)])
+    new_idx = np.concatenate([np.arange(starts[i] + ctxs[i], starts[i + 1]) for i in range(4)])
+    kn = torch.from_numpy(k_all[new_idx]).to(dev).view(-1, hkv * hd)
+    vn = torch.from_numpy(v_all[new_idx]).to(dev).view(-1, hkv * hd)
+    qn = torch.from_numpy(q_new).to(dev).view(-1, hq * hd)
+    qsl = np.concatenate([[0], np.cumsum(qls)]).astype(np.int32)
+    meta = Meta(max(qls), int(sum(qls)), torch.from_numpy(bt).to(dev),
+                torch.tensor(lens, dtype=torch.int32, device=dev),
+                torch.from_numpy(qsl).to(dev), None)
+    out = impl.forward(None, qn, kn, vn, cache, meta)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy().reshape(-1, hq, hd)
+
+    pd = padded_dim(hd)
+    signs = hadamard_signs(pd).numpy()
+    cb = oracle.codebook()
+    cache_np = cache.cpu().numpy()
+    indptr = np.arange(5, dtype=np.int32) * bt.shape[1]
+    ref = np.zeros_like(got, dtype=np.float64)
+    g = hq // hkv
+    for i in range(4):
+        a, b = qsl[i], qsl[i + 1]
+        for kvh in range(hkv):
+            ke, ve = npref.gather_entries(cache_np, bt.reshape(-1), indptr, lens[i], i, kvh)
+            kd = npref.dequant_original(ke, pd, signs, cb)[:, :hd]
+            vd = npref.dequant_original(ve, pd, signs, cb)[:, :hd]
+            fk = k_all[starts[i] + ctxs[i]:starts[i + 1], kvh].astype(np.float64)
+            fv = v_all[starts[i] + ctxs[i]:starts[i + 1], kvh].astype(np.float64)
+            if qls[i] == 1 and ctxs[i] > 0:  # decode row: the whole cache
+                K, V = kd, vd
+            else:  # cached context, then the fresh chunk
+                K = np.concatenate([kd[:ctxs[i]], fk])
+                V = np.concatenate([vd[:ctxs[i]], fv])
+            for r in range(g):
+                h = kvh * g + r
+                for j in range(qls[i]):
+                    vis = ctxs[i] + j + 1
+                    s = K[:vis] @ q_new[a + j, h].astype(np.float64) * scale
+                    p = np.exp(s - s.max())
+                    ref[a + j, h] = p @ V[:vis] / p.sum()
+    G.assert_close(got, ref, "mixed batch")
+
+
+def test_dequant_paged_matches_float64_dequantization():
+    print("case: dequant_paged", flush=True)
+    import oracle
+    from tests import npref
+    from turboquant_amd import ops
+    from turboquant_amd.geometry import hadamard_signs, padded_dim
+    for hd, hkv in ((128, 8), (64, 4), (256, 2), (96, 2)):
+        c = W.decode_case(200 + hd, 1, [333], 4 * hkv, hkv, hd)
+        cache, pd = G.build_cache(c)
+        pages = torch.from_numpy(c["block_table"][0]).to(G.DEV).contiguous()
+        out_k = torch.full((340, hkv, hd), 7.0, dtype=torch.float16, device=G.DEV)
+        out_v = torch.full_like(out_k, 7.0)
+        signs = hadamard_signs(pd, G.DEV)
+        ops.dequant_paged(cache, pages, 333, hkv, hd, pd, signs, out_k, out_v)
+        torch.cuda.synchronize()
+        cache_np = cache.cpu().numpy()
+        indptr = np.array([0, c["block_table"].shape[1]], np.int32)
+        for kvh in range(hkv):
+            ke, ve = npref.gather_entries(cache_np, c["block_table"].reshape(-1), indptr, 333, 0, kvh)
+            for ent, got in ((ke, out_k), (ve, out_v)):
+                want = npref.dequant_original(ent, pd, signs.cpu().numpy(), oracle.codebook())[:, :hd]
+                g = got[:333, kvh].float().cpu().numpy()
+                assert np.abs(g - want).max() <= 2e-3 * max(1.0, np.abs(want).max()), hd
+        assert (out_k[333:] == 7.0).all()  # rows past num_tokens untouched

@@ -128,6 +128,49 @@ def decode_paged_splitkv(q: torch.Tensor, kv_cache: torch.Tensor, indices: torch
     return o
 
 
+def dequant_paged(kv_cache: torch.Tensor, pages: torch.Tensor, num_tokens: int,
+                  num_kv_heads: int, head_dim: int, padded_dim: int,
+                  signs: torch.Tensor | None, out_k: torch.Tensor, out_v: torch.Tensor) -> None:
+    """Cached K/V of tokens [0, num_tokens) of one sequence (its page-table
+    row `pages`) as fp16 rows [num_tokens, H_kv, head_dim] in the original
+    domain, written into out_k / out_v (rows may be strided, heads and dims
+    contiguous)."""
+    _require_gpu(kv_cache, pages, out_k, out_v)
+    if kv_cache.dim() != 5 or kv_cache.size(0) != 2 or not kv_cache.is_contiguous():
+        raise RuntimeError("kv_cache must be contiguous [2, num_blocks, block_size, H, ebs]")
+    _, nb, bs, hk, _ = kv_cache.shape
+    if hk != num_kv_heads:
+        raise RuntimeError(f"kv_cache has {hk} kv heads, num_kv_heads={num_kv_heads}")
+    if pages.dtype != torch.int32 or not pages.is_contiguous():
+        raise RuntimeError("pages must be a contiguous int32 tensor")
+    if num_tokens > pages.numel() * bs:
+        raise RuntimeError("pages do not cover num_tokens")
+    for t in (out_k, out_v):
+        if (t.dtype != torch.float16 or t.dim() != 3 or t.size(0) < num_tokens
+                or t.size(1) != num_kv_heads or t.size(2) != head_dim or t.stride(2) != 1
+                or t.stride(1) != head_dim or t.stride(0) != out_k.stride(0)):
+            raise RuntimeError("out_k / out_v must be fp16 [>= num_tokens, H_kv, head_dim] "
+                               "with contiguous heads and one row stride")
+    if num_tokens == 0:
+        return
+    ebs = kv_cache.size(-1) * kv_cache.element_size()
+    sp = 0
+    if signs is not None and signs.numel() > 0:
+        if signs.dtype != torch.float32 or signs.numel() < padded_dim:
+            raise RuntimeError("signs must be fp32 [padded_dim]")
+        _require_gpu(signs)
+        sp = signs.data_ptr()
+    lib = _lib.load()
+    base = kv_cache.data_ptr()
+    slab = nb * bs * hk * ebs
+    with torch.cuda.device(kv_cache.device):
+        rc = lib.tq_dequant_paged(base, base + slab, pages.data_ptr(), int(num_tokens),
+                                  int(num_kv_heads), int(head_dim), int(padded_dim), bs, ebs, nb,
+                                  sp, out_k.data_ptr(), out_v.data_ptr(), out_k.stride(0),
+                                  _stream_ptr(kv_cache.device))
+    _lib.check(rc, "dequant_paged")
+
+
 # --------------------------------------------------------------------------
 # torch.library registration under the reference's namespaces and schemas
 # --------------------------------------------------------------------------

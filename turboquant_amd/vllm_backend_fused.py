@@ -129,8 +129,9 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
     Write: do_kv_cache_update -> turboquant_write::quantize_write_kv_cache.
     Decode: forward (max_query_len == 1) ->
             turboquant_v5::decode_v5_from_cache_paged_splitkv_ws.
-    Prefill: attention over the fresh K/V of the batch (the reference's
-    prefill ignores cached context too, vllm_backend_fused.py:335-371).
+    Prefill / mixed batches: _prefill_mixed (decode rows through the decode
+    kernel, chunks with cached context over the dequantized context plus the
+    fresh chunk, fresh prompts as in the reference, vllm_backend_fused.py:335-371).
     """
 
     def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes,
@@ -245,6 +246,82 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
             output[a:b] = o.squeeze(0).transpose(0, 1).to(output.dtype)
         return output
 
+    def _prefill_mixed(self, query, key, value, kv_cache, attn_metadata, output):
+        """A batch with max_query_len > 1 whose cache already holds every token
+        of the batch (do_kv_cache_update runs first).  Per request with q_len
+        new tokens and seq_len tokens in all, ctx = seq_len - q_len:
+
+        * q_len == 1 and ctx > 0 (decode rows of a mixed batch): the decode
+          kernel over the cache, as in a pure decode batch;
+        * ctx == 0 (a fresh prompt): causal attention over the fresh K/V,
+          the reference's prefill (vllm_backend_fused.py:335-371);
+        * ctx > 0 (a chunk of a longer prompt): the ctx cached tokens read back
+          from the quantized cache (tq_dequant_paged) followed by the chunk's
+          fresh K/V, causal within the chunk.  The reference attends the fresh
+          chunk only and so drops the cached context; its decode path already
+          attends over the dequantized cache, which this extends to chunks.
+        """
+        from . import ops
+        self._ensure_kernels_loaded()
+        self._ensure(query.device)
+        qsl = attn_metadata.query_start_loc.tolist()
+        seq = attn_metadata.seq_lens.tolist()
+        bt = attn_metadata.block_table
+        g = self.num_heads // self.num_kv_heads
+        dec = []
+        for i in range(len(qsl) - 1):
+            a, b = qsl[i], qsl[i + 1]
+            ql = b - a
+            if ql <= 0:
+                continue
+            ctx = int(seq[i]) - ql
+            if ctx < 0:
+                raise RuntimeError(f"request {i}: seq_len {seq[i]} < query length {ql}")
+            if ql == 1 and ctx > 0:
+                dec.append(i)
+                continue
+            q = query[a:b].to(torch.float16).transpose(0, 1).unsqueeze(0)
+            if ctx == 0:
+                kk = key[a:b].to(torch.float16)
+                vv = value[a:b].to(torch.float16)
+                mask = None
+            else:
+                kk = torch.empty((ctx + ql, self.num_kv_heads, self.head_size),
+                                 dtype=torch.float16, device=query.device)
+                vv = torch.empty_like(kk)
+                pages = bt[i].to(torch.int32).contiguous()
+                ops.dequant_paged(kv_cache, pages, ctx, self.num_kv_heads, self.head_size,
+                                  self._pd, self._signs, kk, vv)
+                kk[ctx:] = key[a:b]
+                vv[ctx:] = value[a:b]
+                r = torch.arange(ql, device=query.device)[:, None]
+                c = torch.arange(ctx + ql, device=query.device)[None, :]
+                mask = c <= r + ctx
+            kt = kk.transpose(0, 1).repeat_interleave(g, dim=0).unsqueeze(0)
+            vt = vv.transpose(0, 1).repeat_interleave(g, dim=0).unsqueeze(0)
+            if mask is None:
+                o = F.scaled_dot_product_attention(q, kt, vt, is_causal=True, scale=self.scale)
+            else:
+                o = F.scaled_dot_product_attention(q, kt, vt, attn_mask=mask, scale=self.scale)
+            output[a:b] = o.squeeze(0).transpose(0, 1).to(output.dtype)
+        if dec:
+            rows = torch.tensor([qsl[i] for i in dec], dtype=torch.long, device=query.device)
+            idx = torch.tensor(dec, dtype=torch.long, device=query.device)
+            q = query.index_select(0, rows).to(torch.float16)
+            if self.head_size < self._pd:
+                q = F.pad(q, (0, self._pd - self.head_size))
+            q = q.contiguous()
+            sub_bt = bt.index_select(0, idx).to(torch.int32).contiguous()
+            sl = attn_metadata.seq_lens.index_select(0, idx).to(torch.int32).contiguous()
+            nbt = sub_bt.shape[1]
+            indptr = torch.arange(len(dec) + 1, dtype=torch.int32, device=query.device) * nbt
+            o = ops.decode_v5_from_cache(q, kv_cache, sub_bt.reshape(-1), indptr, sl, sl,
+                                         self.num_kv_heads, kv_cache.shape[2], self.head_size,
+                                         self._pd, self.scale, self._signs, self._qbytes,
+                                         self._nbytes)
+            output.index_copy_(0, rows, o[:, :, :self.head_size].to(output.dtype))
+        return output
+
     @torch.no_grad()
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
                 output_scale=None, **kwargs):
@@ -263,7 +340,10 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
                 k = key[:num_tokens].view(num_tokens, self.num_kv_heads, self.head_size)
                 v = value[:num_tokens].view(num_tokens, self.num_kv_heads, self.head_size)
                 out3 = output[:num_tokens].view(num_tokens, self.num_heads, self.head_size)
-                self._prefill_fresh(q, k, v, attn_metadata, out3)
+                if kv_cache is None or attn_metadata.seq_lens is None:
+                    self._prefill_fresh(q, k, v, attn_metadata, out3)
+                else:
+                    self._prefill_mixed(q, k, v, kv_cache, attn_metadata, out3)
                 return output
             return super().forward(layer, query, key, value, kv_cache, attn_metadata,
                                    output, output_scale, **kwargs)
