@@ -1,0 +1,182 @@
+"""The algorithm library (turboquant_amd.algorithm) against the bounds and
+known answers of the reference's tests/test_algorithm.py (bit packing,
+FWHT, rotation, codebooks, QJL unbiasedness, MSE distortion table, Prod
+unbiasedness, attention quality), plus pins that do not depend on the
+reference: the Hadamard matrix, the Lloyd-Max centroids, the cache signs.
+CPU; a GPU twin runs in tests/test_gpu_algorithm.py."""
+import math
+
+import numpy as np
+import pytest
+import torch
+from scipy.linalg import hadamard
+
+from turboquant_amd import algorithm as A
+from turboquant_amd.geometry import hadamard_signs
+
+DEV = "cpu"
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_pack_roundtrip_and_size(bits):
+    g = torch.Generator().manual_seed(bits)
+    idx = torch.randint(0, 1 << bits, (10, 128), generator=g, dtype=torch.uint8)
+    p = A.pack_bits(idx, bits)
+    per = 8 // bits
+    assert p.shape[-1] == -(-128 // per)
+    assert torch.equal(A.unpack_bits(p, bits, 128), idx)
+    # odd length pads with zeros
+    q = A.pack_bits(idx[:, :5], bits)
+    assert torch.equal(A.unpack_bits(q, bits, 5), idx[:, :5])
+
+
+def test_pack_layout_low_bits_first():
+    idx = torch.tensor([[1, 2, 3, 0, 1, 1, 0, 3]], dtype=torch.uint8)
+    assert A.pack_bits(idx, 2).tolist() == [[1 | 2 << 2 | 3 << 4, 1 | 1 << 2 | 3 << 6]]
+    assert A.pack_bits(torch.tensor([[5, 3]], dtype=torch.uint8), 3).tolist() == [[5 | 3 << 3]]
+    assert A.pack_bits(torch.tensor([[0xA, 0x5]], dtype=torch.uint8), 4).tolist() == [[0x5A]]
+
+
+def test_fwht_known_answer_and_matrix():
+    y = A.fwht(torch.tensor([1.0, 0.0, 0.0, 0.0]))
+    assert torch.allclose(y, torch.full((4,), 0.5), atol=1e-6)
+    x = torch.randn(3, 64, generator=torch.Generator().manual_seed(1), dtype=torch.float64)
+    want = x @ torch.from_numpy(hadamard(64).astype(np.float64)).T / 8.0
+    assert torch.allclose(A.fwht(x), want, atol=1e-12)
+    z = torch.randn(128)
+    assert torch.allclose(A.fwht(A.fwht(z)), z, atol=1e-5)
+    with pytest.raises(AssertionError):
+        A.fwht(torch.zeros(12))
+
+
+def test_rotation_roundtrip_padding_and_signs():
+    rot = A.RandomHadamardRotation(100, device=DEV, seed=0)
+    assert rot.padded_dim == 128
+    x = torch.randn(5, 100)
+    y = rot.rotate(x)
+    assert y.shape == (5, 128)
+    assert torch.allclose(y.norm(dim=-1), x.norm(dim=-1), atol=1e-5)
+    assert torch.allclose(rot.inverse_rotate(y), x, atol=1e-5)
+    # seed 42 gives the cache's signs
+    assert torch.equal(A.RandomHadamardRotation(128, device=DEV).signs, hadamard_signs(128))
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_codebook_levels_symmetry_and_lloyd_max(bits):
+    cb = A.Codebook(128, bits, device=DEV)
+    assert cb.centroids.numel() == 1 << bits and cb.boundaries.numel() == (1 << bits) - 1
+    assert torch.allclose(cb.centroids + cb.centroids.flip(0), torch.zeros_like(cb.centroids),
+                          atol=1e-7)
+    x = torch.randn(1000) / math.sqrt(128)
+    idx = cb.quantize(x)
+    assert int(idx.min()) >= 0 and int(idx.max()) < (1 << bits)
+    # Lloyd-Max: each centroid is the N(0,1) mean of its cell (to 5e-4)
+    from scipy import stats
+    c = np.array(A._levels(bits))
+    b = np.concatenate([[-np.inf], (c[:-1] + c[1:]) / 2, [np.inf]])
+    mean = (stats.norm.pdf(b[:-1]) - stats.norm.pdf(b[1:])) / (stats.norm.cdf(b[1:]) -
+                                                                stats.norm.cdf(b[:-1]))
+    assert np.abs(mean - c).max() < 5e-4
+
+
+def test_codebook_4bit_equals_cache_codebook_and_ties_go_down():
+    import oracle
+    cb = A.Codebook(1, 4, device=DEV)  # scale 1: the N(0,1) values
+    # the float64 table rounded to fp32 (as the reference's Codebook does) is
+    # within 2 ulp of the cache kernels' 7-digit fp32 literals
+    # (page_turbo.cuh:18-23); the boundaries are the same fp32 values
+    ulp = (cb.centroids.numpy().view(np.int32) - oracle.codebook().view(np.int32))
+    assert np.abs(ulp).max() <= 2
+    assert torch.equal(cb.boundaries, torch.from_numpy(oracle.boundaries()))
+    assert int(cb.quantize(cb.boundaries[3:4])) == 3  # a boundary takes the lower bucket
+
+
+def test_qjl_unbiased():
+    d = 128
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(d, generator=g)
+    x = x / x.norm()
+    y = torch.randn(d, generator=g)
+    est = []
+    for seed in range(200):
+        q = A.QJL(d, device=DEV, seed=seed)
+        s = q.quantize(x.unsqueeze(0))
+        assert s.dtype == torch.int8 and set(s.unique().tolist()) <= {-1, 1}
+        est.append(float(y @ q.dequantize_inner_product(s, torch.ones(1))[0]))
+    assert abs(np.mean(est) - float(x @ y)) < 0.15
+
+
+@pytest.mark.parametrize("bits,expected", [(1, 0.36), (2, 0.117), (3, 0.03), (4, 0.009)])
+def test_mse_distortion(bits, expected):
+    q = A.TurboQuantMSE(128, bits, device=DEV, seed=42)
+    x = torch.randn(500, 128, generator=torch.Generator().manual_seed(bits))
+    x = x / x.norm(dim=-1, keepdim=True)
+    p, n = q.quantize(x)
+    mse = (x - q.dequantize(p, n)).pow(2).sum(-1).mean().item()
+    assert mse < expected * 2.5
+    # the paper's bound: D_mse <= (sqrt(3) pi / 2) 4^-b
+    assert mse <= math.sqrt(3) * math.pi / 2 * 4.0 ** (-bits)
+
+
+def test_mse_deterministic_shapes_monotone_compression():
+    x = torch.randn(200, 128, generator=torch.Generator().manual_seed(3))
+    x = x / x.norm(dim=-1, keepdim=True)
+    p1, n1 = A.TurboQuantMSE(128, 3, device=DEV).quantize(x)
+    p2, n2 = A.TurboQuantMSE(128, 3, device=DEV).quantize(x)
+    assert torch.equal(p1, p2) and torch.equal(n1, n2)
+    prev = float("inf")
+    for b in (1, 2, 3, 4):
+        q = A.TurboQuantMSE(128, b, device=DEV)
+        mse = (x - q.dequantize(*q.quantize(x))).pow(2).sum(-1).mean().item()
+        assert mse < prev
+        prev = mse
+    q = A.TurboQuantMSE(128, 3, device=DEV)
+    xb = torch.randn(2, 4, 8, 128)
+    assert q.dequantize(*q.quantize(xb)).shape == xb.shape
+    p, n = q.quantize(torch.randn(1, 128))
+    assert 128 * 2 / (p.numel() + 4 * n.numel()) > 3.0
+
+
+def test_mse_4bit_codes_match_the_float64_rotation():
+    """4-bit indices equal searchsorted over the float64 rotation of x / |x|
+    away from boundaries (an independent restatement)."""
+    from tests import npref
+    x = torch.randn(64, 128, generator=torch.Generator().manual_seed(5))
+    q = A.TurboQuantMSE(128, 4, device=DEV)
+    p, _ = q.quantize(x)
+    idx = A.unpack_bits(p, 4, 128).numpy()
+    _, _, rot = npref.quantize_rows(x.numpy().astype(np.float64), 128, hadamard_signs(128).numpy())
+    bounds = (npref.CENTROIDS_F64[:-1] + npref.CENTROIDS_F64[1:]) / 2 / math.sqrt(128)
+    want = np.searchsorted(bounds, rot, side="left")  # ties go down, as bucketize
+    near = np.abs(rot[..., None] - bounds).min(-1) < 1e-6
+    assert (idx[~near] == want[~near]).all()
+
+
+def test_prod_unbiased_and_min_bits():
+    d = 128
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(d, generator=g)
+    x = x / x.norm()
+    y = torch.randn(d, generator=g)
+    est = []
+    for seed in range(100):
+        q = A.TurboQuantProd(d, 3, device=DEV, seed=seed)
+        est.append(float(y @ q.dequantize(*q.quantize(x.unsqueeze(0)))[0]))
+    assert abs(np.mean(est) - float(x @ y)) < 0.1
+    with pytest.raises(AssertionError):
+        A.TurboQuantProd(128, 1, device=DEV)
+
+
+def test_attention_quality_3bit():
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(1, 8, 1, 128, generator=g)
+    k = torch.randn(1, 8, 256, 128, generator=g)
+    v = torch.randn(1, 8, 256, 128, generator=g)
+
+    def att(q, k, v):
+        return torch.softmax(q @ k.transpose(-2, -1) / math.sqrt(128), -1) @ v
+
+    quant = A.TurboQuantMSE(128, 3, device=DEV, seed=42)
+    out = att(q, quant.dequantize(*quant.quantize(k)), quant.dequantize(*quant.quantize(v)))
+    ref = att(q, k, v)
+    assert ((out - ref).norm() / ref.norm()).item() < 0.30
