@@ -51,8 +51,8 @@ def hadamard_signs(pd: int, device="cpu"):
 
 
 # Decode split heuristic for MI355X.  A workgroup serves (sequence, split,
-# group of G kv heads) with one wave per kv head, and holds the 1 KB dequant
-# table plus a ring of three LDS tile slots (16 token rows of the group's
+# group of G kv heads) with one wave per kv head, and holds the 32 KB dequant
+# table plus a ring of two LDS tile slots (16 token rows of the group's
 # entries, K and V).  The split count is chosen so the grid fills the
 # workgroup slots of all CUs once: a second, partial round of workgroups
 # would leave most CUs idle at the end.  Each split keeps at least
