@@ -359,7 +359,7 @@ constexpr int kRingSlots = TQ_RING_SLOTS;  // tile slots in the LDS ring
 // Cache policy of the ring copies: nt (non-temporal, bit 1 of the gfx950
 // cache-policy field), since every cache line is read exactly once; measured
 // 3-4 us faster per launch at configs[2] than the default policy.
-constexpr int kCopyPolicy = 2;
+[[maybe_unused]] constexpr int kCopyPolicy = 2;
 
 template <int PD, int G>
 struct RingGeom {
@@ -605,7 +605,7 @@ void decode_partials_kernel(DecodeParams p) {
       const int e = i / (kLutCopies / 4);
       uint32_t x[4];
       dq8((uint32_t)e * 0x01010101u, x);
-      const uint32_t val = (x[2] & 0xffffu) | (x[0] << 16);
+      [[maybe_unused]] const uint32_t val = (x[2] & 0xffffu) | (x[0] << 16);
 #if defined(__HIP_DEVICE_COMPILE__)
       asm volatile("ds_write_b128 %0, %1" : : "v"(lds_addr(&sm.klut[4 * i])), "v"(u32x4{val, val, val, val}) : "memory");
 #endif
@@ -689,11 +689,11 @@ void decode_partials_kernel(DecodeParams p) {
     const int step0 = c0 / STEP, step1 = (c1 - 1) / STEP;
     const int tpp = p.block_size / kTile;  // tiles per page
     const int64_t tokstride = (int64_t)p.Hkv * EBS;
-    const uint8_t* const kslab = p.ks;
-    const uint8_t* const vslab = p.vs;
+    [[maybe_unused]] const uint8_t* const kslab = p.ks;
+    [[maybe_unused]] const uint8_t* const vslab = p.vs;
     const int tile_last = (c1 - 1) / kTile;
     const int tile_end = 2 * step1 + 1;  // last tile any step of this split reads
-    const int rec = (int)(kTile * tokstride);
+    [[maybe_unused]] const int rec = (int)(kTile * tokstride);
 
     // Tile window: lane i holds the byte offset inside a slab of tile
     // wtile + i (64 bit, as lo/hi halves) and tmask bit i says whether that
@@ -743,7 +743,7 @@ void decode_partials_kernel(DecodeParams p) {
     // j = w, w + G, ...  Per-lane source offsets inside the tile's slab
     // (rows of tokstride bytes, the group's entries at hg*G*EBS):
     constexpr int NWMAX = RG::NW_HI;
-    const int nmine = RG::NW_LO + (w < RG::NIT % G ? 1 : 0);  // uniform
+    [[maybe_unused]] const int nmine = RG::NW_LO + (w < RG::NIT % G ? 1 : 0);  // uniform
     uint32_t goff[NWMAX];
 #pragma unroll
     for (int i = 0; i < NWMAX; i++) {
