@@ -110,3 +110,57 @@ def test_graph_replay_matches_eager():
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(o.float().cpu().numpy(), eager), f"replay {i}"
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_larger_pages(bs):
+    """Pages of 32 and 64 tokens (block_size a multiple of 16): the write
+    scatters into them and the decode walks two or four tiles per page."""
+    print(f"case: block_size {bs}", flush=True)
+    import math
+
+    import oracle
+    from turboquant_amd import ops
+    from turboquant_amd.geometry import choose_splits, hadamard_signs
+    rng = np.random.default_rng(bs)
+    hq, hkv, hd = 32, 8, 128
+    lens = [1000, 77, 2 * bs, 3 * bs + 5]
+    npg = [math.ceil(l / bs) for l in lens]
+    nb = sum(npg) + 3
+    perm = rng.permutation(nb).astype(np.int32)
+    maxp = max(npg)
+    bt = np.zeros((len(lens), maxp), np.int32)
+    slots, off = [], 0
+    for b, p in enumerate(npg):
+        bt[b, :p] = perm[off:off + p]
+        off += p
+        t = np.arange(lens[b])
+        slots.append(bt[b, t // bs] * bs + t % bs)
+    slots = np.concatenate(slots).astype(np.int32)
+    k, v = W.write_inputs(rng, len(slots), hkv, hd)
+    q = rng.standard_normal((len(lens), hq, hd)).astype(np.float16)
+    dev = G.DEV
+    cache = torch.zeros((2, nb, bs, hkv, 80), dtype=torch.uint8, device=dev)
+    signs = hadamard_signs(128, dev)
+    ops.quantize_write_kv_cache(cache, torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev),
+                                signs, torch.from_numpy(slots).to(dev), hd, 128)
+    ref_cache = np.zeros(tuple(cache.shape), np.uint8)
+    oracle.write_kv_cache(ref_cache, k, v, hadamard_signs(128).numpy(), slots, hd, 128)
+    got_cache = cache.cpu().numpy()
+    assert np.array_equal(got_cache, ref_cache)
+    b = len(lens)
+    max_len = maxp * bs
+    S, cs = choose_splits(b, max_len, hkv, hq, 128)
+    o = torch.empty((b, hq, 128), dtype=torch.float16, device=dev)
+    po = torch.empty((b * S, hq, 128), dtype=torch.float32, device=dev)
+    pl = torch.empty((b * S, hq), dtype=torch.float32, device=dev)
+    indptr = np.arange(b + 1, dtype=np.int32) * maxp
+    ops.decode_paged_splitkv(torch.from_numpy(q).to(dev), cache,
+                             torch.from_numpy(bt.reshape(-1)).to(dev),
+                             torch.from_numpy(indptr).to(dev),
+                             torch.tensor(lens, dtype=torch.int32, device=dev), hkv, hd, 128,
+                             1.0 / np.sqrt(hd), signs, o, po, pl, S, cs)
+    torch.cuda.synchronize()
+    ref = oracle.decode(q, got_cache, bt.reshape(-1), indptr, np.array(lens, np.int32), hkv, 128,
+                        1.0 / np.sqrt(hd), hadamard_signs(128).numpy())
+    G.assert_close(o.float().cpu().numpy(), ref, f"block_size {bs}")
