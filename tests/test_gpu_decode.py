@@ -48,6 +48,16 @@ def test_split_invariance(splits, chunk):
     _check(c, f"splits={splits}", num_splits=splits, chunk=chunk)
 
 
+@pytest.mark.parametrize("chunk", [64, 67, 80, 512])
+def test_pair_share_grid(chunk):
+    """A grid of exactly two workgroups per CU (8 sequences x 64 splits, 8 kv
+    heads in one group) serves split pairs with an uneven token share; ragged
+    lengths leave some pairs partly or wholly past the end."""
+    print(f"case: pair-share grid B=8 S=64 chunk={chunk}", flush=True)
+    c = W.decode_case(41 + chunk, 8, [0, 1, 17, 100, 1000, 2047, 2048, 4095], 32, 8, 128)
+    _check(c, f"pair chunk={chunk}", num_splits=64, chunk=chunk)
+
+
 def test_edge_lengths_and_gqa():
     """seq_len 0, 1, 15, 16, 17 and a partial last page; GQA ratios 1, 2, 8, 16."""
     for hq, hkv in ((8, 8), (16, 8), (16, 2), (16, 1)):

@@ -121,6 +121,11 @@ struct DecodeParams {
   float* plse;
   int num_blocks;  // clamped to INT_MAX (page ids are int32)
   int B, Hq, Hkv, ratio, block_size, ebs, S, cs, G, HG;
+  // > 0: the grid is two workgroups per CU and splits are served in pairs
+  // (2j, 2j + 1) by blocks u and u + grid/2, which the dispatcher places on one
+  // CU; the first-dispatched block takes the first pair_first tokens of the
+  // pair's 2 * cs (it progresses faster while both are resident)
+  int pair_first;
   float qk_scale;     // sm_scale * log2(e) / (sqrt(pd) * kCbScale)
   float inv_sqrt_pd;  // 1/sqrt(pd)
   float pv_scale;     // 1/(sqrt(pd) * kCbScale)
@@ -619,11 +624,20 @@ void decode_partials_kernel(DecodeParams p) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int q4 = lane >> 4, n = lane & 15;
   const uint32_t lanec = (uint32_t)(lane & 31) * 4u;  // this lane's table copy
-  int bid = blockIdx.x;
+  const int half = gridDim.x >> 1;
+  const int mem = p.pair_first > 0 && (int)blockIdx.x >= half;
+  int bid = blockIdx.x - mem * half;
   const int hg = bid % p.HG;
   bid /= p.HG;
-  const int s = bid % p.S;
-  const int b = bid / p.S;
+  int s, b;
+  if (p.pair_first > 0) {
+    const int pj = bid % (p.S >> 1);
+    b = bid / (p.S >> 1);
+    s = 2 * pj + mem;
+  } else {
+    s = bid % p.S;
+    b = bid / p.S;
+  }
   const int kvh = hg * G + w;
   const int ratio = p.ratio;
   // sequence length and page-table start, loaded before anything else: the
@@ -682,8 +696,14 @@ void decode_partials_kernel(DecodeParams p) {
   st.lsum = 0.f;
   const float lpv = -__log2f(p.pv_scale);
 
-  const int c0 = s * p.cs;
-  const int c1 = min(c0 + p.cs, L);
+  int c0 = s * p.cs, c1 = c0 + p.cs;
+  if (p.pair_first > 0) {
+    const int base = (s & ~1) * p.cs;
+    c0 = (s & 1) ? base + p.pair_first : base;
+    c1 = (s & 1) ? base + 2 * p.cs : base + p.pair_first;
+  }
+  c0 = min(c0, L);
+  c1 = min(c1, L);
   if (c0 < c1) {  // uniform over the workgroup
     constexpr int STEP = 2 * kTile;
     const int step0 = c0 / STEP, step1 = (c1 - 1) / STEP;
@@ -1238,6 +1258,30 @@ int check_geometry(int pd, int hq, int hkv, int bs, int ebs, const char* who) {
   return 0;
 }
 
+// Token share of the first block of a split pair (0: splits keep equal
+// ranges).  When the grid is exactly two resident workgroups on every CU,
+// blocks u and u + grid/2 run side by side on one CU, and the one dispatched
+// first finishes an equal range well before its partner (43 vs 61 us at 8 x
+// 32k tokens, 8 kv heads, pd 128), which then runs alone on a half-empty CU.  Serving splits 2j and
+// 2j + 1 from such a pair and giving the first block 62% of their tokens
+// evens out the finish times.  Any other grid keeps equal ranges: there the
+// pairing is not known and an uneven share would only lengthen the tail.
+int pair_share(const void* kernel, int threads, int64_t blocks, int num_splits,
+               int kv_chunk_size) {
+  if (num_splits < 2 || (num_splits & 1)) return 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess)
+    return 0;
+  if (per_cu != 2 || blocks != 2LL * cus) return 0;
+  const int share = (2 * kv_chunk_size * 62 / 100 + 15) & ~15;
+  return share < 2 * kv_chunk_size ? share : 0;
+}
+
 }  // namespace
 }  // namespace tq
 
@@ -1322,7 +1366,10 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   // parts share one B operand when the GQA ratio leaves 8 columns free
   const bool pack2 = ratio <= 8 && pd <= 128;
   const bool qc = ratio <= 8;
-#define TQ_LAUNCH(PDV, GV, PK, QCV) \
+#define TQ_LAUNCH(PDV, GV, PK, QCV)                                                   \
+  p.pair_first = pair_share(reinterpret_cast<const void*>(                            \
+                                &decode_partials_kernel<PDV, GV, PK, QCV>),           \
+                            64 * GV, blocks, num_splits, kv_chunk_size);              \
   hipLaunchKernelGGL((decode_partials_kernel<PDV, GV, PK, QCV>), grid, block, 0, st, p)
 #define TQ_LAUNCH_G(PDV, PK, QCV)   \
   switch (G) {                      \
