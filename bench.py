@@ -208,7 +208,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's path runs on a single MI355X; "
-              f"--gpus {args.gpus} is not supported (sharding is described in DESIGN.md).",
+              f"--gpus {args.gpus} is not supported (multi-GPU sharding is not built).",
               file=sys.stderr)
         sys.exit(2)
 
