@@ -48,14 +48,17 @@ def test_split_invariance(splits, chunk):
     _check(c, f"splits={splits}", num_splits=splits, chunk=chunk)
 
 
-@pytest.mark.parametrize("chunk", [64, 67, 80, 512])
-def test_pair_share_grid(chunk):
-    """A grid of exactly two workgroups per CU (8 sequences x 64 splits, 8 kv
-    heads in one group) serves split pairs with an uneven token share; ragged
+@pytest.mark.parametrize("hd,b,hq,hkv,chunk", [
+    (128, 8, 32, 8, 64), (128, 8, 32, 8, 67), (128, 8, 32, 8, 80), (128, 8, 32, 8, 512),
+    (64, 8, 32, 8, 80), (256, 4, 16, 8, 80)])
+def test_pair_share_grid(hd, b, hq, hkv, chunk):
+    """A grid of exactly two workgroups per CU (sequences x 64 splits x head
+    groups = 512) serves split pairs with an uneven token share; ragged
     lengths leave some pairs partly or wholly past the end."""
-    print(f"case: pair-share grid B=8 S=64 chunk={chunk}", flush=True)
-    c = W.decode_case(41 + chunk, 8, [0, 1, 17, 100, 1000, 2047, 2048, 4095], 32, 8, 128)
-    _check(c, f"pair chunk={chunk}", num_splits=64, chunk=chunk)
+    print(f"case: pair-share grid hd={hd} B={b} {hq}/{hkv} S=64 chunk={chunk}", flush=True)
+    lens = [0, 1, 17, 100, 1000, 2047, 2048, 4095][8 - b:]
+    c = W.decode_case(41 + chunk + hd, b, lens, hq, hkv, hd)
+    _check(c, f"pair hd={hd} chunk={chunk}", num_splits=64, chunk=chunk)
 
 
 def test_edge_lengths_and_gqa():
