@@ -92,6 +92,41 @@ int tq_decode_paged_splitkv(const void* q, int64_t q_stride_b, int64_t q_stride_
                             tq_stream_t stream);
 
 /*
+ * tq_decode_paged_splitkv with the split plan made on the GPU (ragged
+ * batches).  The reference sizes every sequence's splits from the batch's
+ * max_len (turboquant/vllm_backend_fused.py:128-156), so at mixed lengths
+ * most workgroups of short sequences sit idle; here each workgroup derives
+ * the same plan from seq_lens: a unit size U (a multiple of 32 tokens, the
+ * smallest with sum_b ceil(seq_len_b / U) no more than the grid's work
+ * units) and its own (sequence, token range).  No host read, so a captured
+ * graph stays valid while seq_lens change between replays.  Same inputs and
+ * output as tq_decode_paged_splitkv, except:
+ *   partition_o fp32 [max_rows, num_qo_heads, pd], partition_lse fp32
+ *   [max_rows, num_qo_heads]: workspace; max_rows >= batch, and
+ *   tq_decode_balanced_rows() gives the rows the plan uses at most;
+ *   split_rows int32 [batch + 2] (written): sequence b's partial rows are
+ *   split_rows[b] .. split_rows[b + 1] - 1, split_rows[batch + 1] = U.
+ * batch <= 1024; sum of seq_lens < 2^30.
+ */
+int tq_decode_paged_balanced(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                             const uint8_t* k_slab, const uint8_t* v_slab,
+                             const int32_t* indices, const int32_t* indptr,
+                             const int32_t* seq_lens, int32_t batch,
+                             int32_t num_qo_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t padded_dim,
+                             int32_t block_size, int32_t ebs, int64_t num_blocks,
+                             float sm_scale, const float* signs, int32_t max_rows,
+                             float* partition_o, float* partition_lse,
+                             int32_t* split_rows, void* o, tq_stream_t stream);
+
+/*
+ * Partial rows tq_decode_paged_balanced uses at most for this geometry on
+ * the current device (or -22).  Queries the device once per geometry.
+ */
+int tq_decode_balanced_rows(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                            int32_t padded_dim);
+
+/*
  * The first kernel of tq_decode_paged_splitkv alone (the reference's v5 split
  * kernel, v5_tc.cuh:106-795): writes partition_o (normalised, rotated domain)
  * and partition_lse (natural log; -inf for an empty split) of split s =

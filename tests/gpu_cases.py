@@ -25,6 +25,37 @@ def build_cache(case, block=W.BLOCK):
     return cache, pd
 
 
+def decode_inputs(case, pd):
+    """Device tensors of a case: padded q, strided page table, seq_lens."""
+    q = case["q"]
+    b, hq, hd = q.shape
+    qp = np.zeros((b, hq, pd), np.float16)
+    qp[:, :, :hd] = q
+    bt = torch.from_numpy(case["block_table"]).to(DEV)
+    return dict(
+        qp=qp, q=torch.from_numpy(qp).to(DEV), indices=bt.reshape(-1).contiguous(),
+        indptr=(torch.arange(b + 1, dtype=torch.int32, device=DEV) * bt.shape[1]).contiguous(),
+        seq=torch.from_numpy(np.asarray(case["seq_lens"], np.int32)).to(DEV))
+
+
+def run_balanced(case, cache, pd, signs=True, rows=None):
+    """The balanced-plan decode; returns (o, qp, scale, split_indptr)."""
+    d = decode_inputs(case, pd)
+    b, hq, hd = case["q"].shape
+    if rows is None:
+        rows = ops.balanced_rows(b, hq, case["num_kv_heads"], pd)
+    o = torch.empty((b, hq, pd), dtype=torch.float16, device=DEV)
+    po = torch.empty((rows, hq, pd), dtype=torch.float32, device=DEV)
+    pl = torch.empty((rows, hq), dtype=torch.float32, device=DEV)
+    split = torch.full((b + 2,), -7, dtype=torch.int32, device=DEV)
+    s = hadamard_signs(pd, DEV) if signs else None
+    scale = 1.0 / np.sqrt(hd)
+    ops.decode_paged_balanced(d["q"], cache, d["indices"], d["indptr"], d["seq"],
+                              case["num_kv_heads"], hd, pd, scale, s, o, po, pl, split)
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), d["qp"], scale, split.cpu().numpy()
+
+
 def run_decode(case, cache, pd, num_splits=None, chunk=None, signs=True, sm_scale=None):
     q = case["q"]
     b, hq, hd = q.shape
@@ -70,3 +101,47 @@ def assert_close(got, ref, what=""):
     bad = err > lim
     assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} outside atol {ATOL} / "
                            f"rtol {RTOL}; max abs err {err.max():.3e}")
+
+
+def device_case(seed, seq_lens, hq, hkv, hd, k_dist="normal", chunk_tokens=1 << 16):
+    """A decode case too large for host-generated K/V: q, page table and slot
+    mapping from numpy (seeded), K/V drawn on the GPU (seeded torch generator;
+    K ~ Student-t(3) for k_dist "t3") and written through the write kernel,
+    whose bytes are pinned against the oracle by the write tests.  Returns
+    (case, cache, pd); case has no "k"/"v"."""
+    rng = np.random.default_rng(seed)
+    seq_lens = np.asarray(seq_lens, np.int32)
+    b = len(seq_lens)
+    q = rng.standard_normal((b, hq, hd)).astype(np.float16)
+    bt, slots, nb = W.paged_layout(rng, seq_lens)
+    shape, pd = W.cache_bytes(nb, hkv, hd)
+    cache = torch.zeros(shape, dtype=torch.uint8, device=DEV)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    signs = hadamard_signs(pd, DEV)
+    st = torch.from_numpy(slots).to(DEV)
+    for a in range(0, len(slots), chunk_tokens):
+        n = min(chunk_tokens, len(slots) - a)
+        if k_dist == "t3":
+            # Student-t(3) = N(0,1) / sqrt(chi2_3 / 3), chi2_3 = sum of 3 squared normals
+            z = torch.randn((n, hkv, hd), generator=g, device=DEV)
+            c2 = torch.randn((3, n, hkv, hd), generator=g, device=DEV).square().sum(0)
+            k = (z / torch.sqrt(c2 / 3.0)).half()
+        else:
+            k = torch.randn((n, hkv, hd), generator=g, device=DEV).half()
+        v = torch.randn((n, hkv, hd), generator=g, device=DEV).half()
+        ops.quantize_write_kv_cache(cache, k, v, signs, st[a:a + n], hd, pd)
+    torch.cuda.synchronize()
+    case = dict(q=q, slots=slots, block_table=bt, seq_lens=seq_lens, num_blocks=nb,
+                num_kv_heads=hkv, head_dim=hd)
+    return case, cache, pd
+
+
+def expected_plan(seq_lens, units):
+    """The balanced plan's unit size: the smallest multiple of 32 tokens with
+    sum_b ceil(L_b / U) <= units."""
+    lens = np.maximum(np.asarray(seq_lens, np.int64), 0)
+    u = 32
+    while int(np.sum(-(-lens // u))) > units:
+        u += 32
+    return u

@@ -23,9 +23,13 @@ class Meta:
     slot_mapping: torch.Tensor
 
 
-def test_backend_write_then_decode():
-    print("case: backend write+decode", flush=True)
+@pytest.mark.parametrize("forced", ["", "gfx950_static"])
+def test_backend_write_then_decode(forced, monkeypatch):
+    print(f"case: backend write+decode forced={forced!r}", flush=True)
+    from turboquant_amd import decoder_dispatch as dd
     from turboquant_amd.vllm_backend_fused import TurboQuantBackend, TurboQuantFusedImpl
+    monkeypatch.setenv("TQ_FORCE_KERNEL", forced)
+    dd.pick_decode_op.cache_clear()
     dev = G.DEV
     hq, hkv, hd, bs = 32, 8, 128, 16
     lens = [300, 1000, 17]
@@ -50,8 +54,9 @@ def test_backend_write_then_decode():
     torch.cuda.synchronize()
     ref = G.oracle_decode(c, cache.cpu().numpy(), c["q"], 128, 1.0 / np.sqrt(hd))
     G.assert_close(out.float().cpu().numpy().reshape(b, hq, hd), ref, "backend")
-    # the same through the registered reference op name
-    assert impl._decode_op_name == "gfx950_hip_paged_splitkv"
+    # the balanced op by default, the reference op name when forced
+    assert impl._decode_op_name == (dd.STATIC_KERNEL_NAME if forced else dd.KERNEL_NAME)
+    dd.pick_decode_op.cache_clear()
 
 
 def test_backend_prefill_fresh_attention():

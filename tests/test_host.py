@@ -160,3 +160,94 @@ def test_ops_raise_instead_of_falling_back(monkeypatch):
     with pytest.raises(RuntimeError):
         ops.quantize_write_kv_cache(cache, k, k, geometry.hadamard_signs(128),
                                     torch.zeros(3, dtype=torch.int32), 128, 128)
+
+
+def test_reference_import_path_is_the_same_modules():
+    """The reference's callers import turboquant.vllm_plugin,
+    turboquant.vllm_backend_fused and turboquant.decoder_dispatch
+    (reference tests/bench_vllm_serve.py:54, tests/test_decoder_dispatch.py:17)."""
+    import turboquant
+    import turboquant.vllm_plugin
+    import turboquant_amd.vllm_plugin
+    from turboquant.decoder_dispatch import pick_decode_op
+    from turboquant.vllm_backend_fused import TurboQuantBackend, TurboQuantFusedImpl
+    from turboquant_amd import decoder_dispatch, vllm_backend_fused
+    assert turboquant.vllm_plugin is turboquant_amd.vllm_plugin
+    assert pick_decode_op is decoder_dispatch.pick_decode_op
+    assert TurboQuantBackend is vllm_backend_fused.TurboQuantBackend
+    assert TurboQuantBackend.get_impl_cls() is TurboQuantFusedImpl
+    assert turboquant_amd.vllm_plugin.__spec__.name == "turboquant_amd.vllm_plugin"
+    from turboquant import QJL, Codebook, TurboQuantMSE, fwht  # noqa: F401
+    with pytest.raises(ModuleNotFoundError):
+        import turboquant.no_such_module  # noqa: F401
+
+
+def test_plugin_entry_point_names_the_reference_path():
+    text = open(os.path.join(ROOT, "pyproject.toml")).read()
+    assert 'turboquant = "turboquant.vllm_plugin:register"' in text
+    import importlib
+    mod, fn = "turboquant.vllm_plugin:register".split(":")
+    assert callable(getattr(importlib.import_module(mod), fn))
+
+
+def test_plugin_registers_custom_backend_with_vllm_registry(monkeypatch):
+    """register() maps CUSTOM to turboquant.vllm_backend_fused.TurboQuantBackend
+    through vLLM's registry (reference turboquant/vllm_plugin.py:85-92), checked
+    against a stand-in registry module, since vLLM is not installed here."""
+    import enum
+    import importlib
+    import sys
+    import types
+
+    calls = []
+
+    class AttentionBackendEnum(enum.Enum):
+        FLASH_ATTN = "FLASH_ATTN"
+        CUSTOM = "CUSTOM"
+
+    reg = types.ModuleType("vllm.v1.attention.backends.registry")
+    reg.AttentionBackendEnum = AttentionBackendEnum
+    reg.register_backend = lambda which, path: calls.append((which, path))
+    for name in ("vllm", "vllm.v1", "vllm.v1.attention", "vllm.v1.attention.backends"):
+        monkeypatch.setitem(sys.modules, name, types.ModuleType(name))
+    monkeypatch.setitem(sys.modules, "vllm.v1.attention.backends.registry", reg)
+    import turboquant.vllm_plugin as plugin
+    monkeypatch.setattr(plugin, "_registered", False)
+    plugin.register()
+    plugin.register()  # idempotent: one registration
+    assert calls == [(AttentionBackendEnum.CUSTOM,
+                      "turboquant.vllm_backend_fused.TurboQuantBackend")]
+    # vLLM resolves the registered path by import + attribute
+    mod, cls = calls[0][1].rsplit(".", 1)
+    backend = getattr(importlib.import_module(mod), cls)
+    assert backend.get_name() == "CUSTOM"
+    assert backend.get_kv_cache_shape(10, 16, 8, 128, "fp8") == (2, 10, 16, 8, 80)
+
+
+def test_fake_impls_trace_without_running():
+    """Meta kernels for torch.compile / graph tracing: shapes only, no launch."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from turboquant_amd import ops
+    ops.register_ops()
+    with FakeTensorMode():
+        q = torch.empty(8, 32, 128, dtype=torch.float16)
+        cache = torch.empty(2, 10, 16, 8, 80, dtype=torch.uint8)
+        i = torch.empty(10, dtype=torch.int32)
+        po, pl = torch.empty(8, 32, 128), torch.empty(8, 32)
+        o = torch.ops.turboquant_v5.decode_v5_from_cache_paged_splitkv_ws(
+            q, cache, i, i, i, i, 8, 16, 128, 128, 0.1, torch.empty(128), 64, 4, q, 100, po,
+            pl, i, i, i, i, 1)
+        assert o.shape == (8, 32, 128) and o.dtype == torch.float16
+        k = torch.empty(3, 8, 128)
+        torch.ops.turboquant_write.quantize_write_kv_cache(cache, k, k, torch.empty(128), i,
+                                                           128, 128)
+
+
+def test_write_refuses_rows_narrower_than_head_dim():
+    from turboquant_amd import ops
+    cache = torch.zeros((2, 4, 16, 8, 80), dtype=torch.uint8)
+    k = torch.zeros((3, 8, 96), dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="fewer than head_dim"):
+        ops.quantize_write_kv_cache(cache, k, k, geometry.hadamard_signs(128),
+                                    torch.zeros(3, dtype=torch.int32), 128, 128)

@@ -25,6 +25,10 @@ SIGNATURES = {
     "tq_decode_paged_splitkv": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                        _I32, _I32, _I32, _I32, _I64, _F32, _P, _I32, _I32,
                                        _P, _P, _P, _P]),
+    "tq_decode_paged_balanced": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                        _I32, _I32, _I32, _I32, _I64, _F32, _P, _I32, _P, _P,
+                                        _P, _P, _P]),
+    "tq_decode_balanced_rows": (_I32, [_I32, _I32, _I32, _I32]),
     "tq_decode_partials": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                   _I32, _I32, _I64, _F32, _P, _I32, _I32, _P, _P, _P]),
     "tq_combine_splits": (_I32, [_P, _P, _I32, _I32, _I32, _I32, _P, _P, _P]),
@@ -33,7 +37,7 @@ SIGNATURES = {
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_abi_version": (_I32, []),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 

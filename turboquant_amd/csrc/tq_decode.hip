@@ -37,7 +37,9 @@
 //    only moves when a tile exceeds it by more than 2^3), bounding p <= 8.
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "tq_common.h"
 
@@ -123,9 +125,19 @@ struct DecodeParams {
   int B, Hq, Hkv, ratio, block_size, ebs, S, cs, G, HG;
   // > 0: the grid is two workgroups per CU and splits are served in pairs
   // (2j, 2j + 1) by blocks u and u + grid/2, which the dispatcher places on one
-  // CU; the first-dispatched block takes the first pair_first tokens of the
-  // pair's 2 * cs (it progresses faster while both are resident)
-  int pair_first;
+  // CU; the first-dispatched block takes the first pair_pct percent (rounded
+  // up to 16 tokens) of the pair's tokens (it progresses faster while both
+  // are resident)
+  int pair_pct;
+  // > 0: balanced plan.  The grid serves `units` work units per head group
+  // (pairs of blocks when pair_pct > 0), and each unit covers U consecutive
+  // tokens of one sequence, U being the smallest multiple of kPlanAlign with
+  // sum_b ceil(seq_len_b / U) <= units, computed by every workgroup from
+  // seq_lens on the device.  Partial rows are numbered by unit (two per unit
+  // in pairs), so sequence b owns the contiguous rows split_out[b] ..
+  // split_out[b + 1]; block 0 stores that table and U (split_out[B + 1]).
+  int units;
+  int32_t* split_out;
   float qk_scale;     // sm_scale * log2(e) / (sqrt(pd) * kCbScale)
   float inv_sqrt_pd;  // 1/sqrt(pd)
   float pv_scale;     // 1/(sqrt(pd) * kCbScale)
@@ -180,6 +192,137 @@ __device__ __forceinline__ float lo_half(uint32_t v) {
 }
 __device__ __forceinline__ float hi_half(uint32_t v) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+}
+
+// ---- balanced split plan ------------------------------------------------
+constexpr int kPlanAlign = 2 * kTile;   // unit sizes are whole steps
+constexpr int kPlanMaxBatch = 1024;     // sequence lengths held in registers
+
+__device__ __forceinline__ int xor_lane_i(int v, int m) {
+  return __float_as_int(xor_lane(__int_as_float(v), m));
+}
+__device__ __forceinline__ int permlane_xor16_i(int v) {
+  const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  return (int)r[0] == v ? (int)r[1] : (int)r[0];
+}
+// sum / max over the 64 lanes (every lane gets the result): DPP lane xors
+// inside rows of 16, then the 16- and 32-lane swaps
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v += xor_lane_i(v, 1);
+  v += xor_lane_i(v, 2);
+  v += xor_lane_i(v, 4);
+  v += xor_lane_i(v, 8);
+  auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  v = (int)(r[0] + r[1]);
+  r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  return (int)(r[0] + r[1]);
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+  v = max(v, xor_lane_i(v, 1));
+  v = max(v, xor_lane_i(v, 2));
+  v = max(v, xor_lane_i(v, 4));
+  v = max(v, xor_lane_i(v, 8));
+  auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  v = max((int)r[0], (int)r[1]);
+  r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  return max((int)r[0], (int)r[1]);
+}
+// ceil(a / d) for 0 <= a < 2^24, d > 0: a float estimate (off by at most one
+// for these ranges) corrected both ways in integers
+__device__ __forceinline__ int ceil_div_est(int a, int d, float rd) {
+  const int x = a + d - 1;
+  int f = (int)((float)x * rd);
+  f -= (f * d > x) ? 1 : 0;
+  f += ((f + 1) * d <= x) ? 1 : 0;
+  return f;
+}
+
+// The unit of a balanced plan a workgroup serves: sequence b (-1: none, the
+// grid has more units than the plan uses), unit j of that sequence, its
+// length L, the sequence's first unit Pb and the unit size U in tokens.
+struct PlanSlot {
+  int b, j, L, Pb, U;
+};
+
+// Every lane of a wave calls this; the result is wave-uniform.  writer:
+// this wave also stores the row table (rows = rowmul * units) and U.
+__device__ PlanSlot plan_slot(const int32_t* __restrict__ seq_lens, int B, int units, int u,
+                              int rowmul, int32_t* split_out, bool writer) {
+  constexpr int PR = kPlanMaxBatch / 64;
+  const int lane = threadIdx.x & 63;
+  const int nreg = (B + 63) >> 6;
+  int len[PR];
+#pragma unroll
+  for (int i = 0; i < PR; i++) {
+    const int bb = 64 * i + lane;
+    len[i] = (i < nreg && bb < B) ? max(seq_lens[bb], 0) : 0;
+  }
+  int tsum = 0, mx = 0, nz = 0;
+#pragma unroll
+  for (int i = 0; i < PR; i++) {
+    tsum += len[i];
+    mx = max(mx, len[i]);
+    nz += len[i] > 0 ? 1 : 0;
+  }
+  tsum = __builtin_amdgcn_readfirstlane(wave_sum_i(tsum));
+  mx = __builtin_amdgcn_readfirstlane(wave_max_i(mx));
+  nz = __builtin_amdgcn_readfirstlane(wave_sum_i(nz));
+  constexpr int A = kPlanAlign;
+  auto units_for = [&](int k) -> int {
+    const int d = k * A;
+    const float rd = 1.0f / (float)d;
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < PR; i++)
+      if (i < nreg) c += ceil_div_est(len[i], d, rd);
+    return __builtin_amdgcn_readfirstlane(wave_sum_i(c));
+  };
+  // smallest feasible k in (lo, hi]: every k below tsum / (units * A) needs
+  // more than `units` units; k = ceil(max_len / A) needs nz <= units, and so
+  // does any k >= tsum / ((units - nz) * A) (at most one partial unit per
+  // sequence)
+  int hi = max(1, (mx + A - 1) / A);
+  if (units > nz) hi = min(hi, max(1, (tsum + (units - nz) * A - 1) / ((units - nz) * A)));
+  int lo = (tsum + units * A - 1) / (units * A) - 1;
+  lo = max(0, min(lo, hi - 1));
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (units_for(mid) <= units) hi = mid; else lo = mid;
+  }
+  const int U = hi * A;
+  const float rdU = 1.0f / (float)U;
+  PlanSlot r = {-1, 0, 0, 0, U};
+  int carry = 0;
+#pragma unroll
+  for (int i = 0; i < PR; i++) {
+    if (i < nreg) {
+      const int c = ceil_div_est(len[i], U, rdU);
+      int incl = c;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off);
+        if (lane >= off) incl += y;
+      }
+      incl += carry;
+      const int excl = incl - c;
+      const int bb = 64 * i + lane;
+      if (writer && bb < B) split_out[bb] = excl * rowmul;
+      const uint64_t hit = __ballot(c > 0 && excl <= u && u < incl);
+      if (hit) {
+        const int l0 = __builtin_ctzll(hit);
+        r.b = 64 * i + l0;
+        r.Pb = __builtin_amdgcn_readlane(excl, l0);
+        r.j = u - r.Pb;
+        r.L = __builtin_amdgcn_readlane(len[i], l0);
+      }
+      carry = __builtin_amdgcn_readlane(incl, 63);
+    }
+  }
+  if (writer && lane == 0) {
+    split_out[B] = carry * rowmul;
+    split_out[B + 1] = U;
+  }
+  return r;
 }
 
 // Per-lane register geometry of the decode math for padded head size PD.
@@ -625,25 +768,57 @@ void decode_partials_kernel(DecodeParams p) {
   const int q4 = lane >> 4, n = lane & 15;
   const uint32_t lanec = (uint32_t)(lane & 31) * 4u;  // this lane's table copy
   const int half = gridDim.x >> 1;
-  const int mem = p.pair_first > 0 && (int)blockIdx.x >= half;
+  const int mem = p.pair_pct > 0 && (int)blockIdx.x >= half;
   int bid = blockIdx.x - mem * half;
   const int hg = bid % p.HG;
   bid /= p.HG;
-  int s, b;
-  if (p.pair_first > 0) {
-    const int pj = bid % (p.S >> 1);
-    b = bid / (p.S >> 1);
-    s = 2 * pj + mem;
-  } else {
-    s = bid % p.S;
-    b = bid / p.S;
-  }
   const int kvh = hg * G + w;
   const int ratio = p.ratio;
-  // sequence length and page-table start, loaded before anything else: the
-  // first copies depend on them
-  const int L = p.seq_lens[b];
-  const int ip = p.indptr[b];
+  // the token range [c0, c1) of sequence b this workgroup serves, and its
+  // partial row
+  int b, L, ip, c0, c1;
+  int64_t row;
+  if (p.units > 0) {
+    const PlanSlot ps = plan_slot(p.seq_lens, p.B, p.units, bid, p.pair_pct > 0 ? 2 : 1,
+                                  p.split_out, blockIdx.x == 0 && w == 0);
+    if (ps.b < 0) return;  // unit beyond the plan: no row (uniform over the workgroup)
+    b = ps.b;
+    L = ps.L;
+    ip = p.indptr[b];
+    c0 = ps.j * ps.U;
+    c1 = c0 + ps.U;
+    if (p.pair_pct > 0) {
+      const int first = min((ps.U * p.pair_pct / 100 + 15) & ~15, ps.U);
+      c0 = mem ? c0 + first : c0;
+      c1 = mem ? c1 : c0 + first;
+      row = 2 * (int64_t)(ps.Pb + ps.j) + mem;
+    } else {
+      row = ps.Pb + ps.j;
+    }
+  } else {
+    int s;
+    if (p.pair_pct > 0) {
+      const int pj = bid % (p.S >> 1);
+      b = bid / (p.S >> 1);
+      s = 2 * pj + mem;
+    } else {
+      s = bid % p.S;
+      b = bid / p.S;
+    }
+    // sequence length and page-table start, loaded before anything else:
+    // the first copies depend on them
+    L = p.seq_lens[b];
+    ip = p.indptr[b];
+    c0 = s * p.cs;
+    c1 = c0 + p.cs;
+    if (p.pair_pct > 0) {
+      const int base = (s & ~1) * p.cs;
+      const int first = min((2 * p.cs * p.pair_pct / 100 + 15) & ~15, 2 * p.cs);
+      c0 = (s & 1) ? base + first : base;
+      c1 = (s & 1) ? base + 2 * p.cs : base + first;
+    }
+    row = (int64_t)b * p.S + s;
+  }
 
   half8_t qb[KD], ql[QC ? 1 : KD];  // q' operands
 
@@ -696,12 +871,6 @@ void decode_partials_kernel(DecodeParams p) {
   st.lsum = 0.f;
   const float lpv = -__log2f(p.pv_scale);
 
-  int c0 = s * p.cs, c1 = c0 + p.cs;
-  if (p.pair_first > 0) {
-    const int base = (s & ~1) * p.cs;
-    c0 = (s & 1) ? base + p.pair_first : base;
-    c1 = (s & 1) ? base + 2 * p.cs : base + p.pair_first;
-  }
   c0 = min(c0, L);
   c1 = min(c1, L);
   if (c0 < c1) {  // uniform over the workgroup
@@ -1081,7 +1250,7 @@ void decode_partials_kernel(DecodeParams p) {
   if (n < ratio) {
     // o = pv_scale * O / lsum' (p' = p * pv_scale in both O and lsum')
     const float inv = lt > 0.f ? p.pv_scale / lt : 0.0f;
-    const int64_t orow = ((int64_t)b * p.S + s) * p.Hq + kvh * ratio + n;
+    const int64_t orow = row * p.Hq + kvh * ratio + n;
     float* out = p.po + orow * PD + q4 * (PD / 4);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -1104,7 +1273,8 @@ void decode_partials_kernel(DecodeParams p) {
 // FWHT across its 64 lanes.
 template <int PD>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ po,
-                                                      const float* __restrict__ plse, int S_rows, int step,
+                                                      const float* __restrict__ plse, int S_fixed,
+                                                      const int32_t* __restrict__ split_rows,
                                                       int Hq, const float* __restrict__ signs,
                                                       float inv_sqrt_pd, _Float16* __restrict__ o) {
   constexpr int C = PD / 4;        // float4 columns
@@ -1114,11 +1284,15 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   __shared__ float red[8];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int b = blockIdx.x / Hq, h = blockIdx.x % Hq;
-  // split j of sequence b is row row0 + j * rs (rows of the splits a partials
-  // workgroup merged into its first row are skipped with step > 1)
-  const int64_t row0 = (int64_t)b * S_rows * Hq + h;
-  const int64_t rs = (int64_t)step * Hq;
-  const int S = (S_rows + step - 1) / step;
+  // the splits of sequence b are the partial rows r0 .. r0 + S - 1: b * S_fixed
+  // onwards, or split_rows[b] .. split_rows[b + 1] (a balanced plan)
+  int r0 = b * S_fixed, S = S_fixed;
+  if (split_rows) {
+    r0 = split_rows[b];
+    S = split_rows[b + 1] - r0;
+  }
+  const int64_t row0 = (int64_t)r0 * Hq + h;
+  const int64_t rs = Hq;
 
   const int col = tid % C, grp = tid / C;
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -1258,47 +1432,84 @@ int check_geometry(int pd, int hq, int hkv, int bs, int ebs, const char* who) {
   return 0;
 }
 
-// Token share of the first block of a split pair (0: splits keep equal
-// ranges).  When the grid is exactly two resident workgroups on every CU,
-// blocks u and u + grid/2 run side by side on one CU, and the one dispatched
-// first finishes an equal range well before its partner (43 vs 61 us at 8 x
-// 32k tokens, 8 kv heads, pd 128), which then runs alone on a half-empty CU.  Serving splits 2j and
-// 2j + 1 from such a pair and giving the first block 62% of their tokens
-// evens out the finish times.  Any other grid keeps equal ranges: there the
-// pairing is not known and an uneven share would only lengthen the tail.
-int pair_share(const void* kernel, int threads, int64_t blocks, int num_splits,
-               int kv_chunk_size) {
-  if (num_splits < 2 || (num_splits & 1)) return 0;
+// Occupancy facts of one kernel on the current device: CUs and resident
+// workgroups per CU.  Queried once per (device, kernel) and cached, so a
+// decode launch costs no device queries after the first.
+struct Occupancy {
+  int cus, per_cu;
+};
+Occupancy occupancy(const void* kernel, int threads) {
+  struct Entry {
+    int dev;
+    const void* kernel;
+    int threads;
+    Occupancy occ;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 0;
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess)
-    return 0;
-  if (per_cu != 2 || blocks != 2LL * cus) return 0;
-  const int share = (2 * kv_chunk_size * 62 / 100 + 15) & ~15;
-  return share < 2 * kv_chunk_size ? share : 0;
+  if (hipGetDevice(&dev) != hipSuccess) return {0, 0};
+  std::lock_guard<std::mutex> lock(mu);
+  for (const Entry& e : cache)
+    if (e.dev == dev && e.kernel == kernel && e.threads == threads) return e.occ;
+  Occupancy o = {0, 0};
+  if (hipDeviceGetAttribute(&o.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&o.per_cu, kernel, threads, 0) != hipSuccess)
+    return {0, 0};
+  cache.push_back({dev, kernel, threads, o});
+  return o;
 }
 
-}  // namespace
-}  // namespace tq
+// Share of the first block of a split pair, in percent of the pair's tokens
+// (rounded up to 16 tokens).  When the grid is exactly two resident
+// workgroups on every CU, blocks u and u + grid/2 run side by side on one
+// CU, and the one dispatched first finishes an equal range well before its
+// partner (43 vs 61 us at 8 x 32k tokens, 8 kv heads, pd 128), which then
+// runs alone on a half-empty CU.  Serving two token ranges from such a pair
+// and giving the first block 62% of their tokens evens out the finish
+// times.  Any other grid keeps equal ranges: there the pairing is not known
+// and an uneven share would only lengthen the tail.
+constexpr int kPairPct = 62;
 
-extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                                  const uint8_t* k_slab, const uint8_t* v_slab,
-                                  const int32_t* indices, const int32_t* indptr,
-                                  const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
-                                  int32_t num_kv_heads, int32_t padded_dim, int32_t block_size,
-                                  int32_t ebs, int64_t num_blocks, float sm_scale,
-                                  const float* signs, int32_t num_splits, int32_t kv_chunk_size,
-                                  float* partition_o, float* partition_lse, tq_stream_t stream) {
-  using namespace tq;
+typedef void (*PartialsFn)(DecodeParams);
+
+// The partials instantiation for a geometry: scores of two tiles share one
+// register set when ratio <= 8 (head size 256 keeps one tile per set: two
+// would exceed the register file); q hi/lo parts share one B operand when
+// the GQA ratio leaves 8 columns free.
+PartialsFn partials_kernel(int pd, int G, int ratio) {
+  const bool pack2 = ratio <= 8 && pd <= 128;
+  const bool qc = ratio <= 8;
+#define TQ_PICK_G(PDV, PK, QCV)                                               \
+  switch (G) {                                                                \
+    case 8: return &decode_partials_kernel<PDV, (PDV == 256 ? 4 : 8), PK, QCV>; \
+    case 4: return &decode_partials_kernel<PDV, 4, PK, QCV>;                 \
+    case 2: return &decode_partials_kernel<PDV, 2, PK, QCV>;                 \
+    default: return &decode_partials_kernel<PDV, 1, PK, QCV>;                \
+  }
+  switch (pd) {
+    case 64:
+      if (pack2) { TQ_PICK_G(64, 2, true) } else { TQ_PICK_G(64, 1, false) }
+    case 128:
+      if (pack2) { TQ_PICK_G(128, 2, true) } else { TQ_PICK_G(128, 1, false) }
+    default:
+      if (qc) { TQ_PICK_G(256, 1, true) } else { TQ_PICK_G(256, 1, false) }
+  }
+#undef TQ_PICK_G
+}
+
+// Checks shared by the partials launchers and the parameter block they fill
+// (everything but the split layout).
+int decode_setup(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* k_slab,
+                 const uint8_t* v_slab, const int32_t* indices, const int32_t* indptr,
+                 const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                 int32_t num_kv_heads, int32_t padded_dim, int32_t block_size, int32_t ebs,
+                 int64_t num_blocks, float sm_scale, const float* signs, float* partition_o,
+                 float* partition_lse, DecodeParams& p) {
   int rc = check_geometry(padded_dim, num_qo_heads, num_kv_heads, block_size, ebs, "decode");
   if (rc) return rc;
-  if (batch < 0 || num_splits < 1 || kv_chunk_size < 1) {
-    set_error("decode: batch %d, num_splits %d, kv_chunk_size %d out of range", batch,
-              num_splits, kv_chunk_size);
+  if (batch < 0) {
+    set_error("decode: batch %d out of range", batch);
     return kEinval;
   }
   if (batch == 0) return 0;
@@ -1328,7 +1539,7 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
     set_error("decode: no workgroup shape for %d kv heads, ratio %d", num_kv_heads, ratio);
     return kEinval;
   }
-  DecodeParams p;
+  p = DecodeParams{};
   p.q = static_cast<const _Float16*>(q);
   p.q_sb = q_stride_b;
   p.q_sh = q_stride_h;
@@ -1347,50 +1558,24 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   p.ratio = ratio;
   p.block_size = block_size;
   p.ebs = ebs;
-  p.S = num_splits;
-  p.cs = kv_chunk_size;
   p.G = G;
   p.HG = num_kv_heads / G;
   p.inv_sqrt_pd = 1.0f / sqrtf((float)pd);
   p.qk_scale = sm_scale * 1.4426950408889634f * p.inv_sqrt_pd / kCbScale;
   p.pv_scale = p.inv_sqrt_pd / kCbScale;
-  const int64_t blocks = (int64_t)batch * num_splits * p.HG;
+  return 0;
+}
+
+int launch_partials(PartialsFn fn, const DecodeParams& p, int64_t blocks, tq_stream_t stream) {
   if (blocks > 0x7fffffffLL) {
     set_error("decode: grid too large");
     return kEinval;
   }
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  dim3 grid((unsigned)blocks), block(64 * G);
-  // scores of two tiles share one register set when ratio <= 8 (head size
-  // 256 keeps one tile per set: two would exceed the register file); q hi/lo
-  // parts share one B operand when the GQA ratio leaves 8 columns free
-  const bool pack2 = ratio <= 8 && pd <= 128;
-  const bool qc = ratio <= 8;
-#define TQ_LAUNCH(PDV, GV, PK, QCV)                                                   \
-  p.pair_first = pair_share(reinterpret_cast<const void*>(                            \
-                                &decode_partials_kernel<PDV, GV, PK, QCV>),           \
-                            64 * GV, blocks, num_splits, kv_chunk_size);              \
-  hipLaunchKernelGGL((decode_partials_kernel<PDV, GV, PK, QCV>), grid, block, 0, st, p)
-#define TQ_LAUNCH_G(PDV, PK, QCV)   \
-  switch (G) {                      \
-    case 8: TQ_LAUNCH(PDV, (PDV == 256 ? 4 : 8), PK, QCV); break; \
-    case 4: TQ_LAUNCH(PDV, 4, PK, QCV); break; \
-    case 2: TQ_LAUNCH(PDV, 2, PK, QCV); break; \
-    default: TQ_LAUNCH(PDV, 1, PK, QCV); \
-  }
-  switch (pd) {
-    case 64:
-      if (pack2) { TQ_LAUNCH_G(64, 2, true) } else { TQ_LAUNCH_G(64, 1, false) }
-      break;
-    case 128:
-      if (pack2) { TQ_LAUNCH_G(128, 2, true) } else { TQ_LAUNCH_G(128, 1, false) }
-      break;
-    default:
-      if (qc) { TQ_LAUNCH_G(256, 1, true) } else { TQ_LAUNCH_G(256, 1, false) }
-  }
-#undef TQ_LAUNCH_G
-#undef TQ_LAUNCH
-  hipError_t e = hipGetLastError();
+  DecodeParams arg = p;
+  void* args[] = {&arg};
+  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)blocks),
+                                 dim3(64 * p.G), args, 0, reinterpret_cast<hipStream_t>(stream));
+  if (e == hipSuccess) e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("decode: launch failed: %s", hipGetErrorString(e));
     return (int)e;
@@ -1398,11 +1583,77 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   return 0;
 }
 
+// The balanced grid for a batch: `units` work units per head group and
+// whether they are served by block pairs.  The plan fills the resident
+// workgroup slots once; a batch larger than that gets one unit per sequence.
+struct BalancedGrid {
+  int units, pair_pct;
+  int64_t blocks;
+  int rows;  // partial rows the plan may use
+};
+int balanced_grid(PartialsFn fn, const DecodeParams& p, int max_rows, BalancedGrid& g) {
+  const Occupancy occ = occupancy(reinterpret_cast<const void*>(fn), 64 * p.G);
+  if (occ.cus <= 0 || occ.per_cu <= 0) {
+    set_error("decode: occupancy query failed");
+    return kEinval;
+  }
+  g.pair_pct = 0;
+  if (occ.per_cu == 2 && occ.cus % p.HG == 0 && occ.cus / p.HG >= p.B &&
+      2 * (occ.cus / p.HG) <= max_rows) {
+    g.units = occ.cus / p.HG;
+    g.pair_pct = kPairPct;
+    g.rows = 2 * g.units;
+    g.blocks = (int64_t)2 * g.units * p.HG;
+    return 0;
+  }
+  g.units = min(max(p.B, occ.cus * occ.per_cu / p.HG), max_rows);
+  if (g.units < p.B) {
+    set_error("decode: the partial workspace holds %d rows, fewer than the batch %d", max_rows,
+              p.B);
+    return kEinval;
+  }
+  g.rows = g.units;
+  g.blocks = (int64_t)g.units * p.HG;
+  return 0;
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                  const uint8_t* k_slab, const uint8_t* v_slab,
+                                  const int32_t* indices, const int32_t* indptr,
+                                  const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                  int32_t num_kv_heads, int32_t padded_dim, int32_t block_size,
+                                  int32_t ebs, int64_t num_blocks, float sm_scale,
+                                  const float* signs, int32_t num_splits, int32_t kv_chunk_size,
+                                  float* partition_o, float* partition_lse, tq_stream_t stream) {
+  using namespace tq;
+  if (num_splits < 1 || kv_chunk_size < 1) {
+    set_error("decode: num_splits %d, kv_chunk_size %d out of range", num_splits,
+              kv_chunk_size);
+    return kEinval;
+  }
+  DecodeParams p;
+  int rc = decode_setup(q, q_stride_b, q_stride_h, k_slab, v_slab, indices, indptr, seq_lens,
+                        batch, num_qo_heads, num_kv_heads, padded_dim, block_size, ebs,
+                        num_blocks, sm_scale, signs, partition_o, partition_lse, p);
+  if (rc || batch == 0) return rc;
+  p.S = num_splits;
+  p.cs = kv_chunk_size;
+  const int64_t blocks = (int64_t)batch * num_splits * p.HG;
+  const PartialsFn fn = partials_kernel(padded_dim, p.G, p.ratio);
+  const Occupancy occ = occupancy(reinterpret_cast<const void*>(fn), 64 * p.G);
+  if (occ.per_cu == 2 && blocks == 2LL * occ.cus && num_splits % 2 == 0)
+    p.pair_pct = kPairPct;
+  return launch_partials(fn, p, blocks, stream);
+}
+
 namespace tq {
-static int combine_splits(const float* partition_o, const float* partition_lse, int step,
-                                 int32_t batch, int32_t num_splits, int32_t num_qo_heads,
-                                 int32_t padded_dim, const float* signs, void* o,
-                                 tq_stream_t stream) {
+static int combine_splits(const float* partition_o, const float* partition_lse,
+                          int32_t batch, int32_t num_splits, const int32_t* split_rows,
+                          int32_t max_rows, int32_t num_qo_heads, int32_t padded_dim,
+                          const float* signs, void* o, tq_stream_t stream) {
   const int pd = padded_dim;
   if (pd != 64 && pd != 128 && pd != 256) {
     set_error("combine: padded_dim must be 64, 128 or 256, got %d", pd);
@@ -1425,26 +1676,27 @@ static int combine_splits(const float* partition_o, const float* partition_lse, 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const float isq = 1.0f / sqrtf((float)pd);
   _Float16* out = static_cast<_Float16*>(o);
-  // LDS: split weights, later reused for the group partial sums (256*4 floats)
-  // weights of the splits, or the group sums [NG][pd] plus the group denominators
-  const size_t lds = sizeof(float) * (size_t)(num_splits > 1024 + 64 ? num_splits : 1024 + 64);
+  // LDS: the weights of a sequence's splits, or the group sums [NG][pd] plus
+  // the group denominators
+  const int max_splits = split_rows ? max_rows : num_splits;
+  const size_t lds = sizeof(float) * (size_t)(max_splits > 1024 + 64 ? max_splits : 1024 + 64);
   if (lds > 60 * 1024) {
-    set_error("combine: num_splits %d too large", num_splits);
+    set_error("combine: %d splits per sequence is too many", max_splits);
     return kEinval;
   }
   dim3 grid((unsigned)blocks), block(256);
   switch (pd) {
     case 64:
       hipLaunchKernelGGL(combine_kernel<64>, grid, block, lds, st, partition_o, partition_lse,
-                         num_splits, step, num_qo_heads, signs, isq, out);
+                         num_splits, split_rows, num_qo_heads, signs, isq, out);
       break;
     case 128:
       hipLaunchKernelGGL(combine_kernel<128>, grid, block, lds, st, partition_o, partition_lse,
-                         num_splits, step, num_qo_heads, signs, isq, out);
+                         num_splits, split_rows, num_qo_heads, signs, isq, out);
       break;
     default:
       hipLaunchKernelGGL(combine_kernel<256>, grid, block, lds, st, partition_o, partition_lse,
-                         num_splits, step, num_qo_heads, signs, isq, out);
+                         num_splits, split_rows, num_qo_heads, signs, isq, out);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -1454,14 +1706,57 @@ static int combine_splits(const float* partition_o, const float* partition_lse, 
   return 0;
 }
 
+// Balanced split: partials over a device-computed plan, then the combine
+// over the row table the partials kernel wrote.
+static int decode_balanced(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                           const uint8_t* k_slab, const uint8_t* v_slab, const int32_t* indices,
+                           const int32_t* indptr, const int32_t* seq_lens, int32_t batch,
+                           int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t padded_dim, int32_t block_size, int32_t ebs,
+                           int64_t num_blocks, float sm_scale, const float* signs,
+                           int32_t max_rows, float* partition_o, float* partition_lse,
+                           int32_t* split_rows, void* o, tq_stream_t stream) {
+  if (head_dim <= 0 || head_dim > padded_dim) {
+    set_error("decode: head_dim %d exceeds padded_dim %d", head_dim, padded_dim);
+    return kEinval;
+  }
+  DecodeParams p;
+  int rc = decode_setup(q, q_stride_b, q_stride_h, k_slab, v_slab, indices, indptr, seq_lens,
+                        batch, num_qo_heads, num_kv_heads, padded_dim, block_size, ebs,
+                        num_blocks, sm_scale, signs, partition_o, partition_lse, p);
+  if (rc || batch == 0) return rc;
+  if (batch > kPlanMaxBatch) {
+    set_error("decode: a balanced plan takes at most %d sequences, got %d", kPlanMaxBatch,
+              batch);
+    return kEinval;
+  }
+  if (!split_rows || !o) {
+    set_error("decode: null pointer");
+    return kEinval;
+  }
+  const PartialsFn fn = partials_kernel(padded_dim, p.G, p.ratio);
+  BalancedGrid g;
+  rc = balanced_grid(fn, p, max_rows, g);
+  if (rc) return rc;
+  p.S = 1;
+  p.cs = 1;
+  p.units = g.units;
+  p.pair_pct = g.pair_pct;
+  p.split_out = split_rows;
+  rc = launch_partials(fn, p, g.blocks, stream);
+  if (rc) return rc;
+  return combine_splits(partition_o, partition_lse, batch, 1, split_rows, g.rows,
+                        num_qo_heads, padded_dim, signs, o, stream);
+}
+
 }  // namespace tq
 
 extern "C" int tq_combine_splits(const float* partition_o, const float* partition_lse,
                                  int32_t batch, int32_t num_splits, int32_t num_qo_heads,
                                  int32_t padded_dim, const float* signs, void* o,
                                  tq_stream_t stream) {
-  return tq::combine_splits(partition_o, partition_lse, 1, batch, num_splits, num_qo_heads,
-                            padded_dim, signs, o, stream);
+  return tq::combine_splits(partition_o, partition_lse, batch, num_splits, nullptr, 0,
+                            num_qo_heads, padded_dim, signs, o, stream);
 }
 
 extern "C" int tq_decode_paged_splitkv(const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -1484,7 +1779,44 @@ extern "C" int tq_decode_paged_splitkv(const void* q, int64_t q_stride_b, int64_
                               block_size, ebs, num_blocks, sm_scale, signs, num_splits,
                               kv_chunk_size, partition_o, partition_lse, stream);
   if (rc) return rc;
-  // rows the partials kernel merged away are skipped
-  return tq::combine_splits(partition_o, partition_lse, 1, batch, num_splits, num_qo_heads,
-                            padded_dim, signs, o, stream);
+  return tq::combine_splits(partition_o, partition_lse, batch, num_splits, nullptr, 0,
+                            num_qo_heads, padded_dim, signs, o, stream);
+}
+
+extern "C" int tq_decode_paged_balanced(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                        const uint8_t* k_slab, const uint8_t* v_slab,
+                                        const int32_t* indices, const int32_t* indptr,
+                                        const int32_t* seq_lens, int32_t batch,
+                                        int32_t num_qo_heads, int32_t num_kv_heads,
+                                        int32_t head_dim, int32_t padded_dim,
+                                        int32_t block_size, int32_t ebs, int64_t num_blocks,
+                                        float sm_scale, const float* signs, int32_t max_rows,
+                                        float* partition_o, float* partition_lse,
+                                        int32_t* split_rows, void* o, tq_stream_t stream) {
+  return tq::decode_balanced(q, q_stride_b, q_stride_h, k_slab, v_slab, indices, indptr,
+                             seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, padded_dim,
+                             block_size, ebs, num_blocks, sm_scale, signs, max_rows,
+                             partition_o, partition_lse, split_rows, o, stream);
+}
+
+extern "C" int tq_decode_balanced_rows(int32_t batch, int32_t num_qo_heads,
+                                       int32_t num_kv_heads, int32_t padded_dim) {
+  using namespace tq;
+  const int ratio = num_kv_heads > 0 ? num_qo_heads / num_kv_heads : 0;
+  const int G = num_kv_heads > 0 && num_qo_heads % num_kv_heads == 0 && ratio <= 16 &&
+                        (padded_dim == 64 || padded_dim == 128 || padded_dim == 256)
+                    ? decode_group_size(padded_dim, num_kv_heads, ratio)
+                    : 0;
+  if (G == 0 || batch < 0) {
+    set_error("decode_balanced_rows: unsupported geometry");
+    return kEinval;
+  }
+  const PartialsFn fn = partials_kernel(padded_dim, G, ratio);
+  const Occupancy occ = occupancy(reinterpret_cast<const void*>(fn), 64 * G);
+  if (occ.cus <= 0 || occ.per_cu <= 0) {
+    set_error("decode_balanced_rows: occupancy query failed");
+    return kEinval;
+  }
+  const int hg = num_kv_heads / G;
+  return max(max(batch, occ.cus * occ.per_cu / hg), 2 * (occ.cus / hg));
 }

@@ -4,6 +4,9 @@
   csrc/src/quantize_write_binding.cu:285-286 (reference).
 * ``torch.ops.turboquant_v5.decode_v5_from_cache_paged_splitkv_ws`` — schema of
   csrc/src/decode_v5_tc_binding.cu:966-973 (reference).
+* ``torch.ops.turboquant_v5.decode_paged_balanced_ws`` — the same decode with
+  the split plan made on the GPU from seq_lens (ragged batches); the
+  backend's default.
 * ``torch.ops.turboquant_v5.decode_v5_from_cache_ws`` and
   ``decode_v5_from_cache_splitkv_ws`` — schemas of decode_v5_tc_binding.cu:948-964,
   the non-split (graph-safe) and gather-then-split ops the reference backend
@@ -42,7 +45,6 @@ def quantize_write_kv_cache(kv_cache: torch.Tensor, key: torch.Tensor, value: to
     quantize_write_kv_cache (quantize_write_binding.cu:207-269) including its
     checks; key/value may be fp32 (as the reference requires), fp16 or bf16.
     """
-    _require_gpu(kv_cache, key, value, signs, slot_mapping)
     if kv_cache.dim() != 5 or kv_cache.size(0) != 2:
         raise RuntimeError("kv_cache leading dim must be 2 (K,V)")
     if slot_mapping.dtype != torch.int32:
@@ -51,6 +53,11 @@ def quantize_write_kv_cache(kv_cache: torch.Tensor, key: torch.Tensor, value: to
         raise RuntimeError(f"key/value must share a float dtype, got {key.dtype}/{value.dtype}")
     if key.dim() != 3 or value.shape != key.shape:
         raise RuntimeError("key/value must be [num_tokens, num_heads, head_dim]")
+    if key.size(2) < head_dim:
+        # the kernel reads head_dim elements of every row
+        raise RuntimeError(f"key/value rows hold {key.size(2)} elements, fewer than "
+                           f"head_dim {head_dim}")
+    _require_gpu(kv_cache, key, value, signs, slot_mapping)
     if key.stride(-1) != 1 or value.stride(-1) != 1:
         raise RuntimeError("key/value last dim must be contiguous")
     ebs = kv_cache.size(-1) * kv_cache.element_size()
@@ -125,6 +132,81 @@ def decode_paged_splitkv(q: torch.Tensor, kv_cache: torch.Tensor, indices: torch
             int(kv_chunk_size), partition_o.data_ptr(), partition_lse.data_ptr(), o.data_ptr(),
             _stream_ptr(q.device))
     _lib.check(rc, "decode_paged_splitkv")
+    return o
+
+
+def balanced_rows(batch: int, num_qo_heads: int, num_kv_heads: int, padded_dim: int,
+                  device: torch.device | None = None) -> int:
+    """Partial rows a balanced decode of this geometry may use on `device`
+    (the resident workgroup slots of the partials kernel, at least one per
+    sequence): size partition_o [rows, Hq, pd] and partition_lse [rows, Hq]."""
+    lib = _lib.load()
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        rows = lib.tq_decode_balanced_rows(int(batch), int(num_qo_heads), int(num_kv_heads),
+                                           int(padded_dim))
+    if rows < 0:
+        _lib.check(rows, "decode_balanced_rows")
+    return rows
+
+
+def decode_paged_balanced(q: torch.Tensor, kv_cache: torch.Tensor, indices: torch.Tensor,
+                          indptr: torch.Tensor, seq_lens: torch.Tensor, num_kv_heads: int,
+                          head_dim: int, padded_dim: int, sm_scale: float,
+                          signs: torch.Tensor | None, o: torch.Tensor,
+                          partition_o: torch.Tensor, partition_lse: torch.Tensor,
+                          split_indptr: torch.Tensor) -> torch.Tensor:
+    """Split-KV decode with the split plan made on the GPU from seq_lens:
+    every work unit covers about the same number of tokens whatever the
+    length mix of the batch (the reference sizes splits from max_len,
+    vllm_backend_fused.py:128-156).  split_indptr int32 [B + 2] receives the
+    partial-row table (sequence b owns rows split_indptr[b] ..
+    split_indptr[b + 1]) and, last, the unit size in tokens.  No host read,
+    so it can be captured in a HIP graph whose seq_lens change per replay."""
+    _require_gpu(q, kv_cache, indices, indptr, seq_lens, o, partition_o, partition_lse,
+                 split_indptr)
+    if q.dtype != torch.float16 or q.dim() != 3 or q.size(2) != padded_dim or q.stride(2) != 1:
+        raise RuntimeError("q must be fp16 [B, Hq, padded_dim] with a contiguous last dim")
+    b, hq, pd = q.shape
+    for t, name in ((indices, "indices"), (indptr, "indptr"), (seq_lens, "seq_lens"),
+                    (split_indptr, "split_indptr")):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise RuntimeError(f"{name} must be a contiguous int32 tensor")
+    if seq_lens.numel() < b or indptr.numel() < b:
+        raise RuntimeError("seq_lens / indptr shorter than the batch")
+    if split_indptr.numel() < b + 2:
+        raise RuntimeError("split_indptr must hold batch + 2 entries")
+    if tuple(o.shape) != (b, hq, pd) or o.dtype != torch.float16 or not o.is_contiguous():
+        raise RuntimeError("o_ws shape mismatch")
+    if (partition_o.dtype != torch.float32 or partition_o.dim() != 3
+            or tuple(partition_o.shape[1:]) != (hq, pd) or not partition_o.is_contiguous()):
+        raise RuntimeError("partition_o_ws must be fp32 [rows, Hq, padded_dim]")
+    rows = partition_o.size(0)
+    if (partition_lse.dtype != torch.float32 or partition_lse.numel() < rows * hq
+            or not partition_lse.is_contiguous()):
+        raise RuntimeError("partition_lse_ws must be fp32 [rows, Hq]")
+    if kv_cache.dim() != 5 or kv_cache.size(0) != 2 or not kv_cache.is_contiguous():
+        raise RuntimeError("kv_cache must be contiguous [2, num_blocks, block_size, H, ebs]")
+    _, nb, bs, hk, _ = kv_cache.shape
+    if hk != num_kv_heads:
+        raise RuntimeError(f"kv_cache has {hk} kv heads, num_kv_heads={num_kv_heads}")
+    ebs = kv_cache.size(-1) * kv_cache.element_size()
+    sp = 0
+    if signs is not None and signs.numel() > 0:
+        if signs.dtype != torch.float32 or signs.numel() < pd:
+            raise RuntimeError("hadamard_signs must be fp32 [padded_dim]")
+        _require_gpu(signs)
+        sp = signs.data_ptr()
+    lib = _lib.load()
+    base = kv_cache.data_ptr()
+    slab = nb * bs * hk * ebs
+    with torch.cuda.device(q.device):
+        rc = lib.tq_decode_paged_balanced(
+            q.data_ptr(), q.stride(0), q.stride(1), base, base + slab, indices.data_ptr(),
+            indptr.data_ptr(), seq_lens.data_ptr(), b, hq, int(num_kv_heads), int(head_dim),
+            int(padded_dim), bs, ebs, nb, float(sm_scale), sp, rows, partition_o.data_ptr(),
+            partition_lse.data_ptr(), split_indptr.data_ptr(), o.data_ptr(),
+            _stream_ptr(q.device))
+    _lib.check(rc, "decode_paged_balanced")
     return o
 
 
@@ -289,13 +371,13 @@ def decode_v5_from_cache(q, kv_cache, indices, indptr, last_page_len, seq_lens, 
                          nbytes):
     """The eager decode_v5_from_cache (decode_v5_tc_binding.cu:324-423): it
     allocates its own output and workspaces (not graph-capturable, as in the
-    reference); max_len is the page-table width times page_size."""
+    reference).  max_len is seq_lens.max(), as the reference computes it
+    (decode_v5_tc_binding.cu:350); the op is eager, so this host read is
+    allowed.  A CSR indptr whose later rows are longer than the first is
+    covered."""
     from .geometry import choose_splits
     b, hq, pd = q.size(0), q.size(1), int(padded_dim)
-    if b and indptr.numel() > 1:
-        max_len = int(indptr[1] - indptr[0]) * int(page_size)
-    else:
-        max_len = int(page_size)
+    max_len = int(seq_lens[:b].max()) if b else 0
     max_len = max(max_len, int(page_size))
     splits, chunk = choose_splits(b, max_len, int(num_kv_heads), hq, pd)
     o = torch.empty((b, hq, pd), dtype=torch.float16, device=q.device)
@@ -304,6 +386,25 @@ def decode_v5_from_cache(q, kv_cache, indices, indptr, last_page_len, seq_lens, 
     return decode_paged_splitkv(q, kv_cache, indices, indptr, seq_lens, int(num_kv_heads),
                                 int(head_dim), pd, float(sm_scale), hadamard_signs, o, po, pl,
                                 splits, chunk)
+
+
+def _register_fakes() -> None:
+    """Meta ("fake") kernels, so that torch.compile and vLLM's graph capture
+    can trace the ops without running them: the write mutates its cache
+    argument and returns nothing; the decode ops return a tensor shaped like
+    o_ws (fp16 [B, Hq, padded_dim])."""
+    from torch.library import register_fake
+
+    @register_fake("turboquant_write::quantize_write_kv_cache", lib=_libs[0])
+    def _write_fake(kv_cache, key, value, signs, slot_mapping, head_dim, padded_dim):
+        return None
+
+    def _decode_fake(q, kv_cache, *args):
+        return q.new_empty((q.size(0), q.size(1), q.size(2)), dtype=torch.float16)
+
+    for name in ("decode_v5_from_cache_paged_splitkv_ws", "decode_v5_from_cache_ws",
+                 "decode_v5_from_cache_splitkv_ws", "decode_paged_balanced_ws"):
+        register_fake(f"turboquant_v5::{name}", _decode_fake, lib=_libs[1])
 
 
 def register_ops() -> None:
@@ -344,5 +445,13 @@ def register_ops() -> None:
              "Tensor request_indices, Tensor kv_tile_indices, "
              "Tensor split_indptr, Tensor kv_chunk_size_t, int num_splits) -> Tensor")
     d.impl("decode_v5_from_cache_splitkv_ws", _from_cache_splitkv_ws, "CUDA")
+    # this build's balanced-split decode (no reference counterpart: the
+    # reference plans splits on the host from max_len)
+    d.define("decode_paged_balanced_ws(Tensor q, Tensor kv_cache, Tensor indices, "
+             "Tensor indptr, Tensor seq_lens, int num_kv_heads, int head_dim, "
+             "int padded_dim, float sm_scale, Tensor hadamard_signs, Tensor o_ws, "
+             "Tensor partition_o_ws, Tensor partition_lse_ws, Tensor split_indptr) -> Tensor")
+    d.impl("decode_paged_balanced_ws", decode_paged_balanced, "CUDA")
     _libs.extend([w, d])
+    _register_fakes()
     _registered = True

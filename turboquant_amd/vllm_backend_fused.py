@@ -24,6 +24,7 @@ import traceback
 import torch
 import torch.nn.functional as F
 
+from .decoder_dispatch import KERNEL_NAME
 from .geometry import (QUANT_BYTES_PER_CHUNK, TILE_DIMS, choose_splits, entry_bytes,
                        hadamard_signs, padded_dim)
 
@@ -127,8 +128,10 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
     """Quantized KV cache with the HIP kernels (vllm_backend_fused.py:93-468).
 
     Write: do_kv_cache_update -> turboquant_write::quantize_write_kv_cache.
-    Decode: forward (max_query_len == 1) ->
-            turboquant_v5::decode_v5_from_cache_paged_splitkv_ws.
+    Decode: forward (max_query_len == 1) -> turboquant_v5::decode_paged_balanced_ws
+            (split plan made on the GPU from seq_lens), or the reference's
+            turboquant_v5::decode_v5_from_cache_paged_splitkv_ws with
+            TQ_FORCE_KERNEL=gfx950_static.
     Prefill / mixed batches: _prefill_mixed (decode rows through the decode
     kernel, chunks with cached context over the dequantized context plus the
     fresh chunk, fresh prompts as in the reference, vllm_backend_fused.py:335-371).
@@ -165,9 +168,26 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
         (vllm_backend_fused.py:158-215): allocated on the first call of a
         shape bucket (vLLM warm-up), reused by graph replays.
         Returns (ws, max_len, num_splits)."""
-        key = (batch_size, max_pages)
+        key = (batch_size, max_pages, self._decode_op_name)
         max_len = max_pages * block_size
         ws = self._v5_ws_cache.get(key)
+        if ws is None and self._decode_op_name == KERNEL_NAME:
+            # balanced plan: rows for the resident workgroup slots, the row
+            # table written by the kernel
+            from .ops import balanced_rows
+            rows = balanced_rows(batch_size, self.num_heads, self.num_kv_heads, self._pd,
+                                 device)
+            ws = {
+                "o": torch.empty((batch_size, self.num_heads, self._pd), dtype=torch.float16,
+                                 device=device),
+                "num_splits": 0,
+                "partition_o": torch.empty((rows, self.num_heads, self._pd),
+                                           dtype=torch.float32, device=device),
+                "partition_lse": torch.empty((rows, self.num_heads), dtype=torch.float32,
+                                             device=device),
+                "split_indptr": torch.zeros(batch_size + 2, dtype=torch.int32, device=device),
+            }
+            self._v5_ws_cache[key] = ws
         if ws is None:
             num_splits, chunk = choose_splits(batch_size, max_len, self.num_kv_heads,
                                              self.num_heads, self._pd)
@@ -378,12 +398,18 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
             ws, max_len, num_splits = self._get_v5_ws(batch_size, max_pages, block_size,
                                                       q.device)
             sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
-            result = self._decode_op(
-                q_fp16, kv_cache, kv_indices, kv_indptr, kv_last_page_len, sl,
-                self.num_kv_heads, block_size, self.head_size, self._pd, self.scale,
-                self._signs, self._qbytes, self._nbytes, ws["o"], max_len,
-                ws["partition_o"], ws["partition_lse"], ws["request_indices"],
-                ws["kv_tile_indices"], ws["split_indptr"], ws["kv_chunk_size"], num_splits)
+            if self._decode_op_name == KERNEL_NAME:
+                result = self._decode_op(
+                    q_fp16, kv_cache, kv_indices, kv_indptr, sl, self.num_kv_heads,
+                    self.head_size, self._pd, self.scale, self._signs, ws["o"],
+                    ws["partition_o"], ws["partition_lse"], ws["split_indptr"])
+            else:
+                result = self._decode_op(
+                    q_fp16, kv_cache, kv_indices, kv_indptr, kv_last_page_len, sl,
+                    self.num_kv_heads, block_size, self.head_size, self._pd, self.scale,
+                    self._signs, self._qbytes, self._nbytes, ws["o"], max_len,
+                    ws["partition_o"], ws["partition_lse"], ws["request_indices"],
+                    ws["kv_tile_indices"], ws["split_indptr"], ws["kv_chunk_size"], num_splits)
             out3 = output[:num_actual].view(num_actual, self.num_heads, self.head_size)
             if self.head_size < self._pd:
                 out3.copy_(result[:num_actual, :, :self.head_size])

@@ -1,15 +1,16 @@
 """vLLM plugin entry point (reference turboquant/vllm_plugin.py:85-92).
 
 Declared in pyproject.toml as
-``[project.entry-points."vllm.general_plugins"] turboquant = "turboquant_amd.vllm_plugin:register"``.
+``[project.entry-points."vllm.general_plugins"] turboquant = "turboquant.vllm_plugin:register"``
+(``turboquant.X`` is this module under the reference's import path).
 ``register()`` is idempotent and maps the ``CUSTOM`` attention backend to
-``turboquant_amd.vllm_backend_fused.TurboQuantBackend`` (the registration the
+``turboquant.vllm_backend_fused.TurboQuantBackend`` (the registration the
 reference's archived CUSTOM backend needs; its snapshot only patches Triton
 kernels).  vLLM is imported inside the function, never at module import.
 """
 from __future__ import annotations
 
-BACKEND_PATH = "turboquant_amd.vllm_backend_fused.TurboQuantBackend"
+BACKEND_PATH = "turboquant.vllm_backend_fused.TurboQuantBackend"
 
 _registered = False
 _registration: str | None = None  # how the backend was registered (diagnostics)
