@@ -120,6 +120,29 @@ int tq_decode_paged_balanced(const void* q, int64_t q_stride_b, int64_t q_stride
                              int32_t* split_rows, void* o, tq_stream_t stream);
 
 /*
+ * tq_decode_paged_balanced without workspace arguments and without any
+ * allocation: the row table, partial LSEs and partial rows live in a
+ * 16 MiB device array inside this library (one per GPU, kept until the
+ * process ends), found once per device with hipGetSymbolAddress.  No
+ * counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * The caller still passes inputs and o.  Limit: batch * num_qo_heads *
+ * (padded_dim + 1) * 4 bytes of partials must fit the array (it is refused
+ * with -22 otherwise; at most 1024 sequences); larger batches use fewer
+ * rows per sequence, down to one.  Calls that overlap on one GPU (two
+ * streams, or two threads) share the array and race: serialise them.
+ */
+int tq_decode_paged_balanced_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                     const uint8_t* k_slab, const uint8_t* v_slab,
+                                     const int32_t* indices, const int32_t* indptr,
+                                     const int32_t* seq_lens, int32_t batch,
+                                     int32_t num_qo_heads, int32_t num_kv_heads,
+                                     int32_t head_dim, int32_t padded_dim,
+                                     int32_t block_size, int32_t ebs, int64_t num_blocks,
+                                     float sm_scale, const float* signs, void* o,
+                                     tq_stream_t stream);
+
+/*
  * Partial rows tq_decode_paged_balanced uses at most for this geometry on
  * the current device (or -22).  Queries the device once per geometry.
  */

@@ -39,7 +39,6 @@
 
 #include <mutex>
 #include <type_traits>
-#include <vector>
 
 #include "tq_common.h"
 
@@ -1445,18 +1444,22 @@ Occupancy occupancy(const void* kernel, int threads) {
     int threads;
     Occupancy occ;
   };
+  // a fixed table (no allocation on any call): a few kernels per device
+  constexpr int kEntries = 256;
   static std::mutex mu;
-  static std::vector<Entry> cache;
+  static Entry cache[kEntries];
+  static int used = 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return {0, 0};
   std::lock_guard<std::mutex> lock(mu);
-  for (const Entry& e : cache)
-    if (e.dev == dev && e.kernel == kernel && e.threads == threads) return e.occ;
+  for (int i = 0; i < used; i++)
+    if (cache[i].dev == dev && cache[i].kernel == kernel && cache[i].threads == threads)
+      return cache[i].occ;
   Occupancy o = {0, 0};
   if (hipDeviceGetAttribute(&o.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&o.per_cu, kernel, threads, 0) != hipSuccess)
     return {0, 0};
-  cache.push_back({dev, kernel, threads, o});
+  if (used < kEntries) cache[used++] = {dev, kernel, threads, o};
   return o;
 }
 
@@ -1797,6 +1800,89 @@ extern "C" int tq_decode_paged_balanced(const void* q, int64_t q_stride_b, int64
                              seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, padded_dim,
                              block_size, ebs, num_blocks, sm_scale, signs, max_rows,
                              partition_o, partition_lse, split_rows, o, stream);
+}
+
+namespace tq {
+namespace {
+
+// Workspace of tq_decode_paged_balanced_noalloc: the row table, the partial
+// LSEs and the partial rows of one call, in a file-scope device array (one
+// copy per GPU, held until the process ends).  In host code `scratch` names
+// a host-side stand-in, never the device memory: host code uses only the
+// per-device address from hipGetSymbolAddress.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+int scratch_ptr(uint8_t** out) {
+  static std::mutex mu;
+  static uint8_t* ptrs[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("decode_noalloc: no usable current device");
+    return e != hipSuccess ? (int)e : kEinval;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error("decode_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                hipGetErrorString(e));
+      return e != hipSuccess ? (int)e : kEinval;
+    }
+    ptrs[dev] = static_cast<uint8_t*>(ptr);
+  }
+  *out = ptrs[dev];
+  return 0;
+}
+
+constexpr size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+}  // namespace
+}  // namespace tq
+
+extern "C" int tq_decode_paged_balanced_noalloc(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* k_slab,
+    const uint8_t* v_slab, const int32_t* indices, const int32_t* indptr,
+    const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t padded_dim, int32_t block_size, int32_t ebs, int64_t num_blocks,
+    float sm_scale, const float* signs, void* o, tq_stream_t stream) {
+  using namespace tq;
+  if (batch < 0 || batch > kPlanMaxBatch || num_qo_heads <= 0 ||
+      (padded_dim != 64 && padded_dim != 128 && padded_dim != 256)) {
+    set_error("decode_noalloc: batch %d, num_qo_heads %d, padded_dim %d out of range", batch,
+              num_qo_heads, padded_dim);
+    return kEinval;
+  }
+  if (batch == 0) return 0;
+  uint8_t* base = nullptr;
+  int rc = scratch_ptr(&base);
+  if (rc) return rc;
+  // [row table: batch + 2 int32][lse: rows x Hq f32][partials: rows x Hq x pd f32]
+  const size_t table = align256((size_t)(batch + 2) * 4);
+  const size_t per_row = (size_t)num_qo_heads * 4 * (1 + (size_t)padded_dim);
+  const size_t avail = kScratchBytes - table - 256;
+  const int64_t fit = (int64_t)(avail / per_row);
+  if (fit < batch) {
+    set_error("decode_noalloc: %d sequences x %d heads x pd %d need %zu bytes of partials, "
+              "more than the %zu-byte scratch (use tq_decode_paged_balanced with a workspace)",
+              batch, num_qo_heads, padded_dim, (size_t)batch * per_row + table, kScratchBytes);
+    return kEinval;
+  }
+  const int rows = (int)(fit < 0x7fffffff ? fit : 0x7fffffff);
+  int32_t* split_rows = reinterpret_cast<int32_t*>(base);
+  float* plse = reinterpret_cast<float*>(base + table);
+  float* po = reinterpret_cast<float*>(base + table +
+                                       align256((size_t)rows * num_qo_heads * 4));
+  return tq::decode_balanced(q, q_stride_b, q_stride_h, k_slab, v_slab, indices, indptr,
+                             seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, padded_dim,
+                             block_size, ebs, num_blocks, sm_scale, signs, rows, po, plse,
+                             split_rows, o, stream);
 }
 
 extern "C" int tq_decode_balanced_rows(int32_t batch, int32_t num_qo_heads,
