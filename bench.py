@@ -1,11 +1,19 @@
 """Decode-attention throughput on the packed TurboQuant KV cache (MI355X).
 
-Workload (Qwen3-8B geometry): q fp16 [8, 32, 128],
+Headline workload (Qwen3-8B geometry): q fp16 [8, 32, 128],
 8 sequences x 32768 cached tokens, 8 KV heads, head_dim 128, 16-token pages
 assigned by a seeded random permutation of a 16384-page pool, split-KV + LSE
 merge.  One step = one decode-attention call (partials kernel + combine
-kernel) over the resident cache.  Also measured: the write kernel on
-configs[1] (8192 tokens x 8 heads, K and V, outlier channels, permuted slots).
+kernel) over the resident cache, through the op the vLLM backend calls
+(turboquant_v5::decode_paged_balanced_ws: split plan made on the GPU).
+
+Also measured, as fields of the same line: configs[3] ragged batches (B=64,
+L ~ U[1024, 32768], Student-t K) at head sizes 64/128/256 with the balanced
+plan and with the reference's max_len-based splits; configs[4] end to end
+(random-init Qwen3-8B architecture, 8 x 32768-token prompts, 256 output
+tokens, through TurboQuantFusedImpl); the write kernel on configs[1]; the
+context read-back kernel; and the CPU baseline (a torch-CPU fp32 port of the
+reference's PyTorch path, oracle/torch_ref.py) on the host cores.
 
 Prints ONE JSON line.  value = algorithmic bytes per step / step time, where
 algorithmic bytes = codes + norms of every (token, kv head, K|V) + page-table
@@ -30,6 +38,8 @@ HBM_PEAK_GBS = 8000.0
 # 256 MiB device copy (profiles/decode_partials_cfg3_hbm_traffic.md); keyed by
 # (num_splits, kv_chunk_size) so an overridden layout reports null.
 PROFILED_TRAFFIC = {(64, 512): 346448681}
+TRAFFIC_SOURCE = ("profiled constant: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel at "
+                  "this layout, profiles/decode_partials_cfg3_hbm_traffic.md")
 
 
 def log(msg):
@@ -121,39 +131,135 @@ def time_graph(torch, fn, steps, warmup, per_graph=10):
     return e0.elapsed_time(e1) / (reps * per_graph)  # ms
 
 
-def cpu_baseline(torch, w, budget_s=12.0):
-    """The C oracle (dequantize-then-attend, OpenMP) on the host cores, on a
-    bounded sample: whole sequences of the same workload, repeated until
-    `budget_s` of CPU time is spent; reported in the same GB/s unit."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _median_time(fn, runs=5):
+    fn()  # warm-up run
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(torch, w):
+    """The reference's PyTorch path restated in torch on the CPU
+    (oracle/torch_ref.py, fp32): decode = dequantize, rotate q, GQA softmax
+    attention per (sequence, kv head), inverse rotation
+    (turboquant/triton_decode_ref.py:89-131, 264-299), timed on a bounded
+    sample of the configs[2] workload (one of the 8 sequences, all heads);
+    write = the configs[1] write as whole-tensor torch ops.  One warm-up run,
+    then the median of 5, on the host cores in this process."""
+    from oracle import torch_ref
+    from tests import workloads as W
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    cache = w["cache"].cpu()
+    q = w["q"][:1].cpu()
+    bt = w["bt"][:1].cpu()
+    signs = w["signs"].cpu()
+    L = w["seq_len"]
+    seq = torch.tensor([L], dtype=torch.int32)
+    med, n = _median_time(lambda: torch_ref.decode(q, cache, bt, seq, w["hkv"], w["pd"],
+                                                   1.0 / math.sqrt(w["hd"]), signs))
+    sample = dict(w, batch=1)
+    nbytes = alg_bytes(sample)
+    c = W.cfg2()
+    shape, pd = W.cache_bytes(c["num_blocks"], 8, 128)
+    wcache = torch.zeros(shape, dtype=torch.uint8)
+    k, v = torch.from_numpy(c["k"]), torch.from_numpy(c["v"])
+    slots = torch.from_numpy(c["slots"])
+    wmed, wn = _median_time(lambda: torch_ref.write_kv_cache(wcache, k, v, signs, slots, pd))
+    wbytes = W.algorithmic_write_bytes(8192, 8, 128)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "cpu": cpu_model(),
+            "sample": f"1 of the 8 configs[2] sequences ({L} tokens, 8 kv heads, 32 q heads; "
+                      f"same cache, q, page table), median of {n} runs after one warm-up: "
+                      f"{med * 1e3:.1f} ms; oracle/torch_ref.py fp32 torch-CPU port of the "
+                      f"reference's dequantize-then-attend, {threads} threads",
+            "write": {"value": round(wbytes / wmed / 1e9, 3), "unit": "GB/s",
+                      "ms": round(wmed * 1e3, 2),
+                      "sample": "configs[1] in full (8192 tokens x 8 heads, K+V), median of "
+                                f"{wn} runs after one warm-up"}}
+
+
+def bench_ragged(torch, steps, warmup):
+    """B=64, L ~ U[1024, 32768] (seed 4), K Student-t(3), V N(0,1),
+    at head sizes 128 (32q/8kv), 64 (16q/4kv) and 256 (16q/2kv); the balanced
+    op against the reference's max_len-based static splits, same cache."""
     import numpy as np
 
-    import oracle
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    cache = w["cache"].cpu().numpy()
-    q = w["q"].cpu().numpy()
-    bt = w["bt"].cpu().numpy()
-    signs = w["signs"].cpu().numpy()
-    nseq = 2
-    per = w["pd"] // 2 + 2 * (w["pd"] // 64)
-    L = w["seq_len"]
-    sample_bytes = nseq * L * w["hkv"] * 2 * per + nseq * (L // 16) * 4 + 2 * nseq * w["hq"] * w["pd"] * 2
-    ip = np.arange(nseq + 1, dtype=np.int32) * bt.shape[1]
-    times = []
-    t_start = time.time()
-    while True:
-        t0 = time.perf_counter()
-        oracle.decode(q[:nseq], cache, bt[:nseq].reshape(-1), ip,
-                      np.full(nseq, L, np.int32), w["hkv"], w["pd"], 1.0 / math.sqrt(w["hd"]),
-                      signs)
-        times.append(time.perf_counter() - t0)
-        if time.time() - t_start > budget_s or len(times) >= 20:
-            break
-    med = statistics.median(times)
-    return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{nseq} of 8 sequences x {L} tokens (same cache, q, page table), "
-                      f"{len(times)} runs, median {med * 1e3:.1f} ms; oracle/tq_oracle.c "
-                      f"fp64-accumulated dequantize-then-attend, OpenMP {threads} threads"}
+    from tests import gpu_cases as G
+    from tests import workloads as W
+    from turboquant_amd import ops
+    from turboquant_amd.geometry import choose_splits, hadamard_signs
+    out = []
+    lens = np.random.default_rng(4).integers(1024, 32768 + 1, size=64)
+    for hd in (128, 64, 256):
+        hq, hkv = {64: (16, 4), 128: (32, 8), 256: (16, 2)}[hd]
+        case, cache, pd = G.device_case(4 + 1000 * hd, lens, hq, hkv, hd, k_dist="t3")
+        d = G.decode_inputs(case, pd)
+        b = len(lens)
+        dev = cache.device
+        signs = hadamard_signs(pd, dev)
+        scale = 1.0 / math.sqrt(hd)
+        rows = ops.balanced_rows(b, hq, hkv, pd)
+        o = torch.empty((b, hq, pd), dtype=torch.float16, device=dev)
+        po = torch.empty((rows, hq, pd), dtype=torch.float32, device=dev)
+        pl = torch.empty((rows, hq), dtype=torch.float32, device=dev)
+        split = torch.zeros(b + 2, dtype=torch.int32, device=dev)
+        ms_b = time_graph(torch, lambda: ops.decode_paged_balanced(
+            d["q"], cache, d["indices"], d["indptr"], d["seq"], hkv, hd, pd, scale, signs, o,
+            po, pl, split), steps, warmup)
+        max_len = case["block_table"].shape[1] * W.BLOCK
+        S, cs = choose_splits(b, max_len, hkv, hq, pd)
+        po2 = torch.empty((b * S, hq, pd), dtype=torch.float32, device=dev)
+        pl2 = torch.empty((b * S, hq), dtype=torch.float32, device=dev)
+        ms_s = time_graph(torch, lambda: ops.decode_paged_splitkv(
+            d["q"], cache, d["indices"], d["indptr"], d["seq"], hkv, hd, pd, scale, signs, o,
+            po2, pl2, S, cs), steps, warmup)
+        nbytes = W.algorithmic_decode_bytes(lens, hkv, hd, hq)
+        gbs = nbytes / (ms_b * 1e-3) / 1e9
+        out.append({"head_dim": hd, "batch": b, "qo_heads": hq, "kv_heads": hkv,
+                    "tokens": int(lens.sum()), "alg_bytes": nbytes,
+                    "balanced_us": round(ms_b * 1e3, 2), "GB/s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), "unit_tokens": int(split[b + 1]),
+                    "static_us": round(ms_s * 1e3, 2),
+                    "static_GB/s": round(nbytes / (ms_s * 1e-3) / 1e9, 1),
+                    "static_splits": [S, cs]})
+        log(f"ragged hd={hd}: balanced {ms_b * 1e3:.1f} us ({gbs:.0f} GB/s), static "
+            f"max_len splits {ms_s * 1e3:.1f} us")
+        del cache, d, po, pl, po2, pl2
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_e2e(torch, compare_steps=16):
+    """random-init Qwen3-8B architecture (fp16), 8 random prompts
+    of 32768 tokens, 256 output tokens each, every attention through
+    TurboQuantFusedImpl (turboquant_amd/e2e.py)."""
+    from turboquant_amd import e2e
+    res = e2e.run(e2e.ModelShape.qwen3_8b(), batch=8, prompt_len=32768, new_tokens=256,
+                  seed=0, compare_steps=compare_steps, log=log)
+    res.pop("first_tokens", None)
+    res = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}
+    res["config"] = ("configs[4]: random-init Qwen3-8B architecture fp16 (36 layers, hidden "
+                     "4096, 32q/8kv/128, MLP 12288, vocab 151936), 8 prompts x 32768 random "
+                     "tokens, 256 output tokens, concurrency 8, prefill one prompt at a time, "
+                     "decode steps replayed from one HIP graph")
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_write(torch, steps, warmup):
@@ -198,13 +304,19 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=2000,
-                    help="untimed steps first; the decode step settles only after a few"
-                         " hundred launches (74 us at 20 warmup steps, 65 us at 2000)")
+    ap.add_argument("--warmup", type=int, default=200,
+                    help="untimed steps before each timed leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--splits", type=int, default=0, help="override num_splits")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the configs[4] end-to-end leg")
+    ap.add_argument("--no-ragged", action="store_true", help="skip the configs[3] legs")
+    ap.add_argument("--static", action="store_true",
+                    help="headline through the reference's static-split op instead of the "
+                         "balanced op the backend uses")
+    ap.add_argument("--splits", type=int, default=0, help="override num_splits (--static)")
     ap.add_argument("--copy-ref", action="store_true",
                     help="only run a plain 256 MiB device copy x5 (HBM counter scale reference)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the headline decode steps (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's path runs on a single MI355X; "
@@ -227,6 +339,9 @@ def main():
 
     from turboquant_amd import _lib, ops
     _lib.load()
+    quick = args.decode_only
+    ragged = None if (quick or args.no_ragged) else bench_ragged(torch, args.steps, args.warmup)
+    e2e_res = None if (quick or args.no_e2e) else bench_e2e(torch)
     log("building cfg-3 cache on the GPU (write kernel)")
     w = make_decode_workload(torch)
     if args.splits:
@@ -237,15 +352,21 @@ def main():
     o = torch.empty((b, hq, pd), dtype=torch.float16, device=dev)
     po = torch.empty((b * S, hq, pd), dtype=torch.float32, device=dev)
     pl = torch.empty((b * S, hq), dtype=torch.float32, device=dev)
+    rows = ops.balanced_rows(b, hq, w["hkv"], pd)
+    pob = torch.empty((rows, hq, pd), dtype=torch.float32, device=dev)
+    plb = torch.empty((rows, hq), dtype=torch.float32, device=dev)
+    split = torch.zeros(b + 2, dtype=torch.int32, device=dev)
     scale = 1.0 / math.sqrt(w["hd"])
     lib = _lib.load()
     cache = w["cache"]
-    kbase = cache.data_ptr()
-    vbase = kbase + cache[0].numel()
 
-    def step():
+    def step_static():
         ops.decode_paged_splitkv(w["q"], cache, w["indices"], w["indptr"], w["seq"], w["hkv"],
                                  w["hd"], pd, scale, w["signs"], o, po, pl, S, w["cs"])
+
+    def step_balanced():
+        ops.decode_paged_balanced(w["q"], cache, w["indices"], w["indptr"], w["seq"], w["hkv"],
+                                  w["hd"], pd, scale, w["signs"], o, pob, plb, split)
 
     def combine_only():
         rc = lib.tq_combine_splits(po.data_ptr(), pl.data_ptr(), b, S, hq, pd,
@@ -253,34 +374,45 @@ def main():
                                    torch.cuda.current_stream().cuda_stream)
         _lib.check(rc, "tq_combine_splits")
 
-    log(f"timing decode: splits={S} chunk={w['cs']} steps={args.steps} warmup={args.warmup}")
+    step = step_static if args.static else step_balanced
+    op_name = ("turboquant_v5::decode_v5_from_cache_paged_splitkv_ws (static splits)"
+               if args.static else "turboquant_v5::decode_paged_balanced_ws (balanced plan)")
+    wr = dq = cpu = None
+    if not quick:
+        wr = bench_write(torch, args.steps, args.warmup)
+        log(f"write kernel {wr['us']} us -> {wr['GB/s']} GB/s")
+        dq = bench_dequant(torch, w, args.steps, args.warmup)
+        log(f"dequant kernel {dq['us']} us -> {dq['GB/s']} GB/s")
+    log(f"timing decode ({op_name}): steps={args.steps} warmup={args.warmup}")
     ms_eager = time_launches(torch, step, args.steps, args.warmup)
     ms = time_graph(torch, step, args.steps, args.warmup)
+    ms_other = time_graph(torch, step_balanced if args.static else step_static, args.steps,
+                          args.warmup)
     nbytes = alg_bytes(w)
     value = nbytes / (ms * 1e-3) / 1e9
     log(f"decode step {ms * 1e3:.1f} us (graph replay; {ms_eager * 1e3:.1f} us launched one "
-        f"call at a time from Python) -> {value:.0f} GB/s")
+        f"call at a time from Python) -> {value:.0f} GB/s; the other op "
+        f"{ms_other * 1e3:.1f} us")
     # the partials kernel's average duration inside the step: the step minus
-    # the combine kernel alone (both graph-timed with HIP events on the replay
-    # stream).  HIP events around each launch would add 3-5 us of their own
-    # to every launch; the difference agrees with rocprofv3's average kernel
-    # duration to within 0.5 us.
+    # the combine kernel alone over the same 512 partial rows (both
+    # graph-timed with HIP events on the replay stream).  HIP events around
+    # each launch would add 3-5 us of their own to every launch.
+    step_static()
+    torch.cuda.synchronize()
     ms_c = time_graph(torch, combine_only, args.steps, args.warmup)
     ms_k = ms - ms_c
     achieved = nbytes / (ms_k * 1e-3) / 1e9
     log(f"partials kernel {ms_k * 1e3:.1f} us (step - combine {ms_c * 1e3:.1f} us) -> "
         f"{achieved:.0f} GB/s")
+    plan = split.cpu().tolist()
     layout_bytes = b * w["seq_len"] * w["hkv"] * 2 * w["ebs"]
-    wr = bench_write(torch, args.steps, args.warmup)
-    log(f"write kernel {wr['us']} us -> {wr['GB/s']} GB/s")
-    dq = bench_dequant(torch, w, args.steps, args.warmup)
-    log(f"dequant kernel {dq['us']} us -> {dq['GB/s']} GB/s")
-    cpu = None
-    if not args.no_cpu:
-        log("CPU baseline (oracle) ...")
+    if not (quick or args.no_cpu):
+        log("CPU baseline (torch-CPU port) ...")
         cpu = cpu_baseline(torch, w)
-        log(f"CPU baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+        log(f"CPU baseline {cpu['value']} GB/s decode, {cpu['write']['value']} GB/s write on "
+            f"{cpu['cores']} threads ({cpu['cpu']})")
 
+    kname = "decode_partials_kernel<128, 8, 2, true>"
     line = {
         "metric": "decode-attn GB/s & % HBM peak, Qwen3-8B shape B=8 L=32k",
         "value": round(value, 1),
@@ -291,24 +423,28 @@ def main():
         "ms_per_step": round(ms, 5),
         "ms_per_step_eager": round(ms_eager, 5),
         "higher_is_better": True,
-        "scaling": "weak",
+        "scaling": None,
         "vs_baseline": None,
         "dtype": "u4 codes -> f16 MFMA, f32 accumulate",
         "data": "synthetic (seeded torch RNG, N(0,1) q/K/V, random page permutation)",
         "config": {"workload": "decode attention, configs[2]: Qwen3-8B geometry 32q/8kv/hd128, "
                                "B=8, 32768 cached tokens/seq, 16-token pages, split-KV + LSE merge",
-                   "batch": b, "seq_len": w["seq_len"], "num_qo_heads": hq,
+                   "op": op_name, "batch": b, "seq_len": w["seq_len"], "num_qo_heads": hq,
                    "num_kv_heads": w["hkv"], "head_dim": w["hd"], "page_size": 16,
-                   "num_splits": S, "kv_chunk_size": w["cs"], "parallelism": "single GPU"},
+                   "split_rows": plan[b], "unit_tokens": plan[b + 1],
+                   "parallelism": "single GPU"},
+        "ms_per_step_other_op": round(ms_other, 5),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "layout_GB/s": round(layout_bytes / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": PROFILED_TRAFFIC.get((S, w["cs"])),
-                     "kernel": "decode_partials_kernel<128, 8, 2, true>",
-                     "kernel_us": round(ms_k * 1e3, 2), "combine_us": round(ms_c * 1e3, 2),
-                     "alg_bytes": nbytes},
+                     "traffic_source": TRAFFIC_SOURCE,
+                     "kernel": kname, "kernel_us": round(ms_k * 1e3, 2),
+                     "combine_us": round(ms_c * 1e3, 2), "alg_bytes": nbytes},
         "cpu_baseline": cpu,
+        "configs3_ragged": ragged,
+        "e2e": e2e_res,
         "write_kernel": wr,
         "dequant_kernel": dq,
     }

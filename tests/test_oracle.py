@@ -304,3 +304,43 @@ def test_golden_cfg1():
                         c["seq_lens"], 8, pd, meta["sm_scale"], s)
     want = np.load(os.path.join(GOLDEN, "cfg1_decode.npy"))
     assert np.max(np.abs(out - want)) <= 1e-7
+
+
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_torch_cpu_port_write_matches_oracle(hd):
+    """The torch-CPU port (the bench's CPU baseline) writes the oracle's bytes,
+    up to codes within a few ulp of a boundary (its sum of squares is torch's
+    reduction, not the reference's lane tree)."""
+    import torch
+
+    from oracle import torch_ref
+    rng = np.random.default_rng(hd)
+    c = W.decode_case(17 + hd, 2, [300, 77], 8, 4, hd)
+    shape, pd = W.cache_bytes(c["num_blocks"], 4, hd)
+    s = _signs(pd)
+    want = np.zeros(shape, np.uint8)
+    oracle.write_kv_cache(want, c["k"], c["v"], s, c["slots"], hd, pd)
+    got = torch.zeros(shape, dtype=torch.uint8)
+    torch_ref.write_kv_cache(got, torch.from_numpy(c["k"]), torch.from_numpy(c["v"]),
+                             torch.from_numpy(s), torch.from_numpy(c["slots"]), pd)
+    got = got.numpy()
+    n = pd // 2
+    assert np.array_equal(got[..., n:], want[..., n:])  # norms and pad bytes
+    diff = got[..., :n] != want[..., :n]
+    assert diff.mean() < 1e-3, diff.mean()
+    del rng
+
+
+@pytest.mark.parametrize("hd,hq,hkv", [(128, 8, 2), (64, 4, 4), (256, 4, 1)])
+def test_torch_cpu_port_decode_matches_oracle(hd, hq, hkv):
+    import torch
+
+    from oracle import torch_ref
+    c, cache, ind, ip, q, pd, s = _small_case(29 + hd, [37, 1, 130, 0], hq, hkv, hd)
+    scale = 1.0 / math.sqrt(hd)
+    want = oracle.decode(q, cache, ind, ip, c["seq_lens"], hkv, pd, scale, s)
+    bt = torch.from_numpy(ind.reshape(len(c["seq_lens"]), -1))
+    got = torch_ref.decode(torch.from_numpy(q), torch.from_numpy(cache), bt,
+                           torch.from_numpy(c["seq_lens"]), hkv, pd, scale,
+                           torch.from_numpy(s)).numpy()
+    assert np.max(np.abs(got - want)) < 2e-5

@@ -195,7 +195,7 @@ __device__ __forceinline__ float hi_half(uint32_t v) {
 
 // ---- balanced split plan ------------------------------------------------
 constexpr int kPlanAlign = 2 * kTile;   // unit sizes are whole steps
-constexpr int kPlanMaxBatch = 1024;     // sequence lengths held in registers
+constexpr int kPlanMaxBatch = 1024;     // sequences a balanced plan takes
 
 __device__ __forceinline__ int xor_lane_i(int v, int m) {
   return __float_as_int(xor_lane(__int_as_float(v), m));
@@ -238,30 +238,28 @@ __device__ __forceinline__ int ceil_div_est(int a, int d, float rd) {
 
 // The unit of a balanced plan a workgroup serves: sequence b (-1: none, the
 // grid has more units than the plan uses), unit j of that sequence, its
-// length L, the sequence's first unit Pb and the unit size U in tokens.
+// length L, page-table start ip, the sequence's first unit Pb and the unit
+// size U in tokens.
 struct PlanSlot {
-  int b, j, L, Pb, U;
+  int b, j, L, Pb, U, ip;
 };
 
-// Every lane of a wave calls this; the result is wave-uniform.  writer:
-// this wave also stores the row table (rows = rowmul * units) and U.
-__device__ PlanSlot plan_slot(const int32_t* __restrict__ seq_lens, int B, int units, int u,
-                              int rowmul, int32_t* split_out, bool writer) {
-  constexpr int PR = kPlanMaxBatch / 64;
+// The plan from the sequence lengths, which `lens(i, lane)` returns for
+// sequence 64 i + lane (0 past the batch) and `starts` likewise for the
+// page-table starts; nreg = ceil(B / 64).  Every lane of a wave runs it and
+// every field of the result is wave-uniform.  writer: this wave also stores
+// the row table (rows = rowmul * units) and U.
+template <typename LensFn, typename StartsFn>
+__device__ __forceinline__ PlanSlot plan_slot(LensFn lens, StartsFn starts, int B, int nreg,
+                                              int units, int u, int rowmul, int32_t* split_out,
+                                              bool writer) {
   const int lane = threadIdx.x & 63;
-  const int nreg = (B + 63) >> 6;
-  int len[PR];
-#pragma unroll
-  for (int i = 0; i < PR; i++) {
-    const int bb = 64 * i + lane;
-    len[i] = (i < nreg && bb < B) ? max(seq_lens[bb], 0) : 0;
-  }
   int tsum = 0, mx = 0, nz = 0;
-#pragma unroll
-  for (int i = 0; i < PR; i++) {
-    tsum += len[i];
-    mx = max(mx, len[i]);
-    nz += len[i] > 0 ? 1 : 0;
+  for (int i = 0; i < nreg; i++) {
+    const int l = lens(i);
+    tsum += l;
+    mx = max(mx, l);
+    nz += l > 0 ? 1 : 0;
   }
   tsum = __builtin_amdgcn_readfirstlane(wave_sum_i(tsum));
   mx = __builtin_amdgcn_readfirstlane(wave_max_i(mx));
@@ -271,9 +269,7 @@ __device__ PlanSlot plan_slot(const int32_t* __restrict__ seq_lens, int B, int u
     const int d = k * A;
     const float rd = 1.0f / (float)d;
     int c = 0;
-#pragma unroll
-    for (int i = 0; i < PR; i++)
-      if (i < nreg) c += ceil_div_est(len[i], d, rd);
+    for (int i = 0; i < nreg; i++) c += ceil_div_est(lens(i), d, rd);
     return __builtin_amdgcn_readfirstlane(wave_sum_i(c));
   };
   // smallest feasible k in (lo, hi]: every k below tsum / (units * A) needs
@@ -290,37 +286,44 @@ __device__ PlanSlot plan_slot(const int32_t* __restrict__ seq_lens, int B, int u
   }
   const int U = hi * A;
   const float rdU = 1.0f / (float)U;
-  PlanSlot r = {-1, 0, 0, 0, U};
+  PlanSlot r = {-1, 0, 0, 0, U, 0};
   int carry = 0;
+  for (int i = 0; i < nreg; i++) {
+    const int l = lens(i);
+    const int c = ceil_div_est(l, U, rdU);
+    int incl = c;
 #pragma unroll
-  for (int i = 0; i < PR; i++) {
-    if (i < nreg) {
-      const int c = ceil_div_est(len[i], U, rdU);
-      int incl = c;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(incl, off);
-        if (lane >= off) incl += y;
-      }
-      incl += carry;
-      const int excl = incl - c;
-      const int bb = 64 * i + lane;
-      if (writer && bb < B) split_out[bb] = excl * rowmul;
-      const uint64_t hit = __ballot(c > 0 && excl <= u && u < incl);
-      if (hit) {
-        const int l0 = __builtin_ctzll(hit);
-        r.b = 64 * i + l0;
-        r.Pb = __builtin_amdgcn_readlane(excl, l0);
-        r.j = u - r.Pb;
-        r.L = __builtin_amdgcn_readlane(len[i], l0);
-      }
-      carry = __builtin_amdgcn_readlane(incl, 63);
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off);
+      if (lane >= off) incl += y;
     }
+    incl += carry;
+    const int excl = incl - c;
+    const int bb = 64 * i + lane;
+    if (writer && bb < B) split_out[bb] = excl * rowmul;
+    const uint64_t hit = __ballot(c > 0 && excl <= u && u < incl);
+    if (hit) {
+      const int l0 = __builtin_ctzll(hit);
+      r.b = 64 * i + l0;
+      r.Pb = __builtin_amdgcn_readlane(excl, l0);
+      r.j = u - r.Pb;
+      r.L = __builtin_amdgcn_readlane(l, l0);
+      r.ip = __builtin_amdgcn_readlane(starts(i), l0);
+    }
+    carry = __builtin_amdgcn_readlane(incl, 63);
   }
   if (writer && lane == 0) {
     split_out[B] = carry * rowmul;
     split_out[B + 1] = U;
   }
+  // every field is wave-uniform; saying so keeps the addresses built from
+  // them in scalar registers (buffer descriptors need them there)
+  r.b = __builtin_amdgcn_readfirstlane(r.b);
+  r.j = __builtin_amdgcn_readfirstlane(r.j);
+  r.L = __builtin_amdgcn_readfirstlane(r.L);
+  r.Pb = __builtin_amdgcn_readfirstlane(r.Pb);
+  r.U = __builtin_amdgcn_readfirstlane(r.U);
+  r.ip = __builtin_amdgcn_readfirstlane(r.ip);
   return r;
 }
 
@@ -723,7 +726,7 @@ __device__ __forceinline__ half4_t shl8(half4_t v) {
 // registers, barrier, then the copies of the tiles kRingSlots ahead are
 // issued into the two slots just read, and the math runs while they are in
 // flight.  Slot bases are runtime values (advanced by two slots per step).
-template <int PD, int G, int PACK, bool QC>
+template <int PD, int G, int PACK, bool QC, bool PLAN>
 __global__ __launch_bounds__(64 * G)
 __attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : (PACK == 1 ? 3 : 4))))
 void decode_partials_kernel(DecodeParams p) {
@@ -777,13 +780,36 @@ void decode_partials_kernel(DecodeParams p) {
   // partial row
   int b, L, ip, c0, c1;
   int64_t row;
-  if (p.units > 0) {
-    const PlanSlot ps = plan_slot(p.seq_lens, p.B, p.units, bid, p.pair_pct > 0 ? 2 : 1,
-                                  p.split_out, blockIdx.x == 0 && w == 0);
+  if constexpr (PLAN) {
+    const int rowmul = p.pair_pct > 0 ? 2 : 1;
+    const bool writer = blockIdx.x == 0 && w == 0;
+    PlanSlot ps;
+    if (p.B <= 64) {
+      // one sequence per lane: lengths and page-table starts in registers,
+      // loaded in one round trip
+      const bool in = lane < p.B;
+      const int len = in ? max(p.seq_lens[lane], 0) : 0;
+      const int ipl = in ? p.indptr[lane] : 0;
+      ps = plan_slot([&](int) { return len; }, [&](int) { return ipl; }, p.B, 1, p.units, bid,
+                     rowmul, p.split_out, writer);
+    } else {
+      // staged in LDS where the dequant table goes (built later): lengths,
+      // then page-table starts, kPlanMaxBatch of each
+      int* const st = reinterpret_cast<int*>(sm.klut);
+      for (int i = threadIdx.x; i < kPlanMaxBatch; i += 64 * G) {
+        st[i] = i < p.B ? max(p.seq_lens[i], 0) : 0;
+        st[kPlanMaxBatch + i] = i < p.B ? p.indptr[i] : 0;
+      }
+      __syncthreads();
+      ps = plan_slot([&](int i) { return st[64 * i + lane]; },
+                     [&](int i) { return st[kPlanMaxBatch + 64 * i + lane]; }, p.B,
+                     (p.B + 63) >> 6, p.units, bid, rowmul, p.split_out, writer);
+      __syncthreads();  // the staging area is free again
+    }
     if (ps.b < 0) return;  // unit beyond the plan: no row (uniform over the workgroup)
     b = ps.b;
     L = ps.L;
-    ip = p.indptr[b];
+    ip = ps.ip;
     c0 = ps.j * ps.U;
     c1 = c0 + ps.U;
     if (p.pair_pct > 0) {
@@ -1480,15 +1506,16 @@ typedef void (*PartialsFn)(DecodeParams);
 // register set when ratio <= 8 (head size 256 keeps one tile per set: two
 // would exceed the register file); q hi/lo parts share one B operand when
 // the GQA ratio leaves 8 columns free.
-PartialsFn partials_kernel(int pd, int G, int ratio) {
+template <bool PLAN>
+PartialsFn partials_kernel_t(int pd, int G, int ratio) {
   const bool pack2 = ratio <= 8 && pd <= 128;
   const bool qc = ratio <= 8;
-#define TQ_PICK_G(PDV, PK, QCV)                                               \
-  switch (G) {                                                                \
-    case 8: return &decode_partials_kernel<PDV, (PDV == 256 ? 4 : 8), PK, QCV>; \
-    case 4: return &decode_partials_kernel<PDV, 4, PK, QCV>;                 \
-    case 2: return &decode_partials_kernel<PDV, 2, PK, QCV>;                 \
-    default: return &decode_partials_kernel<PDV, 1, PK, QCV>;                \
+#define TQ_PICK_G(PDV, PK, QCV)                                                        \
+  switch (G) {                                                                         \
+    case 8: return &decode_partials_kernel<PDV, (PDV == 256 ? 4 : 8), PK, QCV, PLAN>; \
+    case 4: return &decode_partials_kernel<PDV, 4, PK, QCV, PLAN>;                    \
+    case 2: return &decode_partials_kernel<PDV, 2, PK, QCV, PLAN>;                    \
+    default: return &decode_partials_kernel<PDV, 1, PK, QCV, PLAN>;                   \
   }
   switch (pd) {
     case 64:
@@ -1499,6 +1526,9 @@ PartialsFn partials_kernel(int pd, int G, int ratio) {
       if (qc) { TQ_PICK_G(256, 1, true) } else { TQ_PICK_G(256, 1, false) }
   }
 #undef TQ_PICK_G
+}
+PartialsFn partials_kernel(int pd, int G, int ratio, bool plan) {
+  return plan ? partials_kernel_t<true>(pd, G, ratio) : partials_kernel_t<false>(pd, G, ratio);
 }
 
 // Checks shared by the partials launchers and the parameter block they fill
@@ -1645,7 +1675,7 @@ extern "C" int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_s
   p.S = num_splits;
   p.cs = kv_chunk_size;
   const int64_t blocks = (int64_t)batch * num_splits * p.HG;
-  const PartialsFn fn = partials_kernel(padded_dim, p.G, p.ratio);
+  const PartialsFn fn = partials_kernel(padded_dim, p.G, p.ratio, false);
   const Occupancy occ = occupancy(reinterpret_cast<const void*>(fn), 64 * p.G);
   if (occ.per_cu == 2 && blocks == 2LL * occ.cus && num_splits % 2 == 0)
     p.pair_pct = kPairPct;
@@ -1737,7 +1767,7 @@ static int decode_balanced(const void* q, int64_t q_stride_b, int64_t q_stride_h
     set_error("decode: null pointer");
     return kEinval;
   }
-  const PartialsFn fn = partials_kernel(padded_dim, p.G, p.ratio);
+  const PartialsFn fn = partials_kernel(padded_dim, p.G, p.ratio, true);
   BalancedGrid g;
   rc = balanced_grid(fn, p, max_rows, g);
   if (rc) return rc;
@@ -1897,7 +1927,7 @@ extern "C" int tq_decode_balanced_rows(int32_t batch, int32_t num_qo_heads,
     set_error("decode_balanced_rows: unsupported geometry");
     return kEinval;
   }
-  const PartialsFn fn = partials_kernel(padded_dim, G, ratio);
+  const PartialsFn fn = partials_kernel(padded_dim, G, ratio, true);
   const Occupancy occ = occupancy(reinterpret_cast<const void*>(fn), 64 * G);
   if (occ.cus <= 0 || occ.per_cu <= 0) {
     set_error("decode_balanced_rows: occupancy query failed");
