@@ -102,20 +102,24 @@ def build_weights(shape: ModelShape, seed: int, device) -> dict:
 
 
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    return F.rms_norm(x.float(), (x.shape[-1],), w.float(), eps).to(x.dtype)
+    """RMSNorm over the last dim (fp32 accumulation inside the fused kernel)."""
+    return F.rms_norm(x, (x.shape[-1],), w, eps)
 
 
-def rope(x: torch.Tensor, pos: torch.Tensor, theta: float) -> torch.Tensor:
-    """Rotate-half RoPE of x [T, H, D] at positions pos [T] (fp32 angles)."""
-    d = x.shape[-1]
-    inv = theta ** (-torch.arange(0, d, 2, device=x.device, dtype=torch.float32) / d)
-    ang = pos.to(torch.float32)[:, None] * inv[None, :]
-    cos = torch.cat((ang.cos(), ang.cos()), -1)[:, None, :]
-    sin = torch.cat((ang.sin(), ang.sin()), -1)[:, None, :]
-    xf = x.float()
-    x1, x2 = xf[..., :d // 2], xf[..., d // 2:]
-    rot = torch.cat((-x2, x1), -1)
-    return (xf * cos + rot * sin).to(x.dtype)
+def rope_tables(n: int, d: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp16 cos and signed-sin tables [n, d] of rotate-half RoPE (angles in
+    fp32): x' = x * cos + roll(x, d/2) * sin_signed, sin_signed = (-sin, sin)."""
+    inv = theta ** (-torch.arange(0, d, 2, device=device, dtype=torch.float32) / d)
+    ang = torch.arange(n, device=device, dtype=torch.float32)[:, None] * inv[None, :]
+    cos = torch.cat((ang.cos(), ang.cos()), -1).half()
+    sin = torch.cat((-ang.sin(), ang.sin()), -1).half()
+    return cos, sin
+
+
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotate-half RoPE of x [T, H, D] with the table rows of its positions."""
+    return torch.addcmul(x * cos[:, None, :], torch.roll(x, x.shape[-1] // 2, dims=-1),
+                         sin[:, None, :])
 
 
 def greedy(logits: torch.Tensor) -> torch.Tensor:
@@ -158,6 +162,7 @@ class Runner:
         self.impls = [TurboQuantFusedImpl(s.heads, s.head_dim, 1.0 / math.sqrt(s.head_dim),
                                           s.kv_heads, None, None, "fp8")
                       for _ in range(s.layers)]
+        self.cos, self.sin = rope_tables(self.max_tokens, s.head_dim, s.rope_theta, dev)
         self.kv16 = None
         if self.keep_fp16_kv:
             self.kv16 = [torch.zeros((2, self.batch, s.kv_heads, self.max_tokens, s.head_dim),
@@ -175,7 +180,8 @@ class Runner:
         self.probe = None  # list collecting (layer, q, out) of decode attention, eager only
 
     # ------------------------------------------------------------ layers
-    def _attn_qkv(self, lw, x, pos):
+    def _attn_qkv(self, lw, x, cs):
+        """q, k, v of the tokens x; cs = (cos, sin) rows of their positions."""
         s = self.shape
         t = x.shape[0]
         h = rms_norm(x, lw["ln1"], s.eps)
@@ -184,9 +190,12 @@ class Runner:
                              s.kv_heads * s.head_dim], dim=-1)
         q = rms_norm(q.reshape(t, s.heads, s.head_dim), lw["q_norm"], s.eps)
         k = rms_norm(k.reshape(t, s.kv_heads, s.head_dim), lw["k_norm"], s.eps)
-        q = rope(q, pos, s.rope_theta)
-        k = rope(k, pos, s.rope_theta)
+        q = rope(q, *cs)
+        k = rope(k, *cs)
         return q, k, v.reshape(t, s.kv_heads, s.head_dim)
+
+    def _rope_rows(self, pos):
+        return self.cos.index_select(0, pos), self.sin.index_select(0, pos)
 
     def _mlp(self, lw, x):
         h = rms_norm(x, lw["ln2"], self.shape.eps)
@@ -212,8 +221,9 @@ class Runner:
         meta = Meta(L, L, pages[None, :], torch.tensor([L], dtype=torch.int32, device=dev),
                     torch.tensor([0, L], dtype=torch.int32, device=dev), slots)
         x = F.embedding(tokens, self.weights["embed"])
+        cs = self._rope_rows(pos)
         for li, lw in enumerate(self.weights["layers"]):
-            q, k, v = self._attn_qkv(lw, x, pos)
+            q, k, v = self._attn_qkv(lw, x, cs)
             impl = self.impls[li]
             impl.do_kv_cache_update(None, k, v, self.caches[li], slots)
             if self.kv16 is not None:
@@ -241,8 +251,9 @@ class Runner:
         self.seq_lens.copy_((pos + 1).to(torch.int32))
         meta = Meta(1, self.batch, bt, self.seq_lens, self.qsl, self.slots)
         x = F.embedding(self.tok, self.weights["embed"])
+        cs = self._rope_rows(pos)
         for li, lw in enumerate(self.weights["layers"]):
-            q, k, v = self._attn_qkv(lw, x, pos)
+            q, k, v = self._attn_qkv(lw, x, cs)
             impl = self.impls[li]
             impl.do_kv_cache_update(None, k, v, self.caches[li], self.slots)
             q2 = q.reshape(self.batch, -1)
@@ -328,8 +339,9 @@ class Runner:
         for step in range(steps):
             p = p0 + step
             x = F.embedding(tok, self.weights["embed"])
+            cs = self._rope_rows(pos)
             for li, lw in enumerate(self.weights["layers"]):
-                q, k, v = self._attn_qkv(lw, x, pos)
+                q, k, v = self._attn_qkv(lw, x, cs)
                 kv = self.kv16[li]
                 kv[0, :, :, p] = k
                 kv[1, :, :, p] = v

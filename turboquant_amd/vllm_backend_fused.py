@@ -381,12 +381,9 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
                                        output, output_scale, **kwargs)
             self._ensure(q.device)
             block_size = kv_cache.shape[2]
-            # strided page table: static shapes, capturable
-            num_pages = (seq_lens + block_size - 1) // block_size
+            # strided page table (indptr = b * max_pages): static shapes,
+            # capturable; the indptr tensor is made once per workspace
             max_pages = block_table.shape[1]
-            kv_indptr = torch.arange(seq_lens.shape[0] + 1, dtype=torch.int32,
-                                     device=q.device) * max_pages
-            kv_last_page_len = seq_lens - (num_pages - 1) * block_size
             kv_indices = block_table.reshape(-1)
             if kv_indices.dtype != torch.int32:
                 kv_indices = kv_indices.to(torch.int32)
@@ -397,24 +394,36 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
             batch_size = q_fp16.shape[0]
             ws, max_len, num_splits = self._get_v5_ws(batch_size, max_pages, block_size,
                                                       q.device)
+            kv_indptr = ws.get("indptr")
+            if kv_indptr is None:
+                kv_indptr = ws["indptr"] = torch.arange(
+                    batch_size + 1, dtype=torch.int32, device=q.device) * max_pages
             sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+            out3 = output[:num_actual].view(num_actual, self.num_heads, self.head_size)
+            # the kernel writes the caller's output directly when it has the
+            # op's layout (fp16, contiguous, head_size == padded_dim)
+            direct = (self.head_size == self._pd and out3.dtype == torch.float16
+                      and out3.is_contiguous())
+            o_ws = out3 if direct else ws["o"]
             if self._decode_op_name == KERNEL_NAME:
                 result = self._decode_op(
                     q_fp16, kv_cache, kv_indices, kv_indptr, sl, self.num_kv_heads,
-                    self.head_size, self._pd, self.scale, self._signs, ws["o"],
+                    self.head_size, self._pd, self.scale, self._signs, o_ws,
                     ws["partition_o"], ws["partition_lse"], ws["split_indptr"])
             else:
+                num_pages = (seq_lens + block_size - 1) // block_size
+                kv_last_page_len = seq_lens - (num_pages - 1) * block_size
                 result = self._decode_op(
                     q_fp16, kv_cache, kv_indices, kv_indptr, kv_last_page_len, sl,
                     self.num_kv_heads, block_size, self.head_size, self._pd, self.scale,
-                    self._signs, self._qbytes, self._nbytes, ws["o"], max_len,
+                    self._signs, self._qbytes, self._nbytes, o_ws, max_len,
                     ws["partition_o"], ws["partition_lse"], ws["request_indices"],
                     ws["kv_tile_indices"], ws["split_indptr"], ws["kv_chunk_size"], num_splits)
-            out3 = output[:num_actual].view(num_actual, self.num_heads, self.head_size)
-            if self.head_size < self._pd:
-                out3.copy_(result[:num_actual, :, :self.head_size])
-            else:
-                out3.copy_(result[:num_actual])
+            if not direct:
+                if self.head_size < self._pd:
+                    out3.copy_(result[:num_actual, :, :self.head_size])
+                else:
+                    out3.copy_(result[:num_actual])
         except Exception as e:
             print(f"[TQ] Decode kernel failed: {e}", file=sys.stderr, flush=True)
             traceback.print_exc(file=sys.stderr)
