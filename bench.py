@@ -297,6 +297,39 @@ def bench_write(torch, steps, warmup):
                                            "permuted slots (configs[1])"}
 
 
+def bench_prefill_chunk(torch, w, steps, warmup, chunk=2048):
+    """One chunked-prefill attention call through TurboQuantFusedImpl.forward:
+    a chunk of `chunk` new tokens at the end of a configs[2] sequence (32768
+    tokens, so 30720 cached before it; the chunk's own K/V are in the cache
+    too, written first as vLLM does), Qwen3-8B geometry.  The cached context
+    is read back by tq_dequant_paged and the chunk attends it plus its fresh
+    K/V in torch's flash kernel (lower-right causal, grouped kv heads).  The
+    metadata carries host copies of the boundaries (as vLLM's does), so no
+    device-to-host read happens; timed call by call with HIP events."""
+    from types import SimpleNamespace
+
+    from turboquant_amd.vllm_backend_fused import TurboQuantFusedImpl
+    dev = w["q"].device
+    L, hq, hkv, hd = w["seq_len"], w["hq"], w["hkv"], w["hd"]
+    impl = TurboQuantFusedImpl(hq, hd, 1.0 / math.sqrt(hd), hkv, None, None, "fp8")
+    g = torch.Generator(device=dev).manual_seed(11)
+    q = torch.randn((chunk, hq * hd), generator=g, device=dev).half()
+    k = torch.randn((chunk, hkv * hd), generator=g, device=dev).half()
+    v = torch.randn((chunk, hkv * hd), generator=g, device=dev).half()
+    out = torch.empty_like(q)
+    meta = SimpleNamespace(
+        max_query_len=chunk, num_actual_tokens=chunk, block_table=w["bt"][:1],
+        seq_lens=torch.tensor([L], dtype=torch.int32, device=dev),
+        query_start_loc=torch.tensor([0, chunk], dtype=torch.int32, device=dev),
+        slot_mapping=None, query_start_loc_cpu=torch.tensor([0, chunk], dtype=torch.int32),
+        seq_lens_cpu=torch.tensor([L], dtype=torch.int32))
+    ms = time_launches(torch, lambda: impl.forward(None, q, k, v, w["cache"], meta, output=out),
+                       max(1, min(steps, 50)), max(1, min(warmup, 5)))
+    return {"us": round(ms * 1e3, 1), "chunk_tokens": chunk, "cached_tokens": L - chunk,
+            "config": "Qwen3-8B geometry 32q/8kv/128, one request, context read back from "
+                      "the quantized cache + torch flash attention (lower-right causal, GQA)"}
+
+
 def bench_dequant(torch, w, steps, warmup):
     """tq_dequant_paged (the read-back of cached context for a prefill chunk)
     over one configs[2] sequence: 32768 tokens x 8 heads of K and V back to
@@ -393,12 +426,15 @@ def main():
     step = step_static if args.static else step_balanced
     op_name = ("turboquant_v5::decode_v5_from_cache_paged_splitkv_ws (static splits)"
                if args.static else "turboquant_v5::decode_paged_balanced_ws (balanced plan)")
-    wr = dq = cpu = None
+    wr = dq = pf = cpu = None
     if not quick:
         wr = bench_write(torch, args.steps, args.warmup)
         log(f"write kernel {wr['us']} us -> {wr['GB/s']} GB/s")
         dq = bench_dequant(torch, w, args.steps, args.warmup)
         log(f"dequant kernel {dq['us']} us -> {dq['GB/s']} GB/s")
+        pf = bench_prefill_chunk(torch, w, args.steps, args.warmup)
+        log(f"prefill chunk {pf['chunk_tokens']} tokens over {pf['cached_tokens']} cached: "
+            f"{pf['us']} us")
     log(f"timing decode ({op_name}): steps={args.steps} warmup={args.warmup}")
     ms_eager = time_launches(torch, step, args.steps, args.warmup)
     ms = time_graph(torch, step, args.steps, args.warmup)
@@ -428,7 +464,8 @@ def main():
         log(f"CPU baseline {cpu['value']} GB/s decode, {cpu['write']['value']} GB/s write on "
             f"{cpu['cores']} threads ({cpu['cpu']})")
 
-    kname = "decode_partials_kernel<128, 8, 2, true>"
+    kname = ("decode_partials_kernel<128, 8, 2, true, false>" if args.static else
+             "decode_partials_kernel<128, 8, 2, true, true>")
     line = {
         "metric": "decode-attn GB/s & % HBM peak, Qwen3-8B shape B=8 L=32k",
         "value": round(value, 1),
@@ -463,6 +500,7 @@ def main():
         "e2e": e2e_res,
         "write_kernel": wr,
         "dequant_kernel": dq,
+        "prefill_chunk": pf,
     }
     print(json.dumps(line), flush=True)
 

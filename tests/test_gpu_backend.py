@@ -84,8 +84,9 @@ def test_backend_prefill_fresh_attention():
             assert torch.allclose(got, ref, atol=2e-2), (a, h)
 
 
-@pytest.mark.parametrize("hq,hkv,hd", [(32, 8, 128), (8, 2, 64)])
-def test_backend_mixed_batch_with_cached_context(hq, hkv, hd):
+@pytest.mark.parametrize("hq,hkv,hd,cpu_copies", [(32, 8, 128, False), (8, 2, 64, False),
+                                                   (32, 8, 128, True)])
+def test_backend_mixed_batch_with_cached_context(hq, hkv, hd, cpu_copies):
     """A max_query_len > 1 batch: a fresh prompt, two chunks of longer prompts
     whose earlier tokens are already cached, and a decode row.  Chunks attend
     the dequantized cached context plus their fresh K/V (causal); the decode
@@ -121,6 +122,9 @@ def test_backend_mixed_batch_with_cached_context(hq, hkv, hd):
     meta = Meta(max(qls), int(sum(qls)), torch.from_numpy(bt).to(dev),
                 torch.tensor(lens, dtype=torch.int32, device=dev),
                 torch.from_numpy(qsl).to(dev), None)
+    if cpu_copies:  # vLLM's host copies of the boundaries: no device read
+        meta.query_start_loc_cpu = torch.from_numpy(qsl)
+        meta.seq_lens_cpu = torch.tensor(lens, dtype=torch.int32)
     out = impl.forward(None, qn, kn, vn, cache, meta)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy().reshape(-1, hq, hd)

@@ -136,3 +136,31 @@ def test_from_cache_ws_rejects_wrong_workspace():
     d["ws"]["k_quant"] = d["ws"]["k_quant"][:, :, :-1]
     with pytest.raises(RuntimeError, match="k_quant_ws shape mismatch"):
         _ws_call(d)
+
+
+def test_from_cache_eager_csr_indptr_longer_later_sequence():
+    """A CSR page table (indices = each sequence's pages back to back) whose
+    later sequence has more pages than the first: the eager op sizes its
+    splits from seq_lens.max() (reference decode_v5_tc_binding.cu:350), so
+    the longer sequence is read in full."""
+    print("case: decode_v5_from_cache eager, CSR indptr", flush=True)
+    import oracle
+    lens = [100, 3000, 17]
+    c = W.decode_case(93, 3, lens, 32, 8, 128)
+    cache, pd = G.build_cache(c)
+    bt = c["block_table"]
+    npg = [-(-n // W.BLOCK) for n in lens]
+    ind = np.concatenate([bt[i, :npg[i]] for i in range(3)]).astype(np.int32)
+    ip = np.concatenate([[0], np.cumsum(npg)]).astype(np.int32)
+    qp = np.zeros((3, 32, pd), np.float16)
+    qp[:, :, :128] = c["q"]
+    dev = G.DEV
+    seq = torch.tensor(lens, dtype=torch.int32, device=dev)
+    o = ops.decode_v5_from_cache(torch.from_numpy(qp).to(dev), cache,
+                                 torch.from_numpy(ind).to(dev), torch.from_numpy(ip).to(dev),
+                                 seq, seq, 8, W.BLOCK, 128, pd, 1.0 / np.sqrt(128),
+                                 hadamard_signs(pd, dev), pd // 2, 2 * (pd // 64))
+    torch.cuda.synchronize()
+    ref = oracle.decode(qp, cache.cpu().numpy(), ind, ip, np.array(lens, np.int32), 8, pd,
+                        1.0 / np.sqrt(128), hadamard_signs(pd).numpy())
+    G.assert_close(o.float().cpu().numpy(), ref, "from_cache eager CSR")

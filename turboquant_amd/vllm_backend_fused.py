@@ -249,45 +249,93 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
                                     layer._k_scale, layer._v_scale)
 
     # -------------------------------------------------------------- forward
+    @staticmethod
+    def _host_boundaries(attn_metadata):
+        """query_start_loc and seq_lens as host lists: the metadata's own CPU
+        copies when it carries them (vLLM's query_start_loc_cpu /
+        seq_lens_cpu), else one device-to-host copy of both together."""
+        qsl = getattr(attn_metadata, "query_start_loc_cpu", None)
+        seq = getattr(attn_metadata, "seq_lens_cpu", None)
+        if qsl is not None and (seq is not None or attn_metadata.seq_lens is None):
+            return qsl.tolist(), (seq.tolist() if seq is not None else None)
+        dq = attn_metadata.query_start_loc
+        if attn_metadata.seq_lens is None:
+            return dq.cpu().tolist(), None
+        n = dq.numel()
+        both = torch.cat([dq.to(torch.int64), attn_metadata.seq_lens.to(torch.int64)]).cpu()
+        return both[:n].tolist(), both[n:].tolist()
+
+    def _attend(self, q, k, v, ctx):
+        """q [ql, Hq, D] over k, v [ctx + ql, Hkv, D] (fp16), causal with the
+        queries at the end of the keys (lower-right alignment): the fused
+        flash kernel with grouped heads, no expanded K/V, no dense mask."""
+        from torch.nn.attention.bias import causal_lower_right
+        qt = q.transpose(0, 1).unsqueeze(0)
+        kt = k.transpose(0, 1).unsqueeze(0)
+        vt = v.transpose(0, 1).unsqueeze(0)
+        ql, kl = q.shape[0], k.shape[0]
+        if ctx == 0:
+            o = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True, scale=self.scale,
+                                               enable_gqa=True)
+        else:
+            o = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=causal_lower_right(ql, kl),
+                                               scale=self.scale, enable_gqa=True)
+        return o.squeeze(0).transpose(0, 1)
+
     def _prefill_fresh(self, query, key, value, attn_metadata, output):
         """Causal attention of each prompt chunk over its own fresh K/V."""
-        n = attn_metadata.num_actual_tokens
-        qsl = attn_metadata.query_start_loc.tolist()
-        g = self.num_heads // self.num_kv_heads
+        qsl, _ = self._host_boundaries(attn_metadata)
         for i in range(len(qsl) - 1):
             a, b = qsl[i], qsl[i + 1]
             if b <= a:
                 continue
-            q = query[a:b].to(torch.float16).transpose(0, 1)
-            k = key[a:b].to(torch.float16).transpose(0, 1).repeat_interleave(g, dim=0)
-            v = value[a:b].to(torch.float16).transpose(0, 1).repeat_interleave(g, dim=0)
-            o = F.scaled_dot_product_attention(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
-                                               is_causal=True, scale=self.scale)
-            output[a:b] = o.squeeze(0).transpose(0, 1).to(output.dtype)
+            o = self._attend(query[a:b].to(torch.float16), key[a:b].to(torch.float16),
+                             value[a:b].to(torch.float16), 0)
+            output[a:b] = o.to(output.dtype)
         return output
+
+    def _decode_ws(self, n, pages, device):
+        """Balanced-decode workspace for n decode rows of a mixed batch."""
+        key = ("mixed", n, pages)
+        ws = self._v5_ws_cache.get(key)
+        if ws is None:
+            from .ops import balanced_rows
+            rows = balanced_rows(n, self.num_heads, self.num_kv_heads, self._pd, device)
+            ws = {
+                "o": torch.empty((n, self.num_heads, self._pd), dtype=torch.float16,
+                                 device=device),
+                "partition_o": torch.empty((rows, self.num_heads, self._pd),
+                                           dtype=torch.float32, device=device),
+                "partition_lse": torch.empty((rows, self.num_heads), dtype=torch.float32,
+                                             device=device),
+                "split_indptr": torch.zeros(n + 2, dtype=torch.int32, device=device),
+                "indptr": torch.arange(n + 1, dtype=torch.int32, device=device) * pages,
+            }
+            self._v5_ws_cache[key] = ws
+        return ws
 
     def _prefill_mixed(self, query, key, value, kv_cache, attn_metadata, output):
         """A batch with max_query_len > 1 whose cache already holds every token
         of the batch (do_kv_cache_update runs first).  Per request with q_len
         new tokens and seq_len tokens in all, ctx = seq_len - q_len:
 
-        * q_len == 1 and ctx > 0 (decode rows of a mixed batch): the decode
-          kernel over the cache, as in a pure decode batch;
+        * q_len == 1 and ctx > 0 (decode rows of a mixed batch): the balanced
+          decode kernels over the cache, as in a pure decode batch;
         * ctx == 0 (a fresh prompt): causal attention over the fresh K/V,
           the reference's prefill (vllm_backend_fused.py:335-371);
         * ctx > 0 (a chunk of a longer prompt): the ctx cached tokens read back
           from the quantized cache (tq_dequant_paged) followed by the chunk's
-          fresh K/V, causal within the chunk.  The reference attends the fresh
-          chunk only and so drops the cached context; its decode path already
-          attends over the dequantized cache, which this extends to chunks.
+          fresh K/V, causal with the chunk's queries at the end.  The
+          reference attends the fresh chunk only and so drops the cached
+          context; its decode path already attends over the dequantized
+          cache, which this extends to chunks.
+        Attention runs in torch's fused flash kernel with grouped kv heads.
         """
         from . import ops
         self._ensure_kernels_loaded()
         self._ensure(query.device)
-        qsl = attn_metadata.query_start_loc.tolist()
-        seq = attn_metadata.seq_lens.tolist()
+        qsl, seq = self._host_boundaries(attn_metadata)
         bt = attn_metadata.block_table
-        g = self.num_heads // self.num_kv_heads
         dec = []
         for i in range(len(qsl) - 1):
             a, b = qsl[i], qsl[i + 1]
@@ -300,11 +348,10 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
             if ql == 1 and ctx > 0:
                 dec.append(i)
                 continue
-            q = query[a:b].to(torch.float16).transpose(0, 1).unsqueeze(0)
+            q = query[a:b].to(torch.float16)
             if ctx == 0:
                 kk = key[a:b].to(torch.float16)
                 vv = value[a:b].to(torch.float16)
-                mask = None
             else:
                 kk = torch.empty((ctx + ql, self.num_kv_heads, self.head_size),
                                  dtype=torch.float16, device=query.device)
@@ -314,31 +361,23 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
                                   self._pd, self._signs, kk, vv)
                 kk[ctx:] = key[a:b]
                 vv[ctx:] = value[a:b]
-                r = torch.arange(ql, device=query.device)[:, None]
-                c = torch.arange(ctx + ql, device=query.device)[None, :]
-                mask = c <= r + ctx
-            kt = kk.transpose(0, 1).repeat_interleave(g, dim=0).unsqueeze(0)
-            vt = vv.transpose(0, 1).repeat_interleave(g, dim=0).unsqueeze(0)
-            if mask is None:
-                o = F.scaled_dot_product_attention(q, kt, vt, is_causal=True, scale=self.scale)
-            else:
-                o = F.scaled_dot_product_attention(q, kt, vt, attn_mask=mask, scale=self.scale)
-            output[a:b] = o.squeeze(0).transpose(0, 1).to(output.dtype)
+            output[a:b] = self._attend(q, kk, vv, ctx).to(output.dtype)
         if dec:
-            rows = torch.tensor([qsl[i] for i in dec], dtype=torch.long, device=query.device)
-            idx = torch.tensor(dec, dtype=torch.long, device=query.device)
+            dev = query.device
+            rows = torch.tensor([qsl[i] for i in dec], dtype=torch.long, device=dev)
+            idx = torch.tensor(dec, dtype=torch.long, device=dev)
             q = query.index_select(0, rows).to(torch.float16)
             if self.head_size < self._pd:
                 q = F.pad(q, (0, self._pd - self.head_size))
             q = q.contiguous()
             sub_bt = bt.index_select(0, idx).to(torch.int32).contiguous()
             sl = attn_metadata.seq_lens.index_select(0, idx).to(torch.int32).contiguous()
-            nbt = sub_bt.shape[1]
-            indptr = torch.arange(len(dec) + 1, dtype=torch.int32, device=query.device) * nbt
-            o = ops.decode_v5_from_cache(q, kv_cache, sub_bt.reshape(-1), indptr, sl, sl,
-                                         self.num_kv_heads, kv_cache.shape[2], self.head_size,
-                                         self._pd, self.scale, self._signs, self._qbytes,
-                                         self._nbytes)
+            ws = self._decode_ws(len(dec), sub_bt.shape[1], dev)
+            o = ops.decode_paged_balanced(q, kv_cache, sub_bt.reshape(-1), ws["indptr"], sl,
+                                          self.num_kv_heads, self.head_size, self._pd,
+                                          self.scale, self._signs, ws["o"],
+                                          ws["partition_o"], ws["partition_lse"],
+                                          ws["split_indptr"])
             output.index_copy_(0, rows, o[:, :, :self.head_size].to(output.dtype))
         return output
 
