@@ -364,6 +364,9 @@ def main():
     ap.add_argument("--splits", type=int, default=0, help="override num_splits (--static)")
     ap.add_argument("--copy-ref", action="store_true",
                     help="only run a plain 256 MiB device copy x5 (HBM counter scale reference)")
+    ap.add_argument("--stream-ref", action="store_true",
+                    help="also time the partials kernel with its math compiled out "
+                         "(tq_diag_decode_stream: the data movement alone)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the headline decode steps (for profiling)")
     args = ap.parse_args()
@@ -456,6 +459,25 @@ def main():
     achieved = nbytes / (ms_k * 1e-3) / 1e9
     log(f"partials kernel {ms_k * 1e3:.1f} us (step - combine {ms_c * 1e3:.1f} us) -> "
         f"{achieved:.0f} GB/s")
+    stream_ref = None
+    if args.stream_ref:
+        def stream_only():
+            rc = lib.tq_diag_decode_stream(
+                w["q"].data_ptr(), w["q"].stride(0), w["q"].stride(1), cache.data_ptr(),
+                cache.data_ptr() + cache[0].numel(), w["indices"].data_ptr(),
+                w["indptr"].data_ptr(), w["seq"].data_ptr(), b, hq, w["hkv"], pd, 16, w["ebs"],
+                w["nb"], scale, w["signs"].data_ptr(), S, w["cs"], po.data_ptr(), pl.data_ptr(),
+                torch.cuda.current_stream().cuda_stream)
+            _lib.check(rc, "tq_diag_decode_stream")
+        ms_s = time_graph(torch, stream_only, args.steps, args.warmup)
+        stream_ref = {"us": round(ms_s * 1e3, 2),
+                      "layout_GB/s": round(b * w["seq_len"] * w["hkv"] * 2 * w["ebs"] /
+                                           (ms_s * 1e-3) / 1e9, 1),
+                      "alg_frac": round(alg_bytes(w) / (ms_s * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                      "what": "decode_partials_kernel<128, 8, 2, true, false, false>: the "
+                              "static-split partials kernel with the attention math compiled "
+                              "out (page walk, LDS copy ring, waits, barriers, slot reads)"}
+        log(f"partials without math {ms_s * 1e3:.1f} us")
     plan = split.cpu().tolist()
     layout_bytes = b * w["seq_len"] * w["hkv"] * 2 * w["ebs"]
     if not (quick or args.no_cpu):
@@ -501,6 +523,7 @@ def main():
         "write_kernel": wr,
         "dequant_kernel": dq,
         "prefill_chunk": pf,
+        "stream_ref": stream_ref,
     }
     print(json.dumps(line), flush=True)
 

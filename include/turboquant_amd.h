@@ -74,7 +74,8 @@ int tq_quantize_write_kv_cache(void* k_slab, void* v_slab,
  * sequence b covers tokens [s*kv_chunk_size, min((s+1)*kv_chunk_size, seq_len)).
  * Pages outside [0, num_blocks) are treated as empty.
  * partition_o: fp32 [batch*num_splits, num_qo_heads, pd] and
- * partition_lse: fp32 [batch*num_splits, num_qo_heads] are workspace.
+ * partition_lse: fp32 [batch*num_splits, num_qo_heads] are workspace (the
+ * partial rows are kept as fp16 in the first half of partition_o's bytes).
  * o: fp16 [batch, num_qo_heads, pd] contiguous, the attention output in the
  * original (unrotated) domain.  signs == NULL disables the rotation.
  * num_qo_heads / num_kv_heads must be an integer <= 16.
@@ -151,9 +152,10 @@ int tq_decode_balanced_rows(int32_t batch, int32_t num_qo_heads, int32_t num_kv_
 
 /*
  * The first kernel of tq_decode_paged_splitkv alone (the reference's v5 split
- * kernel, v5_tc.cuh:106-795): writes partition_o (normalised, rotated domain)
- * and partition_lse (natural log; -inf for an empty split) of split s =
- * tokens [s * kv_chunk_size, min((s + 1) * kv_chunk_size, seq_len)).
+ * kernel, v5_tc.cuh:106-795): writes the partial rows (normalised, rotated
+ * domain, fp16 [batch*num_splits, num_qo_heads, pd] at the start of
+ * partition_o) and partition_lse (natural log; -inf for an empty split) of
+ * split s = tokens [s * kv_chunk_size, min((s + 1) * kv_chunk_size, seq_len)).
  */
 int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                        const uint8_t* k_slab, const uint8_t* v_slab,
@@ -166,7 +168,8 @@ int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                        float* partition_o, float* partition_lse, tq_stream_t stream);
 
 /*
- * The second kernel alone: LSE merge of the splits of each sequence, inverse
+ * The second kernel alone (reads the fp16 partial rows tq_decode_partials
+ * leaves in partition_o): LSE merge of the splits of each sequence, inverse
  * rotation (s * FWHT(o) / sqrt(pd)) and the fp16 store into o.  Replaces
  * SplitKVCombineKernel (combine.cuh:18-79) plus the per-split inverse FWHT of
  * v5_tc.cuh:712-765.  Splits with lse == -inf are skipped; a sequence with
@@ -196,6 +199,24 @@ int tq_dequant_paged(const uint8_t* k_slab, const uint8_t* v_slab,
                      int32_t ebs, int64_t num_blocks, const float* signs,
                      void* out_k, void* out_v, int64_t out_stride_tok,
                      tq_stream_t stream);
+
+/*
+ * Diagnostic, no counterpart in the reference: tq_decode_partials at head
+ * size 128 with 8 kv heads per workgroup (the configs[2] geometry) with the
+ * attention math compiled out -- the same page walk, LDS copy ring, waits,
+ * barriers and slot reads, zero partial rows.  Its duration is the cost of
+ * the data movement alone (the bandwidth ceiling of this kernel design).
+ * Other geometries return -22.
+ */
+int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                          const uint8_t* k_slab, const uint8_t* v_slab,
+                          const int32_t* indices, const int32_t* indptr,
+                          const int32_t* seq_lens, int32_t batch,
+                          int32_t num_qo_heads, int32_t num_kv_heads,
+                          int32_t padded_dim, int32_t block_size, int32_t ebs,
+                          int64_t num_blocks, float sm_scale, const float* signs,
+                          int32_t num_splits, int32_t kv_chunk_size,
+                          float* partition_o, float* partition_lse, tq_stream_t stream);
 
 /* Message for the last non-zero return of a tq_* call on this thread. */
 const char* tq_last_error(void);

@@ -726,7 +726,7 @@ __device__ __forceinline__ half4_t shl8(half4_t v) {
 // registers, barrier, then the copies of the tiles kRingSlots ahead are
 // issued into the two slots just read, and the math runs while they are in
 // flight.  Slot bases are runtime values (advanced by two slots per step).
-template <int PD, int G, int PACK, bool QC, bool PLAN>
+template <int PD, int G, int PACK, bool QC, bool PLAN, bool MATH = true>
 __global__ __launch_bounds__(64 * G)
 __attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : (PACK == 1 ? 3 : 4))))
 void decode_partials_kernel(DecodeParams p) {
@@ -1258,7 +1258,7 @@ void decode_partials_kernel(DecodeParams p) {
         issue(2 * k + kRingSlots, s0);
         if (2 * k + kRingSlots + 1 <= tile_end) issue(2 * k + kRingSlots + 1, s1);
       }
-      compute(k, d);
+      if constexpr (MATH) compute(k, d);
     };
     for (int k = step0, s0 = 0, s1 = 1; k <= step1; k++) {
       run(k, s0, s1);
@@ -1272,23 +1272,48 @@ void decode_partials_kernel(DecodeParams p) {
   if constexpr (PACK == 2) lt = lt + __int_as_float(__builtin_amdgcn_mov_dpp(
                                          __float_as_int(lt), 0x128, 0xf, 0xf, false));
   lt = xor32_sum(xor16_sum(lt));
+  // The wave's partial rows (its `ratio` q heads, consecutive rows of
+  // partition_o) are staged in LDS and written with whole-wave 1 KB stores:
+  // written straight from the MFMA layout they take 16 lanes x 16 B per
+  // store instruction at a 128-byte stride, and those scattered partial-line
+  // writes slow the other workgroups' streaming reads (4-5 us per launch at
+  // configs[2]).  After the barrier no wave reads the table or the ring any
+  // more, so wave w stages at w * ratio * PD floats from the start of LDS.
+  static_assert(G * 16 * PD * 4 <= RG::LDS, "staging of the partial rows exceeds LDS");
+  __builtin_amdgcn_s_barrier();
+  float* const stage = reinterpret_cast<float*>(&sm) + (size_t)w * ratio * PD;
+  const int64_t orow0 = row * p.Hq + kvh * ratio;  // first row of this wave
   if (n < ratio) {
     // o = pv_scale * O / lsum' (p' = p * pv_scale in both O and lsum')
     const float inv = lt > 0.f ? p.pv_scale / lt : 0.0f;
-    const int64_t orow = row * p.Hq + kvh * ratio + n;
-    float* out = p.po + orow * PD + q4 * (PD / 4);
+    float* dst = stage + n * PD + q4 * (PD / 4);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
 #pragma unroll
       for (int i = 0; i < NO; i += 4) {
         float4_t v = {st.O[i][r] * inv, st.O[i + 1][r] * inv, st.O[i + 2][r] * inv,
                       st.O[i + 3][r] * inv};
-        *reinterpret_cast<float4_t*>(out + r * NO + i) = v;
+        *reinterpret_cast<float4_t*>(dst + r * NO + i) = v;
       }
     }
     // natural-log LSE: (m + log2(sum p)) * ln 2 = (mb + log2(lsum')) * ln 2
     if (q4 == 0)
-      p.plse[orow] = lt > 0.f ? (st.mb + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
+      p.plse[orow0 + n] = lt > 0.f ? (st.mb + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
+  }
+  // LDS operations of a wave complete in order: the reads below see the
+  // writes above
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  // rows are stored as fp16 (the combine reads them so): half the bytes of
+  // fp32 rows, and their rounding (relative 2^-11 on normalised outputs) is
+  // far inside the output tolerance
+  _Float16* const out = reinterpret_cast<_Float16*>(p.po) + orow0 * PD;
+  for (int e = 8 * lane; e < ratio * PD; e += 512) {
+    const float4_t a = *reinterpret_cast<const float4_t*>(stage + e);
+    const float4_t c = *reinterpret_cast<const float4_t*>(stage + e + 4);
+    const half8_t h = {(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
+                       (_Float16)c[0], (_Float16)c[1], (_Float16)c[2], (_Float16)c[3]};
+    *reinterpret_cast<half8_t*>(out + e) = h;
   }
 }
 // LSE merge of the splits of one (sequence, q head), inverse rotation, fp16
@@ -1296,8 +1321,14 @@ void decode_partials_kernel(DecodeParams p) {
 // 256/(PD/4) split groups each sum a strided subset of the splits for one
 // float4 column, a tree in LDS adds the groups, and wave 0 runs the inverse
 // FWHT across its 64 lanes.
+// four fp16 partial-row values as fp32
+__device__ __forceinline__ float4_t load_half4(const _Float16* src) {
+  const half4_t h = *reinterpret_cast<const half4_t*>(src);
+  return float4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+
 template <int PD>
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ po,
+__global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict__ po,
                                                       const float* __restrict__ plse, int S_fixed,
                                                       const int32_t* __restrict__ split_rows,
                                                       int Hq, const float* __restrict__ signs,
@@ -1335,7 +1366,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
       v[j] = float4_t{0.f, 0.f, 0.f, 0.f};
       if (s < S) {
         l[j] = plse[row0 + (int64_t)s * rs];
-        v[j] = *reinterpret_cast<const float4_t*>(po + (row0 + (int64_t)s * rs) * PD + col * 4);
+        v[j] = load_half4(po + (row0 + (int64_t)s * rs) * PD + col * 4);
       }
     }
     float mx = -INFINITY;
@@ -1370,7 +1401,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
       const float wgt = sm[s];
       den += wgt;
       if (wgt != 0.0f)
-        acc += wgt * *reinterpret_cast<const float4_t*>(po + (row0 + (int64_t)s * rs) * PD + col * 4);
+        acc += wgt * load_half4(po + (row0 + (int64_t)s * rs) * PD + col * 4);
     }
     __syncthreads();  // weights no longer needed; reuse LDS for group sums
   }
@@ -1720,15 +1751,15 @@ static int combine_splits(const float* partition_o, const float* partition_lse,
   dim3 grid((unsigned)blocks), block(256);
   switch (pd) {
     case 64:
-      hipLaunchKernelGGL(combine_kernel<64>, grid, block, lds, st, partition_o, partition_lse,
+      hipLaunchKernelGGL(combine_kernel<64>, grid, block, lds, st, reinterpret_cast<const _Float16*>(partition_o), partition_lse,
                          num_splits, split_rows, num_qo_heads, signs, isq, out);
       break;
     case 128:
-      hipLaunchKernelGGL(combine_kernel<128>, grid, block, lds, st, partition_o, partition_lse,
+      hipLaunchKernelGGL(combine_kernel<128>, grid, block, lds, st, reinterpret_cast<const _Float16*>(partition_o), partition_lse,
                          num_splits, split_rows, num_qo_heads, signs, isq, out);
       break;
     default:
-      hipLaunchKernelGGL(combine_kernel<256>, grid, block, lds, st, partition_o, partition_lse,
+      hipLaunchKernelGGL(combine_kernel<256>, grid, block, lds, st, reinterpret_cast<const _Float16*>(partition_o), partition_lse,
                          num_splits, split_rows, num_qo_heads, signs, isq, out);
   }
   hipError_t e = hipGetLastError();
@@ -1913,6 +1944,46 @@ extern "C" int tq_decode_paged_balanced_noalloc(
                              seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, padded_dim,
                              block_size, ebs, num_blocks, sm_scale, signs, rows, po, plse,
                              split_rows, o, stream);
+}
+
+// Diagnostic: the configs[2] partials kernel (head size 128, 8 kv heads per
+// workgroup, static splits) with the step math compiled out: the same
+// prologue, page walk, copy ring, waits, barriers and slot reads, zero
+// partial rows.  Its time is what the data movement alone costs.
+extern "C" int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                     const uint8_t* k_slab, const uint8_t* v_slab,
+                                     const int32_t* indices, const int32_t* indptr,
+                                     const int32_t* seq_lens, int32_t batch,
+                                     int32_t num_qo_heads, int32_t num_kv_heads,
+                                     int32_t padded_dim, int32_t block_size, int32_t ebs,
+                                     int64_t num_blocks, float sm_scale, const float* signs,
+                                     int32_t num_splits, int32_t kv_chunk_size,
+                                     float* partition_o, float* partition_lse,
+                                     tq_stream_t stream) {
+  using namespace tq;
+  if (num_splits < 1 || kv_chunk_size < 1) {
+    set_error("diag_decode_stream: num_splits %d, kv_chunk_size %d out of range", num_splits,
+              kv_chunk_size);
+    return kEinval;
+  }
+  DecodeParams p;
+  int rc = decode_setup(q, q_stride_b, q_stride_h, k_slab, v_slab, indices, indptr, seq_lens,
+                        batch, num_qo_heads, num_kv_heads, padded_dim, block_size, ebs,
+                        num_blocks, sm_scale, signs, partition_o, partition_lse, p);
+  if (rc || batch == 0) return rc;
+  if (padded_dim != 128 || p.G != 8 || p.ratio > 8) {
+    set_error("diag_decode_stream: built for head size 128, 8 kv heads per workgroup, GQA "
+              "ratio <= 8 only");
+    return kEinval;
+  }
+  p.S = num_splits;
+  p.cs = kv_chunk_size;
+  const int64_t blocks = (int64_t)batch * num_splits * p.HG;
+  const PartialsFn fn = &decode_partials_kernel<128, 8, 2, true, false, false>;
+  const Occupancy occ = occupancy(reinterpret_cast<const void*>(fn), 64 * p.G);
+  if (occ.per_cu == 2 && blocks == 2LL * occ.cus && num_splits % 2 == 0)
+    p.pair_pct = kPairPct;
+  return launch_partials(fn, p, blocks, stream);
 }
 
 extern "C" int tq_decode_balanced_rows(int32_t batch, int32_t num_qo_heads,
