@@ -349,17 +349,29 @@ struct SoftmaxState {
 };
 
 // The dequant table: 256 entries (entry e = fp16 values of the high and low
-// nibble of code byte e), each held in kLutCopies copies side by side at the
-// start of LDS (entry e, copy c at dword e * kLutCopies + c).  Lane l reads
-// copy l mod 32, so the 32 lanes the LDS serves per cycle always hit 32
-// distinct banks, whatever the codes: a lookup never has a bank conflict.
-constexpr int kLutCopies = 32;
-constexpr int kLutBytes = 256 * 4 * kLutCopies;
+// nibble of code byte e), each held in LC copies side by side at the
+// start of LDS (entry e, copy c at dword e * LC + c).  Lane l reads copy
+// l mod LC; with 32 copies the 32 lanes the LDS serves per cycle always hit
+// 32 distinct banks, whatever the codes, so a lookup never has a bank
+// conflict.
+//
+// Copies of the table for a workgroup of G kv heads of head size PD.  32
+// copies make every lookup conflict-free; 16 halve the table (lanes l and
+// l + 16 may share a bank) so that more workgroups fit a CU.  Measured on
+// configs[3] (B = 64 ragged): head size 256 with 2 kv heads 174 -> 158 us and
+// head size 128 with 4 kv heads 170 -> 146 us with 16 copies; head size 64
+// with 4 kv heads 97 -> 109 us, so it keeps 32, as does the 8-head group of
+// configs[2] (its two workgroups per CU are already bound by the ring).
+__host__ __device__ constexpr int lut_copies(int pd, int g) {
+  return pd == 64 || (pd == 128 && g == 8) ? 32 : 16;
+}
+__host__ __device__ constexpr int lut_shift(int copies) { return copies == 32 ? 7 : 6; }
 
 // LDS byte address of the table entry `byte k of w` for this lane (lanec =
-// 4 * (lane mod 32)).
+// 4 * (lane mod copies), entries 2^SH bytes apart).
+template <int SH>
 __device__ __forceinline__ uint32_t lut_addr(uint32_t w, int k, uint32_t lanec) {
-  return (((w >> (8 * k)) & 0xffu) << 7) | lanec;
+  return (((w >> (8 * k)) & 0xffu) << SH) | lanec;
 }
 
 // Eight table reads in place (each address register receives its entry)
@@ -395,7 +407,7 @@ __device__ __forceinline__ void lut_read8(uint32_t* a) {
 // 8..15 (GQA ratio <= 8), one MFMA per K block, and the two halves are added
 // across lanes n and n+8 (both end up with the sum); otherwise qb/ql are
 // separate hi/lo operands, two MFMAs per K block.
-template <int PD, bool QC>
+template <int PD, bool QC, int SH>
 __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_t* qb,
                                                 const half8_t* ql, uint32_t lanec) {
   constexpr int KD = PD / 32;
@@ -407,7 +419,7 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
 #pragma unroll
     for (int u = 0; u < 2; u++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) x[4 * u + j] = lut_addr(kw[c + u], j, lanec);
+      for (int j = 0; j < 4; j++) x[4 * u + j] = lut_addr<SH>(kw[c + u], j, lanec);
     lut_read8(x);
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -435,7 +447,7 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
 // nibble high): the table maps it to (value of the first, value of the
 // second).  Byte k's low nibbles give dim slot 2k + 1, its high nibbles
 // dim slot 2k.
-template <int PD>
+template <int PD, int SH>
 __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD / 128 : 1],
                                         const uint32_t (*v1)[(PD / 32) >= 4 ? PD / 128 : 1],
                                         half8_t p, SoftmaxState<PD>& st, uint32_t lanec) {
@@ -466,7 +478,7 @@ __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD
       for (int T = 0; T < 2; T++)
 #pragma unroll
         for (int pr = 0; pr < 2; pr++)
-          x[4 * nb + 2 * T + pr] = lut_addr(ix[T][pr][nb][w], j, lanec);
+          x[4 * nb + 2 * T + pr] = lut_addr<SH>(ix[T][pr][nb][w], j, lanec);
     lut_read8(x);
     const half8_t lo8 = as_half8(x[0], x[1], x[2], x[3]);
     const half8_t hi8 = as_half8(x[4], x[5], x[6], x[7]);
@@ -525,7 +537,10 @@ struct RingGeom {
   static constexpr int NW_HI = (NIT + G - 1) / G;             // copies per tile, waves < NIT % G
   static constexpr int NW_LO = NIT / G;                       // copies per tile, other waves
   static constexpr int RING = kRingSlots * TS;
-  static constexpr int LDS = kLutBytes + RING;               // table + ring
+  static constexpr int LC = lut_copies(PD, G);               // table copies
+  static constexpr int SH = lut_shift(LC);                    // log2 of an entry's bytes
+  static constexpr int LUTB = 256 * 4 * LC;                   // table bytes
+  static constexpr int LDS = LUTB + RING;                     // table + ring
 };
 
 // This wave's K codes, V codes and norms of the step's two tiles, read from
@@ -740,19 +755,19 @@ void decode_partials_kernel(DecodeParams p) {
   // LDS: the dequant table at address 0 (the table reads rely on it), then
   // the ring of tile slots
   struct __attribute__((aligned(16))) Lds {
-    uint32_t klut[256 * kLutCopies];
+    uint32_t klut[256 * RG::LC];
     uint8_t ring[RG::RING];
   };
   __shared__ Lds sm;
 
   // dequant table: byte e -> fp16 values of its high nibble (low half) and
   // its low nibble (high half), built with the same table arithmetic as dq8,
-  // in kLutCopies copies (written four at a time, as inline assembly: the
+  // in RG::LC copies (written four at a time, as inline assembly: the
   // copies in flight into the ring do not touch it, which the compiler
   // cannot tell)
   auto init_table = [&]() {
-    for (int i = threadIdx.x; i < 64 * kLutCopies; i += 64 * G) {
-      const int e = i / (kLutCopies / 4);
+    for (int i = threadIdx.x; i < 64 * RG::LC; i += 64 * G) {
+      const int e = i / (RG::LC / 4);
       uint32_t x[4];
       dq8((uint32_t)e * 0x01010101u, x);
       [[maybe_unused]] const uint32_t val = (x[2] & 0xffffu) | (x[0] << 16);
@@ -768,7 +783,7 @@ void decode_partials_kernel(DecodeParams p) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int q4 = lane >> 4, n = lane & 15;
-  const uint32_t lanec = (uint32_t)(lane & 31) * 4u;  // this lane's table copy
+  const uint32_t lanec = (uint32_t)(lane & (RG::LC - 1)) * 4u;  // this lane's table copy
   const int half = gridDim.x >> 1;
   const int mem = p.pair_pct > 0 && (int)blockIdx.x >= half;
   int bid = blockIdx.x - mem * half;
@@ -1187,9 +1202,9 @@ void decode_partials_kernel(DecodeParams p) {
       // scores of both tiles (scheduling barriers keep the two tiles'
       // dequant temporaries from being live at the same time)
       float4_t acc[2];
-      acc[0] = tile_scores<PD, QC>(d.k[0], qb, ql, lanec);
+      acc[0] = tile_scores<PD, QC, RG::SH>(d.k[0], qb, ql, lanec);
       __builtin_amdgcn_sched_barrier(0);
-      acc[1] = tile_scores<PD, QC>(d.k[1], qb, ql, lanec);
+      acc[1] = tile_scores<PD, QC, RG::SH>(d.k[1], qb, ql, lanec);
       __builtin_amdgcn_sched_barrier(0);
       constexpr int NV = 4 * (2 / PACK);  // score values per lane
       float sc[NV], nk[NV], nv[NV];
@@ -1232,7 +1247,7 @@ void decode_partials_kernel(DecodeParams p) {
       } else {
         p8 = half8_t{pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
       }
-      step_pv<PD>(d.v[0], d.v[1], p8, st, lanec);
+      step_pv<PD, RG::SH>(d.v[0], d.v[1], p8, st, lanec);
     };
 
     // one step: tiles 2k, 2k + 1 in ring slots s0, s1
@@ -1244,7 +1259,7 @@ void decode_partials_kernel(DecodeParams p) {
       __builtin_amdgcn_sched_barrier(0);
       StepData<PD> d;
       {
-        const uint32_t b0 = kLutBytes + s0 * RG::TS, b1 = kLutBytes + s1 * RG::TS;  // K regions
+        const uint32_t b0 = RG::LUTB + s0 * RG::TS, b1 = RG::LUTB + s1 * RG::TS;  // K regions
         const uint32_t ka[2] = {oK[0] + b0, oK[0] + b1};
         const uint32_t na = oN + (PACK == 2 && ptile ? b1 : b0);
         read_step<PD, G, PACK>(ka, oV + b0 + RG::SLAB, oV + b1 + RG::SLAB, na, oN + b1, d);
@@ -1279,7 +1294,10 @@ void decode_partials_kernel(DecodeParams p) {
   // writes slow the other workgroups' streaming reads (4-5 us per launch at
   // configs[2]).  After the barrier no wave reads the table or the ring any
   // more, so wave w stages at w * ratio * PD floats from the start of LDS.
-  static_assert(G * 16 * PD * 4 <= RG::LDS, "staging of the partial rows exceeds LDS");
+  // The staging holds G * ratio * PD floats: within the table region when
+  // ratio * PD <= 1024 (the assert), and within table + ring otherwise (the
+  // launcher picks G so that the q scratch of that size fits, the same bound).
+  static_assert(G * 4096 <= RG::LUTB, "the q' scratch of the waves exceeds the table region");
   __builtin_amdgcn_s_barrier();
   float* const stage = reinterpret_cast<float*>(&sm) + (size_t)w * ratio * PD;
   const int64_t orow0 = row * p.Hq + kvh * ratio;  // first row of this wave
@@ -1453,7 +1471,7 @@ int ring_lds_bytes(int pd, int g) {
   const int ech = (pd == 64 ? 48 : (pd == 128 ? 80 : 144)) / 16;
   const int rch = (g * ech) | 1;
   const int ni = (kTile * rch + 63) / 64;
-  return kLutBytes + kRingSlots * 2 * ni * 1024;
+  return 256 * 4 * lut_copies(pd, g) + kRingSlots * 2 * ni * 1024;
 }
 
 // Heads (waves) per partials workgroup: the largest of 8, 4, 2, 1 (at most 4

@@ -71,8 +71,15 @@ def _waves_per_simd(pd: int, ratio: int) -> int:
     return 4 if ratio <= 8 else 3
 
 
-LUT_BYTES = 256 * 4 * 32  # dequant table: 256 entries x 32 bank-spread copies
 RING_SLOTS = 2
+
+
+def lut_bytes(pd: int, g: int) -> int:
+    """Dequant-table bytes of a decode workgroup (tq_decode.hip lut_copies):
+    256 entries x 32 bank-spread copies, 16 copies for head size 128 with
+    fewer than 8 kv heads per workgroup and for head size 256."""
+    copies = 32 if pd == 64 or (pd == 128 and g == 8) else 16
+    return 256 * 4 * copies
 
 
 def ring_lds_bytes(pd: int, g: int) -> int:
@@ -82,7 +89,7 @@ def ring_lds_bytes(pd: int, g: int) -> int:
     ech = entry_bytes(pd)[2] // 16
     rch = (g * ech) | 1
     ni = (16 * rch + 63) // 64
-    return LUT_BYTES + RING_SLOTS * 2 * ni * 1024
+    return lut_bytes(pd, g) + RING_SLOTS * 2 * ni * 1024
 
 
 def decode_group_size(pd: int, num_kv_heads: int, ratio: int) -> int:
