@@ -448,17 +448,35 @@ def main():
     log(f"decode step {ms * 1e3:.1f} us (graph replay; {ms_eager * 1e3:.1f} us launched one "
         f"call at a time from Python) -> {value:.0f} GB/s; the other op "
         f"{ms_other * 1e3:.1f} us")
-    # the partials kernel's average duration inside the step: the step minus
-    # the combine kernel alone over the same 512 partial rows (both
-    # graph-timed with HIP events on the replay stream).  HIP events around
-    # each launch would add 3-5 us of their own to every launch.
+    # the partials kernel's average duration: a HIP graph of the partials
+    # kernel alone, launched back to back, timed with HIP events on the
+    # replay stream (per launch: the kernel plus the graph's launch gap, no
+    # host overhead); the combine likewise alone over the same 512 rows.
+    # HIP events around each launch would add 3-5 us of their own to it.
+    def partials_only():
+        if args.static:
+            rc = lib.tq_decode_partials(
+                w["q"].data_ptr(), w["q"].stride(0), w["q"].stride(1), cache.data_ptr(),
+                cache.data_ptr() + cache[0].numel(), w["indices"].data_ptr(),
+                w["indptr"].data_ptr(), w["seq"].data_ptr(), b, hq, w["hkv"], pd, 16, w["ebs"],
+                w["nb"], scale, w["signs"].data_ptr(), S, w["cs"], po.data_ptr(), pl.data_ptr(),
+                torch.cuda.current_stream().cuda_stream)
+        else:
+            rc = lib.tq_decode_partials_balanced(
+                w["q"].data_ptr(), w["q"].stride(0), w["q"].stride(1), cache.data_ptr(),
+                cache.data_ptr() + cache[0].numel(), w["indices"].data_ptr(),
+                w["indptr"].data_ptr(), w["seq"].data_ptr(), b, hq, w["hkv"], w["hd"], pd, 16,
+                w["ebs"], w["nb"], scale, w["signs"].data_ptr(), rows, pob.data_ptr(),
+                plb.data_ptr(), split.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "partials")
+
+    ms_k = time_graph(torch, partials_only, args.steps, args.warmup)
     step_static()
     torch.cuda.synchronize()
     ms_c = time_graph(torch, combine_only, args.steps, args.warmup)
-    ms_k = ms - ms_c
     achieved = nbytes / (ms_k * 1e-3) / 1e9
-    log(f"partials kernel {ms_k * 1e3:.1f} us (step - combine {ms_c * 1e3:.1f} us) -> "
-        f"{achieved:.0f} GB/s")
+    log(f"partials kernel {ms_k * 1e3:.1f} us -> {achieved:.0f} GB/s; combine {ms_c * 1e3:.1f} us; "
+        f"step - both {(ms - ms_k - ms_c) * 1e3:.1f} us of launch gaps")
     stream_ref = None
     if args.stream_ref:
         def stream_only():
@@ -516,6 +534,8 @@ def main():
                      "traffic": PROFILED_TRAFFIC.get((S, w["cs"])),
                      "traffic_source": TRAFFIC_SOURCE,
                      "kernel": kname, "kernel_us": round(ms_k * 1e3, 2),
+                     "kernel_timing": "HIP events around graph replays of the partials kernel "
+                                      "alone, back to back (kernel + graph launch gap)",
                      "combine_us": round(ms_c * 1e3, 2), "alg_bytes": nbytes},
         "cpu_baseline": cpu,
         "configs3_ragged": ragged,

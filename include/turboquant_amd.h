@@ -144,6 +144,23 @@ int tq_decode_paged_balanced_noalloc(const void* q, int64_t q_stride_b, int64_t 
                                      tq_stream_t stream);
 
 /*
+ * The first kernel of tq_decode_paged_balanced alone: the plan, the partial
+ * rows (fp16 in partition_o) and partition_lse, and the row table in
+ * split_rows; tq_combine_splits does not read a plan's rows, so this serves
+ * timing and inspection of the partials kernel.
+ */
+int tq_decode_partials_balanced(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                const uint8_t* k_slab, const uint8_t* v_slab,
+                                const int32_t* indices, const int32_t* indptr,
+                                const int32_t* seq_lens, int32_t batch,
+                                int32_t num_qo_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t padded_dim,
+                                int32_t block_size, int32_t ebs, int64_t num_blocks,
+                                float sm_scale, const float* signs, int32_t max_rows,
+                                float* partition_o, float* partition_lse,
+                                int32_t* split_rows, tq_stream_t stream);
+
+/*
  * Partial rows tq_decode_paged_balanced uses at most for this geometry on
  * the current device (or -22).  Queries the device once per geometry.
  */

@@ -31,6 +31,9 @@ SIGNATURES = {
     "tq_decode_paged_balanced_noalloc": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P, _I32, _I32,
                                                 _I32, _I32, _I32, _I32, _I32, _I64, _F32, _P,
                                                 _P, _P]),
+    "tq_decode_partials_balanced": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                           _I32, _I32, _I32, _I32, _I64, _F32, _P, _I32, _P,
+                                           _P, _P, _P]),
     "tq_decode_balanced_rows": (_I32, [_I32, _I32, _I32, _I32]),
     "tq_decode_partials": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                   _I32, _I32, _I64, _F32, _P, _I32, _I32, _P, _P, _P]),

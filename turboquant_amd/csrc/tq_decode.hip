@@ -1788,16 +1788,17 @@ static int combine_splits(const float* partition_o, const float* partition_lse,
   return 0;
 }
 
-// Balanced split: partials over a device-computed plan, then the combine
-// over the row table the partials kernel wrote.
-static int decode_balanced(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                           const uint8_t* k_slab, const uint8_t* v_slab, const int32_t* indices,
-                           const int32_t* indptr, const int32_t* seq_lens, int32_t batch,
-                           int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
-                           int32_t padded_dim, int32_t block_size, int32_t ebs,
-                           int64_t num_blocks, float sm_scale, const float* signs,
-                           int32_t max_rows, float* partition_o, float* partition_lse,
-                           int32_t* split_rows, void* o, tq_stream_t stream) {
+// The partials kernel of a balanced decode alone; `rows` receives the rows
+// the plan may use (for the combine's LDS sizing).
+static int partials_balanced(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                             const uint8_t* k_slab, const uint8_t* v_slab,
+                             const int32_t* indices, const int32_t* indptr,
+                             const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t padded_dim,
+                             int32_t block_size, int32_t ebs, int64_t num_blocks, float sm_scale,
+                             const float* signs, int32_t max_rows, float* partition_o,
+                             float* partition_lse, int32_t* split_rows, tq_stream_t stream,
+                             int* rows) {
   if (head_dim <= 0 || head_dim > padded_dim) {
     set_error("decode: head_dim %d exceeds padded_dim %d", head_dim, padded_dim);
     return kEinval;
@@ -1812,7 +1813,7 @@ static int decode_balanced(const void* q, int64_t q_stride_b, int64_t q_stride_h
               batch);
     return kEinval;
   }
-  if (!split_rows || !o) {
+  if (!split_rows) {
     set_error("decode: null pointer");
     return kEinval;
   }
@@ -1825,9 +1826,32 @@ static int decode_balanced(const void* q, int64_t q_stride_b, int64_t q_stride_h
   p.units = g.units;
   p.pair_pct = g.pair_pct;
   p.split_out = split_rows;
-  rc = launch_partials(fn, p, g.blocks, stream);
-  if (rc) return rc;
-  return combine_splits(partition_o, partition_lse, batch, 1, split_rows, g.rows,
+  *rows = g.rows;
+  return launch_partials(fn, p, g.blocks, stream);
+}
+
+// Balanced split: partials over a device-computed plan, then the combine
+// over the row table the partials kernel wrote.
+static int decode_balanced(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                           const uint8_t* k_slab, const uint8_t* v_slab, const int32_t* indices,
+                           const int32_t* indptr, const int32_t* seq_lens, int32_t batch,
+                           int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t padded_dim, int32_t block_size, int32_t ebs,
+                           int64_t num_blocks, float sm_scale, const float* signs,
+                           int32_t max_rows, float* partition_o, float* partition_lse,
+                           int32_t* split_rows, void* o, tq_stream_t stream) {
+  if (!o) {
+    set_error("decode: null pointer");
+    return kEinval;
+  }
+  int rows = 0;
+  const int rc = partials_balanced(q, q_stride_b, q_stride_h, k_slab, v_slab, indices, indptr,
+                                   seq_lens, batch, num_qo_heads, num_kv_heads, head_dim,
+                                   padded_dim, block_size, ebs, num_blocks, sm_scale, signs,
+                                   max_rows, partition_o, partition_lse, split_rows, stream,
+                                   &rows);
+  if (rc || batch == 0) return rc;
+  return combine_splits(partition_o, partition_lse, batch, 1, split_rows, rows,
                         num_qo_heads, padded_dim, signs, o, stream);
 }
 
@@ -2002,6 +2026,20 @@ extern "C" int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t 
   if (occ.per_cu == 2 && blocks == 2LL * occ.cus && num_splits % 2 == 0)
     p.pair_pct = kPairPct;
   return launch_partials(fn, p, blocks, stream);
+}
+
+extern "C" int tq_decode_partials_balanced(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* k_slab,
+    const uint8_t* v_slab, const int32_t* indices, const int32_t* indptr,
+    const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t padded_dim, int32_t block_size, int32_t ebs, int64_t num_blocks,
+    float sm_scale, const float* signs, int32_t max_rows, float* partition_o,
+    float* partition_lse, int32_t* split_rows, tq_stream_t stream) {
+  int rows = 0;
+  return tq::partials_balanced(q, q_stride_b, q_stride_h, k_slab, v_slab, indices, indptr,
+                               seq_lens, batch, num_qo_heads, num_kv_heads, head_dim,
+                               padded_dim, block_size, ebs, num_blocks, sm_scale, signs,
+                               max_rows, partition_o, partition_lse, split_rows, stream, &rows);
 }
 
 extern "C" int tq_decode_balanced_rows(int32_t batch, int32_t num_qo_heads,
