@@ -33,11 +33,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per launch of the partials kernel at the default split layout,
-# from rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), each scale taken from a
-# 256 MiB device copy (profiles/decode_partials_cfg3_hbm_traffic.md); keyed by
-# (num_splits, kv_chunk_size) so an overridden layout reports null.
-PROFILED_TRAFFIC = {(64, 512): 346448681}
+# HBM bytes per launch of the partials kernel at configs[2] (512 rows of 512
+# tokens), from rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), each scale
+# taken from a 256 MiB device copy (profiles/decode_partials_cfg3_hbm_traffic.md);
+# keyed by (op, num_splits, kv_chunk_size) so an overridden layout reports null.
+PROFILED_TRAFFIC = {("balanced", 64, 512): 342022000, ("static", 64, 512): 342262000}
 TRAFFIC_SOURCE = ("profiled constant: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel at "
                   "this layout, profiles/decode_partials_cfg3_hbm_traffic.md")
 
@@ -531,7 +531,8 @@ def main():
         "layout_GB/s": round(layout_bytes / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": PROFILED_TRAFFIC.get((S, w["cs"])),
+                     "traffic": PROFILED_TRAFFIC.get(("static" if args.static else "balanced",
+                                                      S, w["cs"])),
                      "traffic_source": TRAFFIC_SOURCE,
                      "kernel": kname, "kernel_us": round(ms_k * 1e3, 2),
                      "kernel_timing": "HIP events around graph replays of the partials kernel "
