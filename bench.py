@@ -362,6 +362,9 @@ def main():
                     help="headline through the reference's static-split op instead of the "
                          "balanced op the backend uses")
     ap.add_argument("--splits", type=int, default=0, help="override num_splits (--static)")
+    ap.add_argument("--seq-len", type=int, default=32768,
+                    help="cached tokens per sequence of the headline workload (configs[2]: "
+                         "32768; other lengths for the step/fixed-cost split of the kernel)")
     ap.add_argument("--copy-ref", action="store_true",
                     help="only run a plain 256 MiB device copy x5 (HBM counter scale reference)")
     ap.add_argument("--stream-ref", action="store_true",
@@ -395,7 +398,7 @@ def main():
     ragged = None if (quick or args.no_ragged) else bench_ragged(torch, args.steps, args.warmup)
     e2e_res = None if (quick or args.no_e2e) else bench_e2e(torch)
     log("building cfg-3 cache on the GPU (write kernel)")
-    w = make_decode_workload(torch)
+    w = make_decode_workload(torch, seq_len=args.seq_len)
     if args.splits:
         w["splits"] = args.splits
         w["cs"] = -(-w["seq_len"] // args.splits) + 15 & ~15
