@@ -374,6 +374,29 @@ __device__ __forceinline__ uint32_t lut_addr(uint32_t w, int k, uint32_t lanec) 
   return (((w >> (8 * k)) & 0xffu) << SH) | lanec;
 }
 
+// Table addresses from code bytes spread into 16-bit halves: lut_spread
+// puts bytes 2i and 2i + 1 of w into the low and high halves of one register
+// (v_perm), and lut_mad forms half * 2^SH + lanec in one v_mad_u32_u16
+// (op_sel picks the half), so a pair of lookups costs three instructions
+// instead of four.  lut_mad<SH, HI>(lut_spread(w, i), lanec) equals
+// lut_addr<SH>(w, 2 * i + HI, lanec).
+__device__ __forceinline__ uint32_t lut_spread(uint32_t w, int i) {
+  return __builtin_amdgcn_perm(0u, w, i ? 0x0c030c02u : 0x0c010c00u);
+}
+template <int SH, int HI>
+__device__ __forceinline__ uint32_t lut_mad(uint32_t h, uint32_t lanec) {
+  uint32_t a;
+#if defined(__HIP_DEVICE_COMPILE__)
+  if constexpr (HI)
+    asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(a) : "v"(h), "s"(1u << SH), "v"(lanec));
+  else
+    asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(a) : "v"(h), "s"(1u << SH), "v"(lanec));
+#else
+  a = ((HI ? h >> 16 : h & 0xffffu) << SH) + lanec;
+#endif
+  return a;
+}
+
 // Eight table reads in place (each address register receives its entry)
 // and one wait; inline assembly, so the compiler adds no conservative wait
 // for the copies in flight.
@@ -419,7 +442,11 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
 #pragma unroll
     for (int u = 0; u < 2; u++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) x[4 * u + j] = lut_addr<SH>(kw[c + u], j, lanec);
+      for (int i = 0; i < 2; i++) {
+        const uint32_t h = lut_spread(kw[c + u], i);
+        x[4 * u + 2 * i] = lut_mad<SH, 0>(h, lanec);
+        x[4 * u + 2 * i + 1] = lut_mad<SH, 1>(h, lanec);
+      }
     lut_read8(x);
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -456,6 +483,7 @@ __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD
   // ix[T][pair][nibble][w]: pair 0 = tokens 0, 1; pair 1 = tokens 2, 3;
   // nibble 0 = low nibbles, 1 = high nibbles
   uint32_t ix[2][2][2][VW];
+  uint32_t hs[2][2][2];  // two bytes of each index word, spread into 16-bit halves
 #pragma unroll
   for (int T = 0; T < 2; T++) {
     const uint32_t (*v)[VW] = T ? v1 : v0;
@@ -472,13 +500,23 @@ __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD
   for (int k = 0; k < VB; k++) {
     const int w = k / 4, j = k % 4;
     uint32_t x[8];
+    if (j % 2 == 0) {
+      // bytes j and j + 1 of every index word, spread into 16-bit halves
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+        for (int T = 0; T < 2; T++)
+#pragma unroll
+          for (int pr = 0; pr < 2; pr++) hs[nb][T][pr] = lut_spread(ix[T][pr][nb][w], j / 2);
+    }
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
 #pragma unroll
       for (int T = 0; T < 2; T++)
 #pragma unroll
         for (int pr = 0; pr < 2; pr++)
-          x[4 * nb + 2 * T + pr] = lut_addr<SH>(ix[T][pr][nb][w], j, lanec);
+          x[4 * nb + 2 * T + pr] = j % 2 ? lut_mad<SH, 1>(hs[nb][T][pr], lanec)
+                                         : lut_mad<SH, 0>(hs[nb][T][pr], lanec);
     lut_read8(x);
     const half8_t lo8 = as_half8(x[0], x[1], x[2], x[3]);
     const half8_t hi8 = as_half8(x[4], x[5], x[6], x[7]);
