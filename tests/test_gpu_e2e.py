@@ -2,7 +2,8 @@
 geometry (32/8/128) run through TurboQuantFusedImpl (write + prefill +
 balanced decode).  Every layer's decode attention is checked against the
 oracle's dequantize-then-attend (max-abs 2e-3 / rel 1e-2); the graph-captured
-decode step must give the eager step's tokens on every replay."""
+decode step must give the eager step's tokens on every replay; e2e.run's
+tokens must agree with a dequantize-then-attend decode of the same model."""
 import math
 
 import numpy as np
@@ -83,3 +84,10 @@ def test_e2e_run_reports_serving_figures():
               "teacher_forced_in_top5_rate"):
         assert 0.0 <= a[k] <= 1.0, k
     print(f"agreement {a}", flush=True)
+    # against dequantize-then-attend over the same quantized cache only the
+    # fused kernel's arithmetic differs: the tokens must agree
+    d = res["agreement_dequant"]
+    assert d["steps"] == 5
+    print(f"agreement with dequantize-then-attend {d}", flush=True)
+    assert d["teacher_forced_top1_match_rate"] >= 0.8, d
+    assert d["teacher_forced_in_top5_rate"] == 1.0, d

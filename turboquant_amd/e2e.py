@@ -37,6 +37,7 @@ from dataclasses import dataclass, field
 import torch
 import torch.nn.functional as F
 
+from . import ops
 from .vllm_backend_fused import TurboQuantBackend, TurboQuantFusedImpl
 
 BLOCK = 16
@@ -319,15 +320,26 @@ class Runner:
 
     # ------------------------------------------------------- fp16 reference
     @torch.no_grad()
-    def decode_fp16_reference(self, steps: int, forced: torch.Tensor | None = None):
-        """The same model decoded with attention over the fp16 K/V copies
-        (plain SDPA, no quantization), from the state the prefill left.
+    def decode_fp16_reference(self, steps: int, forced: torch.Tensor | None = None,
+                              kv: str = "fp16"):
+        """The same model decoded from the state the prefill left, with
+        attention in torch SDPA over
+
+        * kv="fp16": the fp16 K/V copies (no quantization);
+        * kv="dequant": the quantized cache read back as fp16 rows in the
+          original domain (tq_dequant_paged), the new token's K/V written
+          into the cache first: the reference's dequantize-then-attend
+          semantics (triton_decode_ref.py:264-299), so the difference from
+          the fused decode is the fused kernel's arithmetic alone.  It
+          rewrites the cache entries of the positions it decodes (the same
+          slots the fused decode writes).
 
         forced None: greedy free run; returns its tokens [steps, B].
         forced [steps, B] (another run's tokens): teacher forcing, each step
         fed the forced history; returns (top-1 tokens, rank of the forced
         token among this run's logits), both [steps, B]."""
-        assert self.kv16 is not None
+        assert kv in ("fp16", "dequant")
+        assert kv == "dequant" or self.kv16 is not None
         s = self.shape
         out = torch.zeros((steps, self.batch), dtype=torch.int64, device=self.device)
         rank = torch.zeros((steps, self.batch), dtype=torch.int64, device=self.device)
@@ -335,19 +347,35 @@ class Runner:
         tok = self.first_tok.clone()
         scale = 1.0 / math.sqrt(s.head_dim)
         p0 = int(pos[0])
-        assert bool((pos == p0).all()), "the fp16 reference decode needs equal lengths"
+        assert bool((pos == p0).all()), "the reference decode needs equal lengths"
+        if kv == "dequant":
+            kd = torch.empty((2, self.batch, self.max_tokens, s.kv_heads, s.head_dim),
+                             dtype=torch.float16, device=self.device)
+        bt = self.block_table
         for step in range(steps):
             p = p0 + step
             x = F.embedding(tok, self.weights["embed"])
             cs = self._rope_rows(pos)
+            if kv == "dequant":
+                page = bt.gather(1, (pos // BLOCK)[:, None]).squeeze(1).to(torch.int64)
+                slots = (page * BLOCK + pos % BLOCK).to(torch.int32)
             for li, lw in enumerate(self.weights["layers"]):
                 q, k, v = self._attn_qkv(lw, x, cs)
-                kv = self.kv16[li]
-                kv[0, :, :, p] = k
-                kv[1, :, :, p] = v
-                o = F.scaled_dot_product_attention(
-                    q[:, :, None, :], kv[0, :, :, :p + 1], kv[1, :, :, :p + 1],
-                    scale=scale, enable_gqa=True)
+                if kv == "fp16":
+                    kvl = self.kv16[li]
+                    kvl[0, :, :, p] = k
+                    kvl[1, :, :, p] = v
+                    kk, vv = kvl[0, :, :, :p + 1], kvl[1, :, :, :p + 1]
+                else:
+                    impl = self.impls[li]
+                    impl.do_kv_cache_update(None, k, v, self.caches[li], slots)
+                    for b in range(self.batch):
+                        ops.dequant_paged(self.caches[li], bt[b], p + 1, s.kv_heads, s.head_dim,
+                                          impl._pd, impl._signs, kd[0, b], kd[1, b])
+                    kk = kd[0, :, :p + 1].transpose(1, 2)
+                    vv = kd[1, :, :p + 1].transpose(1, 2)
+                o = F.scaled_dot_product_attention(q[:, :, None, :], kk, vv, scale=scale,
+                                                   enable_gqa=True)
                 x = x + F.linear(o.reshape(self.batch, -1), lw["o"])
                 x = self._mlp(lw, x)
             logits = self._logits(x)
@@ -404,6 +432,7 @@ def run(shape: ModelShape, batch: int = 8, prompt_len: int = 32768, new_tokens: 
     res = {}
     if compare_steps > 0:
         free = r.decode_fp16_reference(compare_steps)
+        free_dq = r.decode_fp16_reference(compare_steps, kv="dequant")
         torch.cuda.synchronize()
     steps = new_tokens - 1
     tc = time.perf_counter()
@@ -417,20 +446,28 @@ def run(shape: ModelShape, batch: int = 8, prompt_len: int = 32768, new_tokens: 
     say(f"[e2e] decode {steps} steps: {t_decode * 1e3:.1f} ms")
     if compare_steps > 0:
         n = min(compare_steps, steps)
-        same = (toks[:n] == free[:n]).cpu()
-        div = [int((~same[:, b]).nonzero()[0, 0]) if (~same[:, b]).any() else n
-               for b in range(batch)]
-        top, rank = r.decode_fp16_reference(n, forced=toks[:n])
-        rank = rank.cpu()
-        res["agreement"] = {
-            "steps": n,
-            "reference": "same model and prefill, attention over fp16 K/V (torch SDPA)",
-            "free_run_token_match_rate": float(same.float().mean()),
-            "free_run_first_divergence_step": div,
-            "teacher_forced_top1_match_rate": float((top[:n] == toks[:n]).float().mean()),
-            "teacher_forced_in_top5_rate": float((rank < 5).float().mean()),
-            "teacher_forced_median_rank": float(rank.float().median()),
-        }
+
+        def agreement(free_toks, kv, what):
+            same = (toks[:n] == free_toks[:n]).cpu()
+            div = [int((~same[:, b]).nonzero()[0, 0]) if (~same[:, b]).any() else n
+                   for b in range(batch)]
+            top, rank = r.decode_fp16_reference(n, forced=toks[:n], kv=kv)
+            rank = rank.cpu()
+            return {
+                "steps": n,
+                "reference": what,
+                "free_run_token_match_rate": float(same.float().mean()),
+                "free_run_first_divergence_step": div,
+                "teacher_forced_top1_match_rate": float((top[:n] == toks[:n]).float().mean()),
+                "teacher_forced_in_top5_rate": float((rank < 5).float().mean()),
+                "teacher_forced_median_rank": float(rank.float().median()),
+            }
+
+        res["agreement"] = agreement(
+            free, "fp16", "same model and prefill, attention over fp16 K/V (torch SDPA)")
+        res["agreement_dequant"] = agreement(
+            free_dq, "dequant", "same model, prefill and quantized cache, attention over the "
+            "cache read back as fp16 rows (dequantize-then-attend, torch SDPA)")
     res.update({
         "output_tok_s": batch * new_tokens / (t_prefill + t_decode),
         "decode_tok_s": batch * steps / t_decode if steps else None,
