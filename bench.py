@@ -540,7 +540,13 @@ def main():
                      "kernel": kname, "kernel_us": round(ms_k * 1e3, 2),
                      "kernel_timing": "HIP events around graph replays of the partials kernel "
                                       "alone, back to back (kernel + graph launch gap)",
-                     "combine_us": round(ms_c * 1e3, 2), "alg_bytes": nbytes},
+                     "combine_us": round(ms_c * 1e3, 2), "alg_bytes": nbytes,
+                     # the same kernel time against the bytes of the cache layout
+                     # (80-byte entries: pad and second norm copy included), which
+                     # whole cache lines make HBM move
+                     "layout_bytes": layout_bytes,
+                     "layout_frac": round(layout_bytes / (ms_k * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                          4)},
         "cpu_baseline": cpu,
         "configs3_ragged": ragged,
         "e2e": e2e_res,

@@ -56,6 +56,24 @@ def test_cfg3_uniform_matches_static_layout():
     _check(case, cache, pd, "balanced cfg3")
 
 
+@pytest.mark.parametrize("b,length", [(3, 1000), (64, 4096), (5, 1), (17, 33)])
+def test_uniform_lengths_closed_form_plan(b, length):
+    """Equal lengths take the plan's closed form (no search): the row table
+    is b equal blocks, the unit size the smallest that fits, and the output
+    matches the oracle."""
+    print(f"case: balanced uniform B={b} L={length}", flush=True)
+    c = W.decode_case(97 + b, b, [length] * b, 32, 8, 128)
+    cache, pd = G.build_cache(c)
+    _, _ = _check(c, cache, pd, f"balanced uniform B={b} L={length}")
+    _, _, _, split = G.run_balanced(c, cache, pd)
+    d = np.diff(split[:b + 1])
+    assert np.all(d == d[0]) and d[0] > 0, split[:b + 1]
+    u = int(split[b + 1])
+    # rows per sequence = rowmul * ceil(L / U); a smaller U (by 32) would need more
+    # units per sequence than U does
+    assert u >= 32 and u % 32 == 0 and (u == 32 or -(-length // (u - 32)) > -(-length // u)), u
+
+
 @pytest.mark.parametrize("hq,hkv,hd", [(32, 8, 128), (16, 2, 128), (16, 16, 64), (16, 4, 256),
                                        (16, 1, 128)])
 def test_edge_lengths(hq, hkv, hd):

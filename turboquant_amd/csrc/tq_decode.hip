@@ -265,6 +265,35 @@ __device__ __forceinline__ PlanSlot plan_slot(LensFn lens, StartsFn starts, int 
   mx = __builtin_amdgcn_readfirstlane(wave_max_i(mx));
   nz = __builtin_amdgcn_readfirstlane(wave_sum_i(nz));
   constexpr int A = kPlanAlign;
+  if (nreg == 1 && nz == B && (int64_t)mx * B == (int64_t)tsum) {
+    // every sequence has the same length L: sum_b ceil(L / U) <= units is
+    // ceil(L / U) <= k = floor(units / B), i.e. U >= L / k, so the plan has
+    // a closed form (no search, no scan before the first page-id loads)
+    const int k = units / B;
+    const int U = ((mx + k - 1) / k + A - 1) / A * A;
+    const int c = (mx + U - 1) / U;  // units per sequence
+    PlanSlot r = {-1, 0, 0, 0, U, 0};
+    if (u < B * c) {
+      r.b = u / c;
+      r.j = u - r.b * c;
+      r.Pb = r.b * c;
+      r.L = mx;
+      r.ip = __builtin_amdgcn_readlane(starts(0), r.b);
+    }
+    if (writer) {
+      if (lane < B) split_out[lane] = lane * c * rowmul;
+      if (lane == 0) {
+        split_out[B] = B * c * rowmul;
+        split_out[B + 1] = U;
+      }
+    }
+    r.b = __builtin_amdgcn_readfirstlane(r.b);
+    r.j = __builtin_amdgcn_readfirstlane(r.j);
+    r.L = __builtin_amdgcn_readfirstlane(r.L);
+    r.Pb = __builtin_amdgcn_readfirstlane(r.Pb);
+    r.ip = __builtin_amdgcn_readfirstlane(r.ip);
+    return r;
+  }
   auto units_for = [&](int k) -> int {
     const int d = k * A;
     const float rd = 1.0f / (float)d;
