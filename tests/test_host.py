@@ -251,3 +251,26 @@ def test_write_refuses_rows_narrower_than_head_dim():
     with pytest.raises(RuntimeError, match="fewer than head_dim"):
         ops.quantize_write_kv_cache(cache, k, k, geometry.hadamard_signs(128),
                                     torch.zeros(3, dtype=torch.int32), 128, 128)
+
+
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_impl_hadamard_helpers_match_the_matrix(hd):
+    """The impl's torch rotation helpers (the reference keeps them on its impl):
+    _fwht is the Sylvester-Hadamard product, _hadamard_forward is
+    H (s * q) / sqrt(d), and _hadamard_inverse undoes it."""
+    from scipy.linalg import hadamard
+
+    from turboquant_amd.geometry import hadamard_signs
+    from turboquant_amd.vllm_backend_fused import TurboQuantFusedImpl
+    impl = TurboQuantFusedImpl(8, hd, 1.0 / math.sqrt(hd), 2, None, None, "fp8")
+    g = torch.Generator().manual_seed(hd)
+    x = torch.randn(3, 5, hd, generator=g, dtype=torch.float64)
+    H = torch.from_numpy(hadamard(hd).astype("float64"))
+    assert torch.allclose(TurboQuantFusedImpl._fwht(x), x @ H.T, rtol=0, atol=1e-12)
+    s = hadamard_signs(hd).double()
+    q = torch.randn(4, 8, hd, generator=g).float()
+    got = impl._hadamard_forward(q)
+    want = ((q.double() * s) @ H.T / math.sqrt(hd)).float()
+    assert got.dtype == q.dtype and torch.allclose(got, want, rtol=0, atol=1e-5)
+    back = impl._hadamard_inverse(got)
+    assert torch.allclose(back, q, rtol=0, atol=1e-5)

@@ -50,9 +50,10 @@ def next_power_of_2(n: int) -> int:
 
 
 @torch.no_grad()
-def fwht(x: torch.Tensor) -> torch.Tensor:
-    """y = H x / sqrt(d) along the last dim (d a power of two); stride-1
-    butterflies first, each stage (a + b, a - b) on pairs (i, i + h)."""
+def fwht_unnormalized(x: torch.Tensor) -> torch.Tensor:
+    """y = H x along the last dim (d a power of two, H the Sylvester
+    Hadamard matrix of +-1 entries); stride-1 butterflies first, each stage
+    (a + b, a - b) on pairs (i, i + h)."""
     d = x.shape[-1]
     if d <= 0 or d & (d - 1):
         raise AssertionError(f"last dim must be a power of 2, got {d}")
@@ -64,7 +65,12 @@ def fwht(x: torch.Tensor) -> torch.Tensor:
         a, b = z[:, :, 0, :], z[:, :, 1, :]
         y = torch.stack((a + b, a - b), dim=2).view(-1, d)
         h *= 2
-    return (y * (1.0 / math.sqrt(d))).view(*lead, d)
+    return y.view(*lead, d)
+
+
+def fwht(x: torch.Tensor) -> torch.Tensor:
+    """y = H x / sqrt(d) along the last dim (d a power of two)."""
+    return fwht_unnormalized(x) * (1.0 / math.sqrt(x.shape[-1]))
 
 
 def _seeded_signs(n: int, seed: int) -> torch.Tensor:

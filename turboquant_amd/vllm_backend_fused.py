@@ -217,6 +217,27 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
             return
         self._signs = hadamard_signs(self._pd, device=dev)
 
+    # torch forms of the rotation the kernels apply (the reference keeps the
+    # same helpers on its impl, vllm_backend_fused.py:227-252; its forward
+    # does not call them either)
+    @staticmethod
+    def _fwht(x):
+        """Unnormalised Walsh-Hadamard transform along the last dim."""
+        from .algorithm import fwht_unnormalized
+        return fwht_unnormalized(x)
+
+    def _hadamard_forward(self, q):
+        """q' = H (s * q) / sqrt(pd), computed in fp32, returned in q's dtype."""
+        self._ensure(q.device)
+        x = self._fwht(q.float() * self._signs.to(q.device))
+        return (x * (1.0 / math.sqrt(x.shape[-1]))).to(q.dtype)
+
+    def _hadamard_inverse(self, out):
+        """o = s * (H o' / sqrt(pd)), the inverse of _hadamard_forward."""
+        self._ensure(out.device)
+        x = self._fwht(out.float()) * (1.0 / math.sqrt(out.shape[-1]))
+        return (x * self._signs.to(out.device)).to(out.dtype)
+
     def _ensure_kernels_loaded(self):
         if self._decode_op is None or self._write_op is None:
             from . import ops
