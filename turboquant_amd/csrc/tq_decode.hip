@@ -1406,6 +1406,36 @@ void decode_partials_kernel(DecodeParams p) {
 // 256/(PD/4) split groups each sum a strided subset of the splits for one
 // float4 column, a tree in LDS adds the groups, and wave 0 runs the inverse
 // FWHT across its 64 lanes.
+// The six cross-lane stages of a 64-lane Walsh-Hadamard transform (lane l
+// ends with sum_j (-1)^popcount(l & j) x_j): at each partner distance d the
+// lower lane keeps x + partner and the upper partner - x, the partner fetched
+// by DPP (d = 1, 2: quad permutes; 4: row shifts; 8: row rotate) or a lane
+// swap (d = 16, 32: the swap returns the lower and the upper lane's value).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float fwht_lanes(float x, int lane) {
+  float p = dpp_f<0xb1>(x);  // quad_perm [1, 0, 3, 2]
+  x = (lane & 1) ? p - x : x + p;
+  p = dpp_f<0x4e>(x);        // quad_perm [2, 3, 0, 1]
+  x = (lane & 2) ? p - x : x + p;
+  {
+    const float up = dpp_f<0x104>(x), dn = dpp_f<0x114>(x);  // row_shl:4, row_shr:4
+    p = (lane & 4) ? dn : up;
+  }
+  x = (lane & 4) ? p - x : x + p;
+  p = dpp_f<0x128>(x);       // row_ror:8
+  x = (lane & 8) ? p - x : x + p;
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = (lane & 16) ? __uint_as_float(r[0]) - __uint_as_float(r[1])
+                  : __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = (lane & 32) ? __uint_as_float(r[0]) - __uint_as_float(r[1])
+                  : __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  return x;
+}
+
 // four fp16 partial-row values as fp32
 __device__ __forceinline__ float4_t load_half4(const _Float16* src) {
   const half4_t h = *reinterpret_cast<const half4_t*>(src);
@@ -1518,12 +1548,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
             x[i + k + hh] = a - c;
           }
 #pragma unroll
-      for (int delta = 1; delta < 64; delta <<= 1)
-#pragma unroll
-        for (int i = 0; i < V; i++) {
-          const float partner = __shfl_xor(x[i], delta);
-          x[i] = (lane & delta) ? (partner - x[i]) : (x[i] + partner);
-        }
+      for (int i = 0; i < V; i++) x[i] = fwht_lanes(x[i], lane);
 #pragma unroll
       for (int i = 0; i < V; i++) x[i] = x[i] * inv_sqrt_pd * signs[lane * V + i];
     }
