@@ -180,3 +180,25 @@ def test_attention_quality_3bit():
     out = att(q, quant.dequantize(*quant.quantize(k)), quant.dequantize(*quant.quantize(v)))
     ref = att(q, k, v)
     assert ((out - ref).norm() / ref.norm()).item() < 0.30
+
+
+def test_reference_module_layout_imports():
+    """The reference's own tests import the algorithm from its submodules
+    (reference tests/test_algorithm.py:11-14, tests/eval_accuracy.py): the same
+    lines resolve to this build's objects, and the codebook tables hold the
+    reference's layout (2^b ascending levels, midpoint boundaries)."""
+    from turboquant.codebook import _BOUNDARIES_N01, _CENTROIDS_N01, Codebook
+    from turboquant.hadamard import RandomHadamardRotation, fwht, next_power_of_2
+    from turboquant.qjl import QJL
+    from turboquant.quantizer import TurboQuantMSE, TurboQuantProd, _pack_bits, _unpack_bits
+    assert (Codebook, QJL, TurboQuantMSE, TurboQuantProd, RandomHadamardRotation, fwht) == (
+        A.Codebook, A.QJL, A.TurboQuantMSE, A.TurboQuantProd, A.RandomHadamardRotation, A.fwht)
+    assert next_power_of_2(96) == 128 and next_power_of_2(1) == 1
+    idx = torch.randint(0, 8, (3, 40), dtype=torch.uint8)
+    assert torch.equal(_unpack_bits(_pack_bits(idx, 3), 3, 40), idx)
+    for b in (1, 2, 3, 4):
+        lv = np.array(_CENTROIDS_N01[b])
+        assert len(lv) == 2 ** b and np.all(np.diff(lv) > 0) and np.allclose(lv, -lv[::-1])
+        np.testing.assert_allclose(_BOUNDARIES_N01[b], (lv[1:] + lv[:-1]) / 2)
+    # the 4-bit table is the cache codebook (Lloyd-Max solution pinned elsewhere)
+    np.testing.assert_allclose(_CENTROIDS_N01[4][8:], A.CENTROIDS_N01[4])
