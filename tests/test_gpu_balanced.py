@@ -75,7 +75,7 @@ def test_uniform_lengths_closed_form_plan(b, length):
 
 
 @pytest.mark.parametrize("hq,hkv,hd", [(32, 8, 128), (16, 2, 128), (16, 16, 64), (16, 4, 256),
-                                       (16, 1, 128)])
+                                       (16, 1, 128), (16, 2, 256), (12, 2, 256)])
 def test_edge_lengths(hq, hkv, hd):
     """Lengths 0, 1, 15, 16, 17, 31, 32, 33 beside long ones, GQA 1..16."""
     lens = [0, 1, 15, 16, 17, 31, 32, 33, 5000, 0, 777]
