@@ -142,15 +142,62 @@ struct DecodeParams {
   float pv_scale;     // 1/(sqrt(pd) * kCbScale)
 };
 
+// Float max without NaN quieting: in IEEE mode fmaxf first canonicalizes
+// both operands (two more VALU instructions); the scores are never
+// signaling NaNs, so the plain instruction gives the same result.
+__device__ __forceinline__ float vmax(float a, float b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+#else
+  return fmaxf(a, b);
+#endif
+}
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+#else
+  return fmaxf(fmaxf(a, b), c);
+#endif
+}
+// max(x, x of lane l ror 8 within its row): one DPP max (the s_nop covers
+// the wait states of a DPP read after a VALU write of its source)
+__device__ __forceinline__ float max_ror8(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  float r;
+  asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0xf"
+      : "=v"(r)
+      : "v"(x));
+  return r;
+#else
+  return fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf,
+                                                          false)));
+#endif
+}
+// score * K norm, the norm an fp16 value in the low half of nr: one
+// v_fma_mix (fp16 operand, fp32 math; +0 addend, which only differs from
+// the product for a -0 score, and that feeds the same max and exp2)
+__device__ __forceinline__ float mul_lo_half(float sc, uint32_t nr) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(nr), "v"(sc));
+  return r;
+#else
+  return sc * (float)__builtin_bit_cast(_Float16, (uint16_t)(nr & 0xffffu));
+#endif
+}
 __device__ __forceinline__ float xor16_max(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor32_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor16_sum(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
@@ -426,28 +473,16 @@ __device__ __forceinline__ uint32_t lut_mad(uint32_t h, uint32_t lanec) {
   return a;
 }
 
-// Eight table reads in place (each address register receives its entry)
-// and one wait; inline assembly, so the compiler adds no conservative wait
-// for the copies in flight.
-__device__ __forceinline__ void lut_read8(uint32_t* a) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  asm volatile(
-      "ds_read_b32 %0, %0\n\t"
-      "ds_read_b32 %1, %1\n\t"
-      "ds_read_b32 %2, %2\n\t"
-      "ds_read_b32 %3, %3\n\t"
-      "ds_read_b32 %4, %4\n\t"
-      "ds_read_b32 %5, %5\n\t"
-      "ds_read_b32 %6, %6\n\t"
-      "ds_read_b32 %7, %7\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]),
-        "+v"(a[7])
-      :
-      : "memory");
-#else
-  (void)a;
-#endif
+// Eight table reads in place (each address register receives its entry):
+// plain LDS loads of the table.  The table is a different field of the
+// workgroup's LDS than the ring the direct-to-LDS copies write, so the
+// compiler neither waits for the copies in flight before these loads nor
+// orders them against the copies, and it interleaves them with the address
+// arithmetic and the MFMAs (partial lgkmcnt waits).
+__device__ __forceinline__ void lut_read8(uint32_t* a, const uint32_t* lut) {
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    a[i] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(lut) + a[i]);
 }
 
 // Scores of one tile, S[t = 4*q4 + r][h = l%16]: the K codes this lane
@@ -459,9 +494,10 @@ __device__ __forceinline__ void lut_read8(uint32_t* a) {
 // 8..15 (GQA ratio <= 8), one MFMA per K block, and the two halves are added
 // across lanes n and n+8 (both end up with the sum); otherwise qb/ql are
 // separate hi/lo operands, two MFMAs per K block.
-template <int PD, bool QC, int SH>
+template <int PD, bool QC, int SH, bool MERGE = true>
 __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_t* qb,
-                                                const half8_t* ql, uint32_t lanec) {
+                                                const half8_t* ql, uint32_t lanec,
+                                                const uint32_t* lut) {
   constexpr int KD = PD / 32;
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -476,7 +512,7 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
         x[4 * u + 2 * i] = lut_mad<SH, 0>(h, lanec);
         x[4 * u + 2 * i + 1] = lut_mad<SH, 1>(h, lanec);
       }
-    lut_read8(x);
+    lut_read8(x, lut);
 #pragma unroll
     for (int u = 0; u < 2; u++) {
       const half8_t kv8 = as_half8(x[4 * u], x[4 * u + 1], x[4 * u + 2], x[4 * u + 3]);
@@ -485,11 +521,40 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv8, ql[c + u], acc, 0, 0, 0);
     }
   }
-  if constexpr (QC) {
+  if constexpr (QC && MERGE) {
 #pragma unroll
     for (int r = 0; r < 4; r++) acc[r] = acc[r] + ror8(acc[r]);
   }
   return acc;
+}
+
+// PACK 2 scores of two tiles from their unmerged QC accumulators: lanes n < 8
+// of each row get tile 0's hi + lo sums (lane n + 8 holds the lo part), lanes
+// n >= 8 tile 1's (lane n - 8 holds the hi part): two DPP adds per value
+// whose bank masks write one half of each row each.  The leading s_nops
+// cover the wait states between the MFMAs that wrote a0 / a1 and their DPP
+// read (inline assembly, so the compiler does not count them).
+__device__ __forceinline__ float4_t pack_merge(float4_t a0, float4_t a1) {
+  float4_t d;
+#if defined(__HIP_DEVICE_COMPILE__)
+  float d0, d1, d2, d3;
+  asm volatile("s_nop 7\n\ts_nop 7\n\t"
+               "v_add_f32_dpp %0, %4, %4 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+               "v_add_f32_dpp %0, %8, %8 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+               "v_add_f32_dpp %1, %5, %5 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+               "v_add_f32_dpp %1, %9, %9 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+               "v_add_f32_dpp %2, %6, %6 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+               "v_add_f32_dpp %2, %10, %10 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+               "v_add_f32_dpp %3, %7, %7 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+               "v_add_f32_dpp %3, %11, %11 row_ror:8 row_mask:0xf bank_mask:0xc"
+               : "=&v"(d0), "=&v"(d1), "=&v"(d2), "=&v"(d3)
+               : "v"(a0[0]), "v"(a0[1]), "v"(a0[2]), "v"(a0[3]), "v"(a1[0]), "v"(a1[1]),
+                 "v"(a1[2]), "v"(a1[3]));
+  d = float4_t{d0, d1, d2, d3};
+#else
+  d = a0 + a1;
+#endif
+  return d;
 }
 
 // O[h][dim slot] += V^T P^T over the 32 tokens of one step with
@@ -506,7 +571,8 @@ __device__ __forceinline__ float4_t tile_scores(const uint32_t* kw, const half8_
 template <int PD, int SH>
 __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD / 128 : 1],
                                         const uint32_t (*v1)[(PD / 32) >= 4 ? PD / 128 : 1],
-                                        half8_t p, SoftmaxState<PD>& st, uint32_t lanec) {
+                                        half8_t p, SoftmaxState<PD>& st, uint32_t lanec,
+                                        const uint32_t* lut) {
   constexpr int VB = PD / 32;
   constexpr int VW = VB >= 4 ? VB / 4 : 1;
   // ix[T][pair][nibble][w]: pair 0 = tokens 0, 1; pair 1 = tokens 2, 3;
@@ -546,7 +612,7 @@ __device__ __forceinline__ void step_pv(const uint32_t (*v0)[(PD / 32) >= 4 ? PD
         for (int pr = 0; pr < 2; pr++)
           x[4 * nb + 2 * T + pr] = j % 2 ? lut_mad<SH, 1>(hs[nb][T][pr], lanec)
                                          : lut_mad<SH, 0>(hs[nb][T][pr], lanec);
-    lut_read8(x);
+    lut_read8(x, lut);
     const half8_t lo8 = as_half8(x[0], x[1], x[2], x[3]);
     const half8_t hi8 = as_half8(x[4], x[5], x[6], x[7]);
     st.O[2 * k + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo8, p, st.O[2 * k + 1], 0, 0, 0);
@@ -754,9 +820,9 @@ __device__ __forceinline__ void softmax_step(float* sc, const float* nk, const f
 #pragma unroll
     for (int r = 0; r < NV; r++) sc[r] = valid[r] ? sc[r] : -INFINITY;
   }
-  float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-  if constexpr (NV == 8) tmax = fmaxf(tmax, fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-  if (rot8) tmax = fmaxf(tmax, ror8(tmax));
+  float tmax = vmax(vmax3(sc[0], sc[1], sc[2]), sc[3]);
+  if constexpr (NV == 8) tmax = vmax3(tmax, vmax3(sc[4], sc[5], sc[6]), sc[7]);
+  if (rot8) tmax = max_ror8(tmax);
   tmax = xor16_max(tmax);
   tmax = xor32_max(tmax);
   const float m_new = fmaxf(st.m, tmax);
@@ -1269,10 +1335,13 @@ void decode_partials_kernel(DecodeParams p) {
       // scores of both tiles (scheduling barriers keep the two tiles'
       // dequant temporaries from being live at the same time)
       float4_t acc[2];
-      acc[0] = tile_scores<PD, QC, RG::SH>(d.k[0], qb, ql, lanec);
+      constexpr bool PM = PACK == 2;  // packed merge of the two tiles' unmerged sums
+      static_assert(PACK == 1 || QC, "two tiles per score set need the hi / lo columns");
+      acc[0] = tile_scores<PD, QC, RG::SH, !PM>(d.k[0], qb, ql, lanec, sm.klut);
       __builtin_amdgcn_sched_barrier(0);
-      acc[1] = tile_scores<PD, QC, RG::SH>(d.k[1], qb, ql, lanec);
+      acc[1] = tile_scores<PD, QC, RG::SH, !PM>(d.k[1], qb, ql, lanec, sm.klut);
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (PM) acc[0] = pack_merge(acc[0], acc[1]);
       constexpr int NV = 4 * (2 / PACK);  // score values per lane
       float sc[NV], nk[NV], nv[NV];
       bool valid[NV];
@@ -1288,9 +1357,14 @@ void decode_partials_kernel(DecodeParams p) {
           if constexpr (PACK == 2) {
             // tile 0's scores in lanes 0..7 of each row, tile 1's in 8..15
             // (with QC both halves of a row hold the same sums)
-            sc[r] = n < 8 ? acc[0][r] : acc[1][r];
+            sc[r] = PM ? acc[0][r] : (n < 8 ? acc[0][r] : acc[1][r]);
           } else {
             sc[4 * g + r] = acc[g][r];
+          }
+          {
+            // the K norm multiplies here, straight from its fp16 half
+            sc[4 * g + r] = mul_lo_half(sc[4 * g + r], nr[r]);
+            nk[4 * g + r] = 1.0f;
           }
         }
       }
@@ -1314,7 +1388,7 @@ void decode_partials_kernel(DecodeParams p) {
       } else {
         p8 = half8_t{pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
       }
-      step_pv<PD, RG::SH>(d.v[0], d.v[1], p8, st, lanec);
+      step_pv<PD, RG::SH>(d.v[0], d.v[1], p8, st, lanec, sm.klut);
     };
 
     // one step: tiles 2k, 2k + 1 in ring slots s0, s1
