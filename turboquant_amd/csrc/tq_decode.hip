@@ -802,20 +802,35 @@ __device__ __forceinline__ void read_step(const uint32_t* ka, uint32_t va, uint3
 #endif
 }
 
+// fp16 pair (a * V norm of na, b * V norm of nb), the norms fp16 values in
+// the high halves of na / nb: v_fma_mixlo writes the low half, v_fma_mixhi
+// the high half (fp32 product, one rounding to fp16 each)
+__device__ __forceinline__ uint32_t mix_pair(float a, uint32_t na, float b, uint32_t nb) {
+  uint32_t r;
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %0, %3, %4, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+      : "=&v"(r)
+      : "v"(a), "v"(na), "v"(b), "v"(nb));
+#else
+  r = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(a * hi_half(na))) |
+      ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(b * hi_half(nb))) << 16);
+#endif
+  return r;
+}
+
 // Online softmax over the NV score values this lane holds for one step
 // (PACK 2: 4 values, tile (l%16)/8, head l%8; PACK 1: 8 values, tile 0 then
-// tile 1, head l%16; tokens 4*q4 + r).  nk / nv: the tokens' K and V norms.
-// valid: token masks, `full` when all are valid.  Writes p * nv (fp16) to
-// pv; the running max only moves when the step exceeds it by more than 2^3,
-// so p <= 8.
+// tile 1, head l%16; tokens 4*q4 + r), already scaled by the K norms.  nvr:
+// the tokens' V norms (fp16, high halves).  valid: token masks, `full` when
+// all are valid (uniform); hmask: the lanes of real heads (head < ratio).
+// Writes p * nv as fp16 pairs to pw; the running
+// max only moves when the step exceeds it by more than 2^3, so p <= 8.
 template <int PD, int NV>
-__device__ __forceinline__ void softmax_step(float* sc, const float* nk, const float* nv,
-                                             bool full, const bool* valid, bool rot8, int head,
-                                             int ratio, float lpv, SoftmaxState<PD>& st,
-                                             _Float16* pv) {
+__device__ __forceinline__ void softmax_step(float* sc, const uint32_t* nvr, bool full,
+                                             const bool* valid, bool rot8, uint64_t hmask,
+                                             float lpv, SoftmaxState<PD>& st, uint32_t* pw) {
   constexpr int NO = PD / 16;
-#pragma unroll
-  for (int r = 0; r < NV; r++) sc[r] = sc[r] * nk[r];
   if (!full) {
 #pragma unroll
     for (int r = 0; r < NV; r++) sc[r] = valid[r] ? sc[r] : -INFINITY;
@@ -825,9 +840,9 @@ __device__ __forceinline__ void softmax_step(float* sc, const float* nk, const f
   if (rot8) tmax = max_ror8(tmax);
   tmax = xor16_max(tmax);
   tmax = xor32_max(tmax);
-  const float m_new = fmaxf(st.m, tmax);
-  const bool need = (head < ratio) && (m_new > st.m + 3.0f);
-  if (__any(need)) {
+  const float m_new = vmax(st.m, tmax);
+  // lanes of padding heads (head >= ratio) never move the max
+  if ((__builtin_amdgcn_ballot_w64(m_new > st.m + 3.0f) & hmask) != 0) {
     const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(st.m - m_new);
 #pragma unroll
     for (int i = 0; i < NO; i++) st.O[i] *= alpha;
@@ -838,28 +853,34 @@ __device__ __forceinline__ void softmax_step(float* sc, const float* nk, const f
   float pr[NV];
 #pragma unroll
   for (int r = 0; r < NV; r++) pr[r] = __builtin_amdgcn_exp2f(sc[r] - st.mb);
-  if (!full) {
+  float ls;
+  if (full) {
+    ls = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    if constexpr (NV == 8) ls += (pr[4] + pr[5]) + (pr[6] + pr[7]);
+#pragma unroll
+    for (int r = 0; r < NV; r += 2) pw[r / 2] = mix_pair(pr[r], nvr[r], pr[r + 1], nvr[r + 1]);
+  } else {
+    // masked entries: p = 0, and their norm bits may be anything (0 * inf
+    // is NaN), so their products are zeroed too
 #pragma unroll
     for (int r = 0; r < NV; r++) pr[r] = valid[r] ? pr[r] : 0.0f;
-  }
-  float ls = (pr[0] + pr[1]) + (pr[2] + pr[3]);
-  if constexpr (NV == 8) ls += (pr[4] + pr[5]) + (pr[6] + pr[7]);
-  st.lsum += ls;
+    ls = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    if constexpr (NV == 8) ls += (pr[4] + pr[5]) + (pr[6] + pr[7]);
 #pragma unroll
-  for (int r = 0; r < NV; r++) {
-    float x = pr[r] * nv[r];
-    if (!full) x = valid[r] ? x : 0.0f;  // masked entries may hold any bits
-    pv[r] = (_Float16)x;
+    for (int r = 0; r < NV; r += 2) {
+      const float x0 = valid[r] ? pr[r] * hi_half(nvr[r]) : 0.0f;
+      const float x1 = valid[r + 1] ? pr[r + 1] * hi_half(nvr[r + 1]) : 0.0f;
+      pw[r / 2] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x0) |
+                  ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16);
+    }
   }
+  st.lsum += ls;
 }
 
 // Bring tile 1's packed probabilities (lanes 8..15 of each row) to lanes
 // 0..7 (DPP row_shl:8), the B-operand position of the PV MFMA.
-__device__ __forceinline__ half4_t shl8(half4_t v) {
-  u32x2 u = __builtin_bit_cast(u32x2, v);
-  u[0] = (uint32_t)__builtin_amdgcn_mov_dpp((int)u[0], 0x108, 0xf, 0xf, false);
-  u[1] = (uint32_t)__builtin_amdgcn_mov_dpp((int)u[1], 0x108, 0xf, 0xf, false);
-  return __builtin_bit_cast(half4_t, u);
+__device__ __forceinline__ uint32_t shl8(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x108, 0xf, 0xf, false);
 }
 
 // Split-KV partials.  Workgroup = (sequence b, split s, group hg of G kv
@@ -1178,6 +1199,7 @@ void decode_partials_kernel(DecodeParams p) {
     const int slotw = 16 / PACK;   // lanes per packed tile
     const int ptile = n / slotw;   // tile of this lane's packed scores
     const int head = n % slotw;    // head of this lane's packed scores
+    const uint64_t hmask = __builtin_amdgcn_ballot_w64(head < ratio);  // lanes of real heads
     const uint32_t oN = (4 * q4 + (lane & 3)) * ROWB + (hb + PD / 32) * 16;
 
     // the q' scratch lives where the dequant table goes (the table is built
@@ -1343,7 +1365,8 @@ void decode_partials_kernel(DecodeParams p) {
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (PM) acc[0] = pack_merge(acc[0], acc[1]);
       constexpr int NV = 4 * (2 / PACK);  // score values per lane
-      float sc[NV], nk[NV], nv[NV];
+      float sc[NV];
+      uint32_t nvr[NV];
       bool valid[NV];
 #pragma unroll
       for (int g = 0; g < 2 / PACK; g++) {
@@ -1352,24 +1375,18 @@ void decode_partials_kernel(DecodeParams p) {
                                 quad_bcast<3>(nkv)};
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          nk[4 * g + r] = lo_half(nr[r]);
-          nv[4 * g + r] = hi_half(nr[r]);
-          if constexpr (PACK == 2) {
-            // tile 0's scores in lanes 0..7 of each row, tile 1's in 8..15
-            // (with QC both halves of a row hold the same sums)
-            sc[r] = PM ? acc[0][r] : (n < 8 ? acc[0][r] : acc[1][r]);
-          } else {
-            sc[4 * g + r] = acc[g][r];
-          }
-          {
-            // the K norm multiplies here, straight from its fp16 half
-            sc[4 * g + r] = mul_lo_half(sc[4 * g + r], nr[r]);
-            nk[4 * g + r] = 1.0f;
-          }
+          // tile 0's scores in lanes 0..7 of each row and tile 1's in 8..15
+          // (PACK 2), times the K norm straight from its fp16 half
+          const float a = PACK == 2 ? acc[0][r] : acc[g][r];
+          sc[4 * g + r] = mul_lo_half(a, nr[r]);
+          nvr[4 * g + r] = nr[r];
         }
       }
       const int t_first = 2 * k * kTile;  // first token of this step
-      const bool full = okT[0] && okT[1] && t_first >= c0 && t_first + 2 * kTile <= c1;
+      // (uniform; read back as a scalar so that it stays one)
+      const bool full = __builtin_amdgcn_readfirstlane(
+                            (okT[0] && okT[1] && t_first >= c0 && t_first + 2 * kTile <= c1)
+                                ? 1 : 0) != 0;
       if (!full) {
 #pragma unroll
         for (int i = 0; i < NV; i++) {
@@ -1378,15 +1395,13 @@ void decode_partials_kernel(DecodeParams p) {
           valid[i] = okT[T] && t >= c0 && t < c1;
         }
       }
-      _Float16 pv[NV];
-      softmax_step<PD, NV>(sc, nk, nv, full, valid, PACK == 2, head, ratio, lpv, st, pv);
+      uint32_t pw[NV / 2];
+      softmax_step<PD, NV>(sc, nvr, full, valid, PACK == 2, hmask, lpv, st, pw);
       half8_t p8;
       if constexpr (PACK == 2) {
-        half4_t p4 = {pv[0], pv[1], pv[2], pv[3]};
-        const half4_t p4b = shl8(p4);
-        p8 = half8_t{p4[0], p4[1], p4[2], p4[3], p4b[0], p4b[1], p4b[2], p4b[3]};
+        p8 = as_half8(pw[0], pw[1], shl8(pw[0]), shl8(pw[1]));
       } else {
-        p8 = half8_t{pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
+        p8 = as_half8(pw[0], pw[1], pw[2], pw[3]);
       }
       step_pv<PD, RG::SH>(d.v[0], d.v[1], p8, st, lanec, sm.klut);
     };
