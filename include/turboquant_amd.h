@@ -218,6 +218,28 @@ int tq_dequant_paged(const uint8_t* k_slab, const uint8_t* v_slab,
                      tq_stream_t stream);
 
 /*
+ * Causal GQA attention of a prefill chunk over fp16 K/V (head_dim 128):
+ * o[i, h] = softmax_j(q[i, h] . k[j, h / r] * sm_scale) v[j, h / r] over keys
+ * j <= (kv_len - q_len) + i, r = num_qo_heads / num_kv_heads.  q, o: fp16
+ * element (i, h, d) at base + i*stride_tok + h*stride_head + d; k, v: fp16
+ * element (j, g, d) likewise.  Strides are multiples of 8 elements, bases
+ * 16-byte aligned, 0 <= q_len <= kv_len.
+ *
+ * Replaces the flash-attn call of the reference's prefill
+ * (flash_attn_varlen_func in TurboQuantFusedImpl.forward,
+ * turboquant/vllm_backend_fused.py:335-371, which attends a chunk's fresh
+ * K/V); the backend here calls it per request with the chunk's cached
+ * context (tq_dequant_paged) in front of its fresh K/V.
+ */
+int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                         const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                         const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                         void* o, int64_t o_stride_tok, int64_t o_stride_head,
+                         int32_t q_len, int32_t kv_len, int32_t num_qo_heads,
+                         int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                         tq_stream_t stream);
+
+/*
  * Diagnostic, no counterpart in the reference: tq_decode_partials at head
  * size 128 with 8 kv heads per workgroup (the configs[2] geometry) with the
  * attention math compiled out -- the same page walk, LDS copy ring, waits,

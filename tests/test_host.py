@@ -140,6 +140,16 @@ def test_cabi_argument_errors_without_gpu():
     assert rc == -22 and lib.tq_last_error()
     rc = lib.tq_combine_splits(null, null, 1, 0, 32, 128, null, null, null)
     assert rc == -22
+    # prefill attention: head size 128 only, GQA ratio must divide, q_len <= kv_len
+    rc = lib.tq_prefill_attention(null, 0, 0, null, 0, 0, null, 0, 0, null, 0, 0, 4, 4, 32, 8,
+                                  64, 0.1, null)
+    assert rc == -22 and b"head_dim" in lib.tq_last_error()
+    rc = lib.tq_prefill_attention(null, 0, 0, null, 0, 0, null, 0, 0, null, 0, 0, 4, 4, 30, 8,
+                                  128, 0.1, null)
+    assert rc == -22 and b"multiple" in lib.tq_last_error()
+    rc = lib.tq_prefill_attention(null, 0, 0, null, 0, 0, null, 0, 0, null, 0, 0, 5, 4, 32, 8,
+                                  128, 0.1, null)
+    assert rc == -22 and b"q_len" in lib.tq_last_error()
     # an empty batch is a no-op that succeeds
     assert lib.tq_combine_splits(null, null, 0, 1, 32, 128, null, null, null) == 0
 

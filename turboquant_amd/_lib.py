@@ -42,10 +42,12 @@ SIGNATURES = {
     "tq_combine_splits": (_I32, [_P, _P, _I32, _I32, _I32, _I32, _P, _P, _P]),
     "tq_dequant_paged": (_I32, [_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I64, _P, _P,
                                 _P, _I64, _P]),
+    "tq_prefill_attention": (_I32, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64,
+                                    _I64, _I32, _I32, _I32, _I32, _I32, _F32, _P]),
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_abi_version": (_I32, []),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 

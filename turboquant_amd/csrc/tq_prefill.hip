@@ -1,0 +1,365 @@
+// tq_prefill.hip -- causal GQA flash attention of a prefill chunk (fp16 K/V).
+//
+// Semantics: o[i, h] = softmax_j(q[i, h] . k[j, h / ratio] * sm_scale) v[j, h / ratio]
+// over keys j <= (Lk - Lq) + i (causal, aligned to the end of the keys: a
+// chunk of Lq new tokens whose keys are the Lk - Lq earlier tokens of its
+// sequence followed by its own).  This is the attention the backend's prefill
+// path needs (reference turboquant/vllm_backend_fused.py:335-371 runs it over
+// the fresh chunk only, in flash-attn; TurboQuantFusedImpl here prepends the
+// cached context read back from the quantized cache).
+//
+// gfx950 design:
+//  * One workgroup = 128 query rows of one q head (4 waves x 32 rows); grid
+//    (q heads, query blocks): the longest (last) query blocks are dispatched
+//    first, and the q heads of one kv head are neighbours (their K/V tiles
+//    are shared in L2).
+//  * Scores are computed transposed, S^T = K Q^T, with
+//    v_mfma_f32_32x32x16_f16 (A = K rows from LDS, B = q columns held in
+//    registers for the whole kernel): the C layout then gives each lane one
+//    query row (lane % 32) and 16 key rows per 32-key block, so the softmax
+//    max and sum are in-lane plus one permlane32 swap, and the lane's
+//    probabilities are, in order, the B operand of O^T = V^T P^T (the MFMA's
+//    reduction order is the C layout's row order; V^T is read in the same
+//    order).  O^T's C layout again gives each lane its own query row, so the
+//    online-softmax rescale is a per-lane scalar.
+//  * K tiles (64 keys) stream into LDS with direct-to-LDS 16-byte copies whose
+//    16-byte chunks are XOR-swizzled by row (conflict-free A reads); V tiles
+//    are loaded into registers one tile ahead and written transposed
+//    ([dim][key], padded rows) with v_perm_b32 and 8-byte LDS stores.  Two
+//    buffers of each (distinct LDS arrays, so the compiler does not wait for
+//    the copies in flight into the other buffer), one barrier per tile.
+//  * Online softmax in the exp2 domain with a lazy rescale (the running max
+//    moves only when a tile exceeds it by more than 8 / scale); probabilities
+//    enter the PV MFMA as fp16 (round to nearest), accumulation is fp32.
+#include "tq_common.h"
+
+namespace tq {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// two floats as an fp16 pair, round to nearest even (one v_cvt_pk_f16_f32)
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, half2_t));
+}
+
+constexpr int kD = 128;      // head size
+constexpr int kBM = 128;     // query rows per workgroup (4 waves x 32)
+constexpr int kBN = 64;      // keys per tile
+constexpr int kKRow = kD * 2;        // bytes of one K row in LDS (16 chunks of 16 B)
+constexpr int kVtRow = kBN * 2 + 8;  // bytes of one V^T row (64 keys + 4 pad halves)
+
+struct PrefillParams {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* v;
+  _Float16* o;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;  // strides in elements
+  int lq, lk, ratio, nqb;
+  float c;  // sm_scale * log2(e)
+};
+
+// max / sum of x over lanes l and l ^ 32: v_permlane32_swap of x with
+// itself returns (x, x of lane l ^ 32) in some order in every lane
+__device__ __forceinline__ float max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t kbuf0[kBN * kKRow];
+  __shared__ __attribute__((aligned(16))) uint8_t kbuf1[kBN * kKRow];
+  __shared__ __attribute__((aligned(16))) uint8_t vt0[kD * kVtRow];
+  __shared__ __attribute__((aligned(16))) uint8_t vt1[kD * kVtRow];
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int hh = lane >> 5, n = lane & 31;
+  const int qb = p.nqb - 1 - (int)blockIdx.y;
+  const int head = blockIdx.x, g = head / p.ratio;
+  const int q0 = qb * kBM;
+  const int off = p.lk - p.lq;
+  const int qrow = q0 + 32 * w + n;  // this lane's query row
+  const int kend = min(p.lk, off + min(q0 + kBM, p.lq));  // keys any row here sees
+  const int ntiles = (kend + kBN - 1) / kBN;
+
+  // q^T as the B operand of S^T = K Q^T: k-step s covers dims 16s .. 16s+15,
+  // lane (hh, n) holds dims 16s + 8hh .. +7 of query row qrow
+  half8_t qB[kD / 16];
+  {
+    const _Float16* qp = p.q + (int64_t)qrow * p.q_st + (int64_t)head * p.q_sh + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < kD / 16; s++) {
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (qrow < p.lq) x = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+      qB[s] = __builtin_bit_cast(half8_t, x);
+    }
+  }
+
+  // K copies: copy j (0..15) fills LDS bytes [1024 j, 1024 j + 1024) of a
+  // buffer = rows 4j .. 4j+3; lane l writes row 4j + l/16, physical chunk
+  // l%16, which holds logical chunk (l%16) ^ (row%16) of that key row.
+  const int kst_b = (int)(p.k_st * 2);
+  uint32_t koff[4];  // per-lane byte offsets of the four copies inside a tile
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int j = w + 4 * i, row = 4 * j + (lane >> 4);
+    koff[i] = (uint32_t)(row * kst_b + (((lane & 15) ^ (row & 15)) * 16));
+  }
+  // buffer resource over rows [kb, Lk) of a K or V tile (wave-uniform base
+  // and size; rows past Lk read as zeros)
+  auto tile_rsrc = [&](const _Float16* base, int64_t st, int kb) {
+    const int rows = min(kBN, p.lk - kb);
+    const uint64_t a = (uint64_t)(uintptr_t)(base + (int64_t)kb * st);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    const int nrec = __builtin_amdgcn_readfirstlane(rows * (int)(st * 2));
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)(((uint64_t)hi << 32) | lo),
+                                             (short)0, nrec, 0x00020000);
+  };
+  const _Float16* const kbase = p.k + (int64_t)g * p.k_sh;
+  const _Float16* const vbase = p.v + (int64_t)g * p.v_sh;
+  auto issue_k = [&](int kt, uint8_t* buf) {
+    const __amdgpu_buffer_rsrc_t r = tile_rsrc(kbase, p.k_st, kt * kBN);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (void*)(buf + 1024 * (w + 4 * i)), 16, koff[i],
+                                               0, 0, 0);
+  };
+  // V: thread (w, lane) loads keys 4a .. 4a+3 (a = lane/4) x dims 8b .. 8b+7
+  // (b = 4w + lane%4) of a tile, then writes them transposed
+  const int va = lane >> 2, vb = 4 * w + (lane & 3);
+  const int vst_b = (int)(p.v_st * 2);
+  u32x4 vr[4];
+  auto load_v = [&](int kt) {
+    const __amdgpu_buffer_rsrc_t r = tile_rsrc(vbase, p.v_st, kt * kBN);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            r, (uint32_t)((4 * va + i) * vst_b + 16 * vb), 0, 0));
+  };
+  auto store_vt = [&](uint8_t* vt) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {  // dims 8vb + 2e, 8vb + 2e + 1
+      const uint32_t lo01 = __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x05040100u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(vr[3][e], vr[2][e], 0x05040100u);
+      const uint32_t hi01 = __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x07060302u);
+      const uint32_t hi23 = __builtin_amdgcn_perm(vr[3][e], vr[2][e], 0x07060302u);
+      uint8_t* d = vt + (8 * vb + 2 * e) * kVtRow + 8 * va;
+      *reinterpret_cast<u32x2*>(d) = u32x2{lo01, lo23};
+      *reinterpret_cast<u32x2*>(d + kVtRow) = u32x2{hi01, hi23};
+    }
+  };
+
+  f32x16 oacc[kD / 32];
+#pragma unroll
+  for (int d = 0; d < kD / 32; d++)
+#pragma unroll
+    for (int j = 0; j < 16; j++) oacc[d][j] = 0.0f;
+  float m = -INFINITY, mc = -INFINITY, lsum = 0.0f;
+  const int qlim = off + qrow;  // last key of this lane's row
+
+  auto tile = [&](int kt, const uint8_t* kbuf, const uint8_t* vt) {
+    const int kb = kt * kBN;
+    // the wave's rows are q0 + 32w .. +31: nothing to do when all its keys
+    // in this tile are beyond every row (uniform)
+    if (kb > off + q0 + 32 * w + 31) return;
+    f32x16 sacc[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int row = 32 * u + n;
+      f32x16 acc;
+#pragma unroll
+      for (int j = 0; j < 16; j++) acc[j] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kD / 16; s++) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(
+            kbuf + row * kKRow + (((2 * s + hh) ^ (row & 15)) * 16));
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), qB[s], acc,
+                                                     0, 0, 0);
+      }
+      sacc[u] = acc;
+    }
+    // mask keys beyond the row (causal) or beyond Lk (uniform test)
+    if (kb + kBN - 1 > off + q0 + 32 * w || kb + kBN > p.lk) {
+#pragma unroll
+      for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          const int key = kb + 32 * u + 8 * (j >> 2) + 4 * hh + (j & 3);
+          if (key > qlim || key >= p.lk) sacc[u][j] = -INFINITY;
+        }
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+      for (int j = 0; j < 16; j++) tmax = fmaxf(tmax, sacc[u][j]);
+    tmax = max32(tmax);
+    const float m_new = fmaxf(m, tmax);
+    // lazy rescale: p = exp2((s - m) c) stays below 2^8 between rescales
+    if (__builtin_amdgcn_ballot_w64(m_new * p.c > mc + 8.0f) != 0) {
+      const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - m_new * p.c);
+#pragma unroll
+      for (int d = 0; d < kD / 32; d++) oacc[d] *= alpha;
+      lsum *= alpha;
+      m = m_new;
+      mc = m_new * p.c;
+    }
+    half8_t pB[4];  // B operand of O^T = V^T P^T for k-steps (u, t)
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        float pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[u][8 * t + i], p.c, -mc));
+          lsum += pr[i];
+        }
+        u32x4 pk;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          pk[i] = pack_h2(pr[2 * i], pr[2 * i + 1]);
+        pB[2 * u + t] = __builtin_bit_cast(half8_t, pk);
+      }
+    // O^T += V^T P^T: k-step (u, t) reduces keys 32u + 16t + {4hh + 0..3,
+    // 8 + 4hh + 0..3} (the C-layout rows of the lane's probabilities)
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+      const int key0 = 16 * st + 4 * hh;
+#pragma unroll
+      for (int d = 0; d < kD / 32; d++) {
+        const uint8_t* vr0 = vt + (32 * d + n) * kVtRow + 2 * key0;
+        const u32x2 a0 = *reinterpret_cast<const u32x2*>(vr0);
+        const u32x2 a1 = *reinterpret_cast<const u32x2*>(vr0 + 16);
+        const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
+        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), pB[st],
+                                                         oacc[d], 0, 0, 0);
+      }
+    }
+  };
+
+  if (ntiles > 0) {
+    issue_k(0, kbuf0);
+    load_v(0);
+  }
+  for (int kt = 0; kt < ntiles; kt += 2) {
+    // tile kt: buffers 0
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): copies and loads of tile kt
+    store_vt(vt0);
+    __syncthreads();
+    if (kt + 1 < ntiles) {
+      issue_k(kt + 1, kbuf1);
+      load_v(kt + 1);
+    }
+    tile(kt, kbuf0, vt0);
+    if (kt + 1 >= ntiles) break;
+    // tile kt + 1: buffers 1
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    store_vt(vt1);
+    __syncthreads();
+    if (kt + 2 < ntiles) {
+      issue_k(kt + 2, kbuf0);
+      load_v(kt + 2);
+    }
+    tile(kt + 1, kbuf1, vt1);
+  }
+
+  // o = O / sum, lane (hh, n) holds dims 32d + 8jq + 4hh + 0..3 of row qrow
+  lsum = sum32(lsum);
+  if (qrow < p.lq) {
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    _Float16* op = p.o + (int64_t)qrow * p.o_st + (int64_t)head * p.o_sh + 4 * hh;
+#pragma unroll
+    for (int d = 0; d < kD / 32; d++)
+#pragma unroll
+      for (int jq = 0; jq < 4; jq++) {
+        const uint32_t lo = pack_h2(oacc[d][4 * jq] * inv, oacc[d][4 * jq + 1] * inv);
+        const uint32_t hi = pack_h2(oacc[d][4 * jq + 2] * inv, oacc[d][4 * jq + 3] * inv);
+        *reinterpret_cast<u32x2*>(op + 32 * d + 8 * jq) = u32x2{lo, hi};
+      }
+  }
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                    const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                                    const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                                    void* o, int64_t o_stride_tok, int64_t o_stride_head,
+                                    int32_t q_len, int32_t kv_len, int32_t num_qo_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                                    tq_stream_t stream) {
+  using namespace tq;
+  if (head_dim != kD) {
+    set_error("prefill_attention: head_dim %d unsupported (128 only)", head_dim);
+    return kEinval;
+  }
+  if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads != 0) {
+    set_error("prefill_attention: num_qo_heads %d not a multiple of num_kv_heads %d",
+              num_qo_heads, num_kv_heads);
+    return kEinval;
+  }
+  if (q_len < 0 || kv_len < q_len) {
+    set_error("prefill_attention: need 0 <= q_len (%d) <= kv_len (%d)", q_len, kv_len);
+    return kEinval;
+  }
+  if (!q || !k || !v || !o) {
+    set_error("prefill_attention: null pointer");
+    return kEinval;
+  }
+  const int64_t strides[8] = {q_stride_tok, q_stride_head, k_stride_tok, k_stride_head,
+                              v_stride_tok, v_stride_head, o_stride_tok, o_stride_head};
+  for (int i = 0; i < 8; i++) {
+    if (strides[i] < 0 || strides[i] % 8 != 0) {
+      set_error("prefill_attention: strides must be non-negative multiples of 8 elements");
+      return kEinval;
+    }
+  }
+  if (k_stride_tok < kD || v_stride_tok < kD ||
+      (k_stride_tok > v_stride_tok ? k_stride_tok : v_stride_tok) * 2 * (int64_t)kBN > INT32_MAX) {
+    set_error("prefill_attention: k / v token strides out of range");
+    return kEinval;
+  }
+  const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o;
+  if (al & 15) {
+    set_error("prefill_attention: tensors must be 16-byte aligned");
+    return kEinval;
+  }
+  if (q_len == 0) return 0;
+  PrefillParams p;
+  p.q = static_cast<const _Float16*>(q);
+  p.k = static_cast<const _Float16*>(k);
+  p.v = static_cast<const _Float16*>(v);
+  p.o = static_cast<_Float16*>(o);
+  p.q_st = q_stride_tok;
+  p.q_sh = q_stride_head;
+  p.k_st = k_stride_tok;
+  p.k_sh = k_stride_head;
+  p.v_st = v_stride_tok;
+  p.v_sh = v_stride_head;
+  p.o_st = o_stride_tok;
+  p.o_sh = o_stride_head;
+  p.lq = q_len;
+  p.lk = kv_len;
+  p.ratio = num_qo_heads / num_kv_heads;
+  p.nqb = (q_len + kBM - 1) / kBM;
+  p.c = sm_scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(prefill_kernel, dim3(num_qo_heads, p.nqb), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), p);
+  return (int)hipGetLastError();
+}

@@ -210,6 +210,31 @@ def decode_paged_balanced(q: torch.Tensor, kv_cache: torch.Tensor, indices: torc
     return o
 
 
+def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                      sm_scale: float) -> torch.Tensor:
+    """Causal GQA attention of q [Lq, Hq, 128] over k, v [Lk, Hkv, 128] (fp16,
+    Lq <= Lk), the queries aligned to the end of the keys (query i sees keys
+    <= Lk - Lq + i), written into o [Lq, Hq, 128] fp16.  Heads and dims of
+    every tensor contiguous; token strides free (multiples of 8)."""
+    _require_gpu(q, k, v, o)
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (o, "o")):
+        if t.dtype != torch.float16 or t.dim() != 3 or t.stride(2) != 1:
+            raise RuntimeError(f"{name} must be fp16 [tokens, heads, head_dim] with contiguous dims")
+    lq, hq, d = q.shape
+    lk, hkv, dk = k.shape
+    if tuple(v.shape) != (lk, hkv, dk) or dk != d or tuple(o.shape) != (lq, hq, d):
+        raise RuntimeError("prefill_attention: q/k/v/o shapes disagree")
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = lib.tq_prefill_attention(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                                      k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
+                                      v.stride(1), o.data_ptr(), o.stride(0), o.stride(1),
+                                      int(lq), int(lk), int(hq), int(hkv), int(d),
+                                      float(sm_scale), _stream_ptr(q.device))
+    _lib.check(rc, "prefill_attention")
+    return o
+
+
 def dequant_paged(kv_cache: torch.Tensor, pages: torch.Tensor, num_tokens: int,
                   num_kv_heads: int, head_dim: int, padded_dim: int,
                   signs: torch.Tensor | None, out_k: torch.Tensor, out_v: torch.Tensor) -> None:

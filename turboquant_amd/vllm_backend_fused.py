@@ -286,10 +286,17 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
         both = torch.cat([dq.to(torch.int64), attn_metadata.seq_lens.to(torch.int64)]).cpu()
         return both[:n].tolist(), both[n:].tolist()
 
-    def _attend(self, q, k, v, ctx):
+    def _attend(self, q, k, v, ctx, out=None):
         """q [ql, Hq, D] over k, v [ctx + ql, Hkv, D] (fp16), causal with the
-        queries at the end of the keys (lower-right alignment): the fused
-        flash kernel with grouped heads, no expanded K/V, no dense mask."""
+        queries at the end of the keys (lower-right alignment).  Head size
+        128: this library's prefill kernel (tq_prefill_attention), written
+        into `out` when given (fp16 [ql, Hq, D]); other head sizes: torch's
+        fused flash kernel with grouped heads (no expanded K/V, no mask)."""
+        if self.head_size == 128:
+            from . import ops
+            if out is None or out.dtype != torch.float16:
+                out = torch.empty(q.shape, dtype=torch.float16, device=q.device)
+            return ops.prefill_attention(q, k, v, out, self.scale)
         from torch.nn.attention.bias import causal_lower_right
         qt = q.transpose(0, 1).unsqueeze(0)
         kt = k.transpose(0, 1).unsqueeze(0)
@@ -310,9 +317,11 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
             a, b = qsl[i], qsl[i + 1]
             if b <= a:
                 continue
+            dst = output[a:b]
             o = self._attend(query[a:b].to(torch.float16), key[a:b].to(torch.float16),
-                             value[a:b].to(torch.float16), 0)
-            output[a:b] = o.to(output.dtype)
+                             value[a:b].to(torch.float16), 0, dst)
+            if o.data_ptr() != dst.data_ptr():
+                dst.copy_(o)
         return output
 
     def _decode_ws(self, n, pages, device):
@@ -350,7 +359,8 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
           reference attends the fresh chunk only and so drops the cached
           context; its decode path already attends over the dequantized
           cache, which this extends to chunks.
-        Attention runs in torch's fused flash kernel with grouped kv heads.
+        Attention runs in this library's prefill kernel (head size 128) or
+        torch's fused flash kernel with grouped kv heads (other sizes).
         """
         from . import ops
         self._ensure_kernels_loaded()
@@ -382,7 +392,10 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
                                   self._pd, self._signs, kk, vv)
                 kk[ctx:] = key[a:b]
                 vv[ctx:] = value[a:b]
-            output[a:b] = self._attend(q, kk, vv, ctx).to(output.dtype)
+            dst = output[a:b]
+            o = self._attend(q, kk, vv, ctx, dst)
+            if o.data_ptr() != dst.data_ptr():
+                dst.copy_(o)
         if dec:
             dev = query.device
             rows = torch.tensor([qsl[i] for i in dec], dtype=torch.long, device=dev)
