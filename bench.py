@@ -12,7 +12,9 @@ L ~ U[1024, 32768], Student-t K) at head sizes 64/128/256 with the balanced
 plan and with the reference's max_len-based splits; configs[4] end to end
 (random-init Qwen3-8B architecture, 8 x 32768-token prompts, 256 output
 tokens, through TurboQuantFusedImpl); the write kernel on configs[1]; the
-context read-back kernel; and the CPU baseline (a torch-CPU fp32 port of the
+context read-back kernel; the prefill attention kernel (one 32k-token
+causal prompt, beside torch's flash kernel) and a chunked-prefill call
+through the backend; and the CPU baseline (a torch-CPU fp32 port of the
 reference's PyTorch path, oracle/torch_ref.py) on the host cores.
 
 Prints ONE JSON line.  value = algorithmic bytes per step / step time, where
@@ -37,7 +39,7 @@ HBM_PEAK_GBS = 8000.0
 # tokens), from rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), each scale
 # taken from a 256 MiB device copy (profiles/decode_partials_cfg3_hbm_traffic.md);
 # keyed by (op, num_splits, kv_chunk_size) so an overridden layout reports null.
-PROFILED_TRAFFIC = {("balanced", 64, 512): 342304000, ("static", 64, 512): 341839000}
+PROFILED_TRAFFIC = {("balanced", 64, 512): 342077000, ("static", 64, 512): 342260000}
 TRAFFIC_SOURCE = ("profiled constant: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel at "
                   "this layout, profiles/decode_partials_cfg3_hbm_traffic.md")
 
@@ -303,7 +305,7 @@ def bench_prefill_chunk(torch, w, steps, warmup, chunk=2048):
     tokens, so 30720 cached before it; the chunk's own K/V are in the cache
     too, written first as vLLM does), Qwen3-8B geometry.  The cached context
     is read back by tq_dequant_paged and the chunk attends it plus its fresh
-    K/V in torch's flash kernel (lower-right causal, grouped kv heads).  The
+    K/V in tq_prefill_attention (lower-right causal, grouped kv heads).  The
     metadata carries host copies of the boundaries (as vLLM's does), so no
     device-to-host read happens; timed call by call with HIP events."""
     from types import SimpleNamespace
@@ -327,7 +329,42 @@ def bench_prefill_chunk(torch, w, steps, warmup, chunk=2048):
                        max(1, min(steps, 50)), max(1, min(warmup, 5)))
     return {"us": round(ms * 1e3, 1), "chunk_tokens": chunk, "cached_tokens": L - chunk,
             "config": "Qwen3-8B geometry 32q/8kv/128, one request, context read back from "
-                      "the quantized cache + torch flash attention (lower-right causal, GQA)"}
+                      "the quantized cache (tq_dequant_paged) + tq_prefill_attention "
+                      "(lower-right causal, GQA)"}
+
+
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill_kernel(torch, seq_len=32768):
+    """tq_prefill_attention on one 32768-token prompt at the Qwen3-8B
+    geometry (32 q heads, 8 kv heads, head size 128, causal), the attention
+    of configs[4]'s prefill, beside torch's fused flash kernel on the same
+    tensors.  Work: 4 * Hq * D * (causal query-key pairs) FLOPs (QK^T and
+    PV); bound: fp16 MFMA (2.5 PFLOP/s dense)."""
+    import torch.nn.functional as F
+
+    from turboquant_amd import ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(12)
+    hq, hkv, d, L = 32, 8, 128, seq_len
+    q = torch.randn((L, hq, d), generator=g, device=dev).half()
+    k = torch.randn((L, hkv, d), generator=g, device=dev).half()
+    v = torch.randn((L, hkv, d), generator=g, device=dev).half()
+    o = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(d)
+    flops = 4 * hq * d * (L * (L + 1) // 2)
+    ms = time_launches(torch, lambda: ops.prefill_attention(q, k, v, o, scale), 10, 2)
+    qt, kt, vt = (t.transpose(0, 1).unsqueeze(0) for t in (q, k, v))
+    ms_t = time_launches(torch, lambda: F.scaled_dot_product_attention(
+        qt, kt, vt, is_causal=True, scale=scale, enable_gqa=True), 10, 2)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+            "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "bound": "mfma (fp16, 2.5 PFLOP/s)",
+            "flops": flops, "torch_flash_us": round(ms_t * 1e3, 1),
+            "torch_flash_TFLOP/s": round(flops / (ms_t * 1e-3) / 1e12, 1),
+            "config": f"one {L}-token prompt, causal, 32q/8kv/128 fp16 (configs[4] prefill "
+                      "attention per layer)"}
 
 
 def bench_dequant(torch, w, steps, warmup):
@@ -432,7 +469,7 @@ def main():
     step = step_static if args.static else step_balanced
     op_name = ("turboquant_v5::decode_v5_from_cache_paged_splitkv_ws (static splits)"
                if args.static else "turboquant_v5::decode_paged_balanced_ws (balanced plan)")
-    wr = dq = pf = cpu = None
+    wr = dq = pf = pk = cpu = None
     if not quick:
         wr = bench_write(torch, args.steps, args.warmup)
         log(f"write kernel {wr['us']} us -> {wr['GB/s']} GB/s")
@@ -441,6 +478,9 @@ def main():
         pf = bench_prefill_chunk(torch, w, args.steps, args.warmup)
         log(f"prefill chunk {pf['chunk_tokens']} tokens over {pf['cached_tokens']} cached: "
             f"{pf['us']} us")
+        pk = bench_prefill_kernel(torch)
+        log(f"prefill attention kernel {pk['us']} us ({pk['TFLOP/s']} TFLOP/s); torch flash "
+            f"{pk['torch_flash_us']} us")
     log(f"timing decode ({op_name}): steps={args.steps} warmup={args.warmup}")
     ms_eager = time_launches(torch, step, args.steps, args.warmup)
     ms = time_graph(torch, step, args.steps, args.warmup)
@@ -553,6 +593,7 @@ def main():
         "write_kernel": wr,
         "dequant_kernel": dq,
         "prefill_chunk": pf,
+        "prefill_kernel": pk,
         "stream_ref": stream_ref,
     }
     print(json.dumps(line), flush=True)
