@@ -406,7 +406,8 @@ def main():
                     help="only run a plain 256 MiB device copy x5 (HBM counter scale reference)")
     ap.add_argument("--stream-ref", action="store_true",
                     help="also time the partials kernel with its math compiled out "
-                         "(tq_diag_decode_stream: the data movement alone)")
+                         "and the bare copy ring (tq_diag_decode_stream: the data movement "
+                         "alone)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the headline decode steps (for profiling)")
     args = ap.parse_args()
@@ -522,23 +523,31 @@ def main():
         f"step - both {(ms - ms_k - ms_c) * 1e3:.1f} us of launch gaps")
     stream_ref = None
     if args.stream_ref:
-        def stream_only():
+        def diag(mode):
             rc = lib.tq_diag_decode_stream(
                 w["q"].data_ptr(), w["q"].stride(0), w["q"].stride(1), cache.data_ptr(),
                 cache.data_ptr() + cache[0].numel(), w["indices"].data_ptr(),
                 w["indptr"].data_ptr(), w["seq"].data_ptr(), b, hq, w["hkv"], pd, 16, w["ebs"],
                 w["nb"], scale, w["signs"].data_ptr(), S, w["cs"], po.data_ptr(), pl.data_ptr(),
-                torch.cuda.current_stream().cuda_stream)
+                mode, torch.cuda.current_stream().cuda_stream)
             _lib.check(rc, "tq_diag_decode_stream")
-        ms_s = time_graph(torch, stream_only, args.steps, args.warmup)
-        stream_ref = {"us": round(ms_s * 1e3, 2),
-                      "layout_GB/s": round(b * w["seq_len"] * w["hkv"] * 2 * w["ebs"] /
-                                           (ms_s * 1e-3) / 1e9, 1),
-                      "alg_frac": round(alg_bytes(w) / (ms_s * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                      "what": "decode_partials_kernel<128, 8, 2, true, false, false>: the "
-                              "static-split partials kernel with the attention math compiled "
-                              "out (page walk, LDS copy ring, waits, barriers, slot reads)"}
-        log(f"partials without math {ms_s * 1e3:.1f} us")
+        lbytes = b * w["seq_len"] * w["hkv"] * 2 * w["ebs"]
+        stream_ref = {}
+        for mode, key, what in (
+                (1, "no_math", "decode_partials_kernel<128, 8, 2, true, false, 1>: the "
+                 "static-split partials kernel with the attention math compiled out (page "
+                 "walk, LDS copy ring, waits, barriers, slot reads; q setup, table build and "
+                 "partial-row stores kept)"),
+                (0, "bare_ring", "decode_partials_kernel<128, 8, 2, true, false, 0>: the bare "
+                 "copy ring (page walk, copies, waits, barriers, slot reads; no q setup, "
+                 "table or stores)")):
+            ms_s = time_graph(torch, lambda: diag(mode), args.steps, args.warmup)
+            stream_ref[key] = {"us": round(ms_s * 1e3, 2),
+                               "layout_GB/s": round(lbytes / (ms_s * 1e-3) / 1e9, 1),
+                               "alg_frac": round(alg_bytes(w) / (ms_s * 1e-3) / 1e9 /
+                                                 HBM_PEAK_GBS, 4),
+                               "what": what}
+            log(f"partials diagnostic {key}: {ms_s * 1e3:.1f} us")
     plan = split.cpu().tolist()
     layout_bytes = b * w["seq_len"] * w["hkv"] * 2 * w["ebs"]
     if not (quick or args.no_cpu):

@@ -241,11 +241,13 @@ int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_h
 
 /*
  * Diagnostic, no counterpart in the reference: tq_decode_partials at head
- * size 128 with 8 kv heads per workgroup (the configs[2] geometry) with the
- * attention math compiled out -- the same page walk, LDS copy ring, waits,
- * barriers and slot reads, zero partial rows.  Its duration is the cost of
- * the data movement alone (the bandwidth ceiling of this kernel design).
- * Other geometries return -22.
+ * size 128 with 8 kv heads per workgroup (the configs[2] geometry) with parts
+ * compiled out.  mode 1: the attention math (the same page walk, LDS copy
+ * ring, waits, barriers and slot reads, plus the q setup, table build and
+ * partial-row stores; zero partial rows).  mode 0: the bare copy ring (page
+ * walk, copies, waits, barriers and slot reads; nothing stored).  Their
+ * durations are the cost of the data movement alone (the bandwidth ceiling
+ * of this kernel design).  Other geometries return -22.
  */
 int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           const uint8_t* k_slab, const uint8_t* v_slab,
@@ -255,7 +257,8 @@ int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           int32_t padded_dim, int32_t block_size, int32_t ebs,
                           int64_t num_blocks, float sm_scale, const float* signs,
                           int32_t num_splits, int32_t kv_chunk_size,
-                          float* partition_o, float* partition_lse, tq_stream_t stream);
+                          float* partition_o, float* partition_lse, int32_t mode,
+                          tq_stream_t stream);
 
 /* Message for the last non-zero return of a tq_* call on this thread. */
 const char* tq_last_error(void);

@@ -895,7 +895,11 @@ __device__ __forceinline__ uint32_t shl8(uint32_t v) {
 // registers, barrier, then the copies of the tiles kRingSlots ahead are
 // issued into the two slots just read, and the math runs while they are in
 // flight.  Slot bases are runtime values (advanced by two slots per step).
-template <int PD, int G, int PACK, bool QC, bool PLAN, bool MATH = true>
+// MATH: 2 = the kernel; 1 and 0 are diagnostics of its data movement: 1 =
+// the attention math compiled out (q' setup, table build and partial-row
+// stores kept), 0 = the bare copy ring (page walk, copies, waits, barriers
+// and slot reads only).
+template <int PD, int G, int PACK, bool QC, bool PLAN, int MATH = 2>
 __global__ __launch_bounds__(64 * G)
 __attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : (PACK == 1 ? 3 : 4))))
 void decode_partials_kernel(DecodeParams p) {
@@ -1025,7 +1029,7 @@ void decode_partials_kernel(DecodeParams p) {
   const bool qreg = ratio * PD <= 512 * NQL;  // uniform
   float qx[NQL][8];
 #if defined(__HIP_DEVICE_COMPILE__)
-  {
+  if constexpr (MATH >= 1) {
     const _Float16* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)kvh * ratio * p.q_sh;
     const int qrec = qreg ? (int)(((ratio - 1) * p.q_sh + PD) * 2) : 0;
     const __amdgpu_buffer_rsrc_t rq =
@@ -1216,7 +1220,13 @@ void decode_partials_kernel(DecodeParams p) {
     // fp32-level accuracy even for heavy-tailed keys), in the MFMA B layout.
     const float qsc = (p.signs ? p.inv_sqrt_pd : 1.0f) * p.qk_scale;
     const int hq = QC ? (n & 7) : n;  // q head of this lane's B column
-    if (qreg) {
+    if constexpr (MATH == 0) {
+      if (!qreg) {
+#pragma unroll
+        for (int r = 0; r < kRingSlots; r++)
+          if (2 * step0 + r <= tile_end) issue(2 * step0 + r, r);
+      }
+    } else if (qreg) {
       // in registers: butterflies h = 1, 2, 4 inside a lane, h >= 8 between
       // lanes l and l ^ (h / 8) (DPP, one fma with a lane sign each)
       // the second 512 elements only exist when ratio * PD > 512
@@ -1429,7 +1439,7 @@ void decode_partials_kernel(DecodeParams p) {
         issue(2 * k + kRingSlots, s0);
         if (2 * k + kRingSlots + 1 <= tile_end) issue(2 * k + kRingSlots + 1, s1);
       }
-      if constexpr (MATH) compute(k, d);
+      if constexpr (MATH >= 2) compute(k, d);
     };
     for (int k = step0, s0 = 0, s1 = 1; k <= step1; k++) {
       run(k, s0, s1);
@@ -1438,6 +1448,7 @@ void decode_partials_kernel(DecodeParams p) {
     }
   }
 
+  if constexpr (MATH == 0) return;  // the bare ring stores nothing
   // ---- finish: O[i][r] = o[h = n][dim (4*q4 + r)*NO + i]
   float lt = st.lsum;
   if constexpr (PACK == 2) lt = lt + __int_as_float(__builtin_amdgcn_mov_dpp(
@@ -2181,9 +2192,13 @@ extern "C" int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t 
                                      int32_t padded_dim, int32_t block_size, int32_t ebs,
                                      int64_t num_blocks, float sm_scale, const float* signs,
                                      int32_t num_splits, int32_t kv_chunk_size,
-                                     float* partition_o, float* partition_lse,
+                                     float* partition_o, float* partition_lse, int32_t mode,
                                      tq_stream_t stream) {
   using namespace tq;
+  if (mode != 0 && mode != 1) {
+    set_error("diag_decode_stream: mode %d is neither 0 (bare ring) nor 1 (no math)", mode);
+    return kEinval;
+  }
   if (num_splits < 1 || kv_chunk_size < 1) {
     set_error("diag_decode_stream: num_splits %d, kv_chunk_size %d out of range", num_splits,
               kv_chunk_size);
@@ -2202,7 +2217,8 @@ extern "C" int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t 
   p.S = num_splits;
   p.cs = kv_chunk_size;
   const int64_t blocks = (int64_t)batch * num_splits * p.HG;
-  const PartialsFn fn = &decode_partials_kernel<128, 8, 2, true, false, false>;
+  const PartialsFn fn = mode == 0 ? &decode_partials_kernel<128, 8, 2, true, false, 0>
+                                  : &decode_partials_kernel<128, 8, 2, true, false, 1>;
   const Occupancy occ = occupancy(reinterpret_cast<const void*>(fn), 64 * p.G);
   if (occ.per_cu == 2 && blocks == 2LL * occ.cus && num_splits % 2 == 0)
     p.pair_pct = kPairPct;
