@@ -280,6 +280,11 @@ def bench_e2e(torch, compare_steps=16):
 
 
 def bench_write(torch, steps, warmup):
+    """configs[1] (8192 tokens x 8 kv heads x 128, fp16, outlier channels,
+    permuted slots), then the same chunk at head size 64 (4 kv heads) and 256
+    (2 kv heads); graph-timed, algorithmic bytes as in workloads."""
+    import numpy as np
+
     from tests import workloads as W
     from turboquant_amd import ops
     from turboquant_amd.geometry import hadamard_signs
@@ -294,9 +299,33 @@ def bench_write(torch, steps, warmup):
     ms = time_graph(torch, lambda: ops.quantize_write_kv_cache(cache, k, v, signs, slots,
                                                                128, pd), steps, warmup)
     nbytes = W.algorithmic_write_bytes(8192, 8, 128)
-    return {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "alg_bytes": nbytes, "config": "8192 tok x 8 heads x 128, K+V fp16, outliers x20, "
-                                           "permuted slots (configs[1])"}
+    res = {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+           "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "alg_bytes": nbytes, "config": "8192 tok x 8 heads x 128, K+V fp16, outliers x20, "
+                                          "permuted slots (configs[1])"}
+    del cache, k, v
+    # the same chunk at the other head sizes of configs[3] (kv heads 4 at hd 64,
+    # 2 at hd 256), same seeding scheme
+    other = []
+    for hd, h in ((64, 4), (256, 2)):
+        rng = np.random.default_rng(2 + hd)
+        kk, vv = W.write_inputs(rng, 8192, h, hd, outliers=True)
+        sl = torch.from_numpy(rng.permutation(512 * W.BLOCK)[:8192].astype(np.int32)).to(dev)
+        shape, pd = W.cache_bytes(512, h, hd)
+        cache = torch.zeros(shape, dtype=torch.uint8, device=dev)
+        kk = torch.from_numpy(kk).to(dev)
+        vv = torch.from_numpy(vv).to(dev)
+        sg = hadamard_signs(pd, dev)
+        ms = time_graph(torch, lambda: ops.quantize_write_kv_cache(cache, kk, vv, sg, sl, hd, pd),
+                        steps, warmup)
+        nb = W.algorithmic_write_bytes(8192, h, hd)
+        other.append({"head_dim": hd, "kv_heads": h, "us": round(ms * 1e3, 2),
+                      "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                      "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "alg_bytes": nb})
+        log(f"write hd={hd} x {h} heads: {ms * 1e3:.2f} us")
+        del cache, kk, vv
+    res["other_head_sizes"] = other
+    return res
 
 
 def bench_prefill_chunk(torch, w, steps, warmup, chunk=2048):
