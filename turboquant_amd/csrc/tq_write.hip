@@ -306,8 +306,11 @@ __global__ __launch_bounds__(256) void write_kernel(
 //    NaN everywhere after the FWHT, i.e. code 0, as in the reference.
 template <int PD>
 struct FastGeom {
-  static constexpr int CPL = 4;                // 16-byte chunks (8 dims) per lane
-  static constexpr int P = PD / (8 * CPL);     // lanes per vector (2, 4, 8)
+  // 16-byte chunks (8 dims) per lane: 4, and 2 at pd 64, where 4 would leave
+  // a launch half the waves (measured 8.3 against 8.6 us for 8192 tokens x 8
+  // heads; 1 chunk per lane: 9.7 us)
+  static constexpr int CPL = PD == 64 ? 2 : 4;
+  static constexpr int P = PD / (8 * CPL);     // lanes per vector (4, 4, 8)
   static constexpr int VEC = PD / 32;          // dims per reference lane
   static constexpr int E = 8 / VEC;            // reference lanes per chunk
   static constexpr int PE = P * E;             // reference lanes per chunk row (32 / CPL)
@@ -510,6 +513,8 @@ __global__ __launch_bounds__(256) void write_f16_kernel(
       }
     }
   };
+  level(std::integral_constant<int, 16>{});
+  level(std::integral_constant<int, 8>{});
   level(std::integral_constant<int, 4>{});
   level(std::integral_constant<int, 2>{});
   level(std::integral_constant<int, 1>{});
