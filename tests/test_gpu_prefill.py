@@ -38,6 +38,9 @@ CASES = [
     (64, 4096, 32, 8),
     (1, 777, 32, 4),
     (300, 300, 32, 32),
+    # 256-row workgroups (q heads x 256-row blocks >= the CU count)
+    (2085, 3000, 32, 8),
+    (2048, 2048, 128, 16),
 ]
 
 
