@@ -54,9 +54,8 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 }
 
 constexpr int kD = 128;      // head size
-constexpr int kBN = 64;      // keys per tile
-constexpr int kKRow = kD * 2;        // bytes of one K row in LDS (16 chunks of 16 B)
-constexpr int kVtRow = kBN * 2 + 8;  // bytes of one V^T row (64 keys + 4 pad halves)
+constexpr int kKRow = kD * 2;  // bytes of one K row in LDS (16 chunks of 16 B)
+constexpr int kBNmax = 128;    // largest tile (keys)
 
 struct PrefillParams {
   const _Float16* q;
@@ -81,10 +80,12 @@ __device__ __forceinline__ float sum32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int NW>
+template <int NW, int kBN>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(PrefillParams p) {
   constexpr int kBM = 32 * NW;  // query rows per workgroup
+  constexpr int kVtRow = kBN * 2 + 8;  // bytes of one V^T row (kBN keys + 4 pad halves)
+  constexpr int kNU = kBN / 32, kNS = kBN / 16;  // 32-key score blocks, 16-key PV steps
   __shared__ __attribute__((aligned(16))) uint8_t kbuf0[kBN * kKRow];
   __shared__ __attribute__((aligned(16))) uint8_t kbuf1[kBN * kKRow];
   __shared__ __attribute__((aligned(16))) uint8_t vt0[kD * kVtRow];
@@ -118,7 +119,7 @@ void prefill_kernel(PrefillParams p) {
   // buffer = rows 4j .. 4j+3; lane l writes row 4j + l/16, physical chunk
   // l%16, which holds logical chunk (l%16) ^ (row%16) of that key row.
   // Wave w issues copies j = w + NW i.
-  constexpr int kKC = 16 / NW;  // copies per wave and tile
+  constexpr int kKC = (kBN / 4) / NW;  // copies per wave and tile
   const int kst_b = (int)(p.k_st * 2);
   uint32_t koff[kKC];  // per-lane byte offsets of this wave's copies inside a tile
 #pragma unroll
@@ -151,12 +152,13 @@ void prefill_kernel(PrefillParams p) {
     (void)buf;
 #endif
   };
-  // V: thread (w, lane) of waves 0..3 loads keys 4a .. 4a+3 (a = lane/4) x
-  // dims 8b .. 8b+7 (b = 4w + lane%4) of a tile, then writes them transposed
-  // (with eight waves the other four skip it: spreading the tile over all
-  // eight, 4 keys x 4 dims a lane, measured 2% slower)
-  const bool vmover = NW == 4 || w < 4;
-  const int va = lane >> 2, vb = 4 * (w & 3) + (lane & 3);
+  // V: thread (w, lane) loads keys 4a .. 4a+3 x dims 8b .. 8b+7 of a tile
+  // (a = lane/4, plus 16 for waves 4..7 of a 128-key tile; b = 4 (w % 4) +
+  // lane%4), then writes them transposed.  Four waves cover a 64-key tile
+  // (with eight waves the other four skip it: spreading it over all eight,
+  // 4 keys x 4 dims a lane, measured 2% slower); eight cover a 128-key tile.
+  const bool vmover = NW == 4 || w < 4 || kBN == 128;
+  const int va = (lane >> 2) + (kBN == 128 ? 16 * (w >> 2) : 0), vb = 4 * (w & 3) + (lane & 3);
   const int vst_b = (int)(p.v_st * 2);
   u32x4 vr[4];
   auto load_v = [&](int kt) {
@@ -194,9 +196,9 @@ void prefill_kernel(PrefillParams p) {
     // the wave's rows are q0 + 32w .. +31: nothing to do when all its keys
     // in this tile are beyond every row (uniform)
     if (kb > off + q0 + 32 * w + 31) return;
-    f32x16 sacc[2];
+    f32x16 sacc[kNU];
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
+    for (int u = 0; u < kNU; u++) {
       const int row = 32 * u + n;
       f32x16 acc;
 #pragma unroll
@@ -210,19 +212,24 @@ void prefill_kernel(PrefillParams p) {
       }
       sacc[u] = acc;
     }
-    // mask keys beyond the row (causal) or beyond Lk (uniform test)
+    // mask keys beyond the row (causal) or beyond Lk (uniform test): lim is
+    // the lane's last visible key relative to key 4 hh of the tile, and the
+    // score at tile key 4 hh + kk gets -inf (the sign bits of lim - kk spread
+    // into 0xff800000) or +0 added; no compare masks, so no scalar registers
+    // for them
     if (kb + kBN - 1 > off + q0 + 32 * w || kb + kBN > p.lk) {
+      const int lim = min(qlim, p.lk - 1) - kb - 4 * hh;
 #pragma unroll
-      for (int u = 0; u < 2; u++)
+      for (int u = 0; u < kNU; u++)
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-          const int key = kb + 32 * u + 8 * (j >> 2) + 4 * hh + (j & 3);
-          if (key > qlim || key >= p.lk) sacc[u][j] = -INFINITY;
+          const int kk = 32 * u + 8 * (j >> 2) + (j & 3);
+          sacc[u][j] += __int_as_float(((lim - kk) >> 31) & (int)0xff800000u);
         }
     }
     float tmax = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 2; u++)
+    for (int u = 0; u < kNU; u++)
 #pragma unroll
       for (int j = 0; j < 16; j++) tmax = fmaxf(tmax, sacc[u][j]);
     tmax = max32(tmax);
@@ -236,9 +243,9 @@ void prefill_kernel(PrefillParams p) {
       m = m_new;
       mc = m_new * p.c;
     }
-    half8_t pB[4];  // B operand of O^T = V^T P^T for k-steps (u, t)
+    half8_t pB[kNS];  // B operand of O^T = V^T P^T for k-steps (u, t)
 #pragma unroll
-    for (int u = 0; u < 2; u++)
+    for (int u = 0; u < kNU; u++)
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         float pr[8];
@@ -256,7 +263,7 @@ void prefill_kernel(PrefillParams p) {
     // O^T += V^T P^T: k-step (u, t) reduces keys 32u + 16t + {4hh + 0..3,
     // 8 + 4hh + 0..3} (the C-layout rows of the lane's probabilities)
 #pragma unroll
-    for (int st = 0; st < 4; st++) {
+    for (int st = 0; st < kNS; st++) {
       const int key0 = 16 * st + 4 * hh;
 #pragma unroll
       for (int d = 0; d < kD / 32; d++) {
@@ -315,9 +322,9 @@ void prefill_kernel(PrefillParams p) {
 // the two workgroup shapes
 hipError_t launch_prefill(int nw, int heads, hipStream_t st, const PrefillParams& p) {
   if (nw == 8)
-    hipLaunchKernelGGL((prefill_kernel<8>), dim3(heads, p.nqb), dim3(512), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<8, 128>), dim3(heads, p.nqb), dim3(512), 0, st, p);
   else
-    hipLaunchKernelGGL((prefill_kernel<4>), dim3(heads, p.nqb), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<4, 64>), dim3(heads, p.nqb), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -370,7 +377,7 @@ extern "C" int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
     }
   }
   if (k_stride_tok < kD || v_stride_tok < kD ||
-      (k_stride_tok > v_stride_tok ? k_stride_tok : v_stride_tok) * 2 * (int64_t)kBN > INT32_MAX) {
+      (k_stride_tok > v_stride_tok ? k_stride_tok : v_stride_tok) * 2 * (int64_t)kBNmax > INT32_MAX) {
     set_error("prefill_attention: k / v token strides out of range");
     return kEinval;
   }
