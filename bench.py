@@ -39,7 +39,7 @@ HBM_PEAK_GBS = 8000.0
 # tokens), from rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), each scale
 # taken from a 256 MiB device copy (profiles/decode_partials_cfg3_hbm_traffic.md);
 # keyed by (op, num_splits, kv_chunk_size) so an overridden layout reports null.
-PROFILED_TRAFFIC = {("balanced", 64, 512): 342077000, ("static", 64, 512): 342260000}
+PROFILED_TRAFFIC = {("balanced", 64, 512): 342085000, ("static", 64, 512): 342244000}
 TRAFFIC_SOURCE = ("profiled constant: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel at "
                   "this layout, profiles/decode_partials_cfg3_hbm_traffic.md")
 
@@ -577,6 +577,22 @@ def main():
                                                  HBM_PEAK_GBS, 4),
                                "what": what}
             log(f"partials diagnostic {key}: {ms_s * 1e3:.1f} us")
+        # a plain non-temporal stream over the same cache bytes (both slabs of
+        # the cache tensor): the read rate HBM gives without the ring's page
+        # walk, dependent start and barriers
+        sink = torch.zeros(4, dtype=torch.int32, device=cache.device)
+        cbytes = cache.numel() // 16 * 16
+
+        def sread():
+            _lib.check(lib.tq_diag_stream_read(cache.data_ptr(), cbytes, sink.data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream),
+                       "tq_diag_stream_read")
+        ms_r = time_graph(torch, sread, args.steps, args.warmup)
+        stream_ref["plain_stream"] = {"us": round(ms_r * 1e3, 2), "bytes": cbytes,
+                                      "GB/s": round(cbytes / (ms_r * 1e-3) / 1e9, 1),
+                                      "what": "stream_read_kernel: non-temporal 16-byte loads "
+                                              "over the whole cache tensor, no page table"}
+        log(f"plain stream read of {cbytes / 1e6:.1f} MB: {ms_r * 1e3:.1f} us")
     plan = split.cpu().tolist()
     layout_bytes = b * w["seq_len"] * w["hkv"] * 2 * w["ebs"]
     if not (quick or args.no_cpu):

@@ -260,6 +260,15 @@ int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           float* partition_o, float* partition_lse, int32_t mode,
                           tq_stream_t stream);
 
+/*
+ * Diagnostic, no counterpart in the reference: reads `bytes` (a multiple of
+ * 16, 16-byte aligned) from device memory with non-temporal 16-byte loads,
+ * a 2048 x 256 grid-strided stream, and stores to *sink only for one
+ * improbable xor of the data.  Its duration is the HBM read rate a plain
+ * stream reaches, beside which the decode kernel's copy ring is measured.
+ */
+int tq_diag_stream_read(const void* src, int64_t bytes, uint32_t* sink, tq_stream_t stream);
+
 /* Message for the last non-zero return of a tq_* call on this thread. */
 const char* tq_last_error(void);
 

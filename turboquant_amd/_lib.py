@@ -39,6 +39,7 @@ SIGNATURES = {
                                   _I32, _I32, _I64, _F32, _P, _I32, _I32, _P, _P, _P]),
     "tq_diag_decode_stream": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                      _I32, _I32, _I64, _F32, _P, _I32, _I32, _P, _P, _I32, _P]),
+    "tq_diag_stream_read": (_I32, [_P, _I64, _P, _P]),
     "tq_combine_splits": (_I32, [_P, _P, _I32, _I32, _I32, _I32, _P, _P, _P]),
     "tq_dequant_paged": (_I32, [_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I64, _P, _P,
                                 _P, _I64, _P]),

@@ -2225,6 +2225,44 @@ extern "C" int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t 
   return launch_partials(fn, p, blocks, stream);
 }
 
+namespace tq {
+namespace {
+// Streaming read of n 16-byte words with non-temporal loads, four per lane in
+// flight per iteration, grid-strided; the xor of everything read is stored
+// only if it equals a constant no sane input produces, which keeps the loads.
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ src,
+                                                          int64_t n, uint32_t* sink) {
+  uint32_t acc = 0;
+  const int64_t stride = (int64_t)gridDim.x * 1024;
+  for (int64_t i = (int64_t)blockIdx.x * 1024 + threadIdx.x; i < n; i += stride) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      v[u] = i + 256 * u < n ? __builtin_nontemporal_load(src + i + 256 * u) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < 4; u++) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+  if (acc == 0x7e57c0deu) sink[0] = acc;
+}
+}  // namespace
+}  // namespace tq
+
+// Diagnostic: the HBM read rate a plain stream reaches (no page table, no
+// LDS, no barriers), the reference point for the copy ring above.
+extern "C" int tq_diag_stream_read(const void* src, int64_t bytes, uint32_t* sink,
+                                   tq_stream_t stream) {
+  using namespace tq;
+  if (!src || !sink || bytes < 0 || bytes % 16 != 0 || ((uintptr_t)src & 15)) {
+    set_error("diag_stream_read: need a 16-byte aligned source of a multiple of 16 bytes");
+    return kEinval;
+  }
+  if (bytes == 0) return 0;
+  hipLaunchKernelGGL(stream_read_kernel, dim3(2048), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const u32x4*>(src),
+                     bytes / 16, sink);
+  return (int)hipGetLastError();
+}
+
 extern "C" int tq_decode_partials_balanced(
     const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* k_slab,
     const uint8_t* v_slab, const int32_t* indices, const int32_t* indptr,
