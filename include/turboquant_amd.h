@@ -263,8 +263,8 @@ int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 /*
  * Diagnostic, no counterpart in the reference: reads `bytes` (a multiple of
  * 16, 16-byte aligned) from device memory with non-temporal 16-byte loads,
- * a 2048 x 256 grid-strided stream, and stores to *sink only for one
- * improbable xor of the data.  Its duration is the HBM read rate a plain
+ * a 2048 x 256 grid-strided stream; a lane stores to *sink only if the xor
+ * of the words it read equals one constant.  Its duration is the HBM read rate a plain
  * stream reaches, beside which the decode kernel's copy ring is measured.
  */
 int tq_diag_stream_read(const void* src, int64_t bytes, uint32_t* sink, tq_stream_t stream);

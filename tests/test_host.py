@@ -152,6 +152,10 @@ def test_cabi_argument_errors_without_gpu():
     assert rc == -22 and b"q_len" in lib.tq_last_error()
     # an empty batch is a no-op that succeeds
     assert lib.tq_combine_splits(null, null, 0, 1, 32, 128, null, null, null) == 0
+    # the stream-read diagnostic: null source, size not a multiple of 16
+    assert lib.tq_diag_stream_read(null, 16, null, null) == -22
+    assert lib.tq_diag_stream_read(ctypes.c_void_p(256), 24, ctypes.c_void_p(256), null) == -22
+    assert lib.tq_diag_stream_read(ctypes.c_void_p(256), 0, ctypes.c_void_p(256), null) == 0
 
 
 def test_missing_library_raises(monkeypatch):

@@ -2228,8 +2228,8 @@ extern "C" int tq_diag_decode_stream(const void* q, int64_t q_stride_b, int64_t 
 namespace tq {
 namespace {
 // Streaming read of n 16-byte words with non-temporal loads, four per lane in
-// flight per iteration, grid-strided; the xor of everything read is stored
-// only if it equals a constant no sane input produces, which keeps the loads.
+// flight per iteration, grid-strided; a lane stores the xor of the words it
+// read only if it equals one constant, which keeps the loads.
 __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ src,
                                                           int64_t n, uint32_t* sink) {
   uint32_t acc = 0;
