@@ -64,13 +64,15 @@ def test_prefill_matches_float64(lq, lk, hq, hkv):
     assert (err <= tol).all(), f"max err {err.max().item():.3e}"
 
 
-def test_prefill_strided_rows_and_heavy_tails():
+@pytest.mark.parametrize("lq,lk", [(300, 700), (2100, 2500)])
+def test_prefill_strided_rows_and_heavy_tails(lq, lk):
     """Rows of q/k/v/o taken from wider packed tensors (as the backend's
-    qkv projection slices them), Student-t keys with a few large scores."""
-    print("case: prefill strided rows, t3 keys", flush=True)
+    qkv projection slices them), Student-t keys with a few large scores; a
+    128-row and a 256-row workgroup shape."""
+    print(f"case: prefill strided rows, t3 keys lq={lq} lk={lk}", flush=True)
     from turboquant_amd import ops
     g = torch.Generator(device=DEV).manual_seed(5)
-    lq, lk, hq, hkv, d = 300, 700, 32, 8, 128
+    hq, hkv, d = 32, 8, 128
     qkv = torch.randn((lk, (hq + 2 * hkv) * d), generator=g, device=DEV).half()
     t = torch.distributions.StudentT(3.0).sample((lk, hkv * d)).to(DEV).half()
     qkv[:, hq * d:(hq + hkv) * d] = t
@@ -87,11 +89,12 @@ def test_prefill_strided_rows_and_heavy_tails():
     assert (err <= 2e-3 + 1e-2 * ref.abs()).all(), f"max err {err.max().item():.3e}"
 
 
-def test_prefill_graph_replay_matches_eager():
-    print("case: prefill graph replay", flush=True)
+@pytest.mark.parametrize("lq,lk", [(256, 512), (2048, 2300)])
+def test_prefill_graph_replay_matches_eager(lq, lk):
+    print(f"case: prefill graph replay lq={lq} lk={lk}", flush=True)
     from turboquant_amd import ops
     g = torch.Generator(device=DEV).manual_seed(9)
-    lq, lk, hq, hkv, d = 256, 512, 32, 8, 128
+    hq, hkv, d = 32, 8, 128
     q = torch.randn((lq, hq, d), generator=g, device=DEV).half()
     k = torch.randn((lk, hkv, d), generator=g, device=DEV).half()
     v = torch.randn((lk, hkv, d), generator=g, device=DEV).half()
