@@ -42,14 +42,21 @@ CASES = [
     (2085, 3000, 32, 8),
     (2048, 2048, 128, 16),
 ]
+# head size 64 (the configs[3] geometry: 16 q / 4 kv heads), both shapes
+CASES64 = [
+    (1, 1, 16, 4),
+    (129, 400, 16, 4),
+    (1000, 1000, 16, 4),
+    (4100, 4500, 16, 4),
+]
 
 
-@pytest.mark.parametrize("lq,lk,hq,hkv", CASES)
-def test_prefill_matches_float64(lq, lk, hq, hkv):
-    print(f"case: prefill lq={lq} lk={lk} hq={hq} hkv={hkv}", flush=True)
+@pytest.mark.parametrize("lq,lk,hq,hkv,d", [c + (128,) for c in CASES] +
+                         [c + (64,) for c in CASES64])
+def test_prefill_matches_float64(lq, lk, hq, hkv, d):
+    print(f"case: prefill lq={lq} lk={lk} hq={hq} hkv={hkv} d={d}", flush=True)
     from turboquant_amd import ops
-    g = torch.Generator(device=DEV).manual_seed(lq * 7919 + lk)
-    d = 128
+    g = torch.Generator(device=DEV).manual_seed(lq * 7919 + lk + d)
     q = torch.randn((lq, hq, d), generator=g, device=DEV).half()
     k = torch.randn((lk, hkv, d), generator=g, device=DEV).half()
     v = torch.randn((lk, hkv, d), generator=g, device=DEV).half()

@@ -140,9 +140,9 @@ def test_cabi_argument_errors_without_gpu():
     assert rc == -22 and lib.tq_last_error()
     rc = lib.tq_combine_splits(null, null, 1, 0, 32, 128, null, null, null)
     assert rc == -22
-    # prefill attention: head size 128 only, GQA ratio must divide, q_len <= kv_len
+    # prefill attention: head size 64 or 128 only, GQA ratio must divide, q_len <= kv_len
     rc = lib.tq_prefill_attention(null, 0, 0, null, 0, 0, null, 0, 0, null, 0, 0, 4, 4, 32, 8,
-                                  64, 0.1, null)
+                                  96, 0.1, null)
     assert rc == -22 and b"head_dim" in lib.tq_last_error()
     rc = lib.tq_prefill_attention(null, 0, 0, null, 0, 0, null, 0, 0, null, 0, 0, 4, 4, 30, 8,
                                   128, 0.1, null)

@@ -1,4 +1,5 @@
-// tq_prefill.hip -- causal GQA flash attention of a prefill chunk (fp16 K/V).
+// tq_prefill.hip -- causal GQA flash attention of a prefill chunk (fp16 K/V,
+// head size 64 or 128).
 //
 // Semantics: o[i, h] = softmax_j(q[i, h] . k[j, h / ratio] * sm_scale) v[j, h / ratio]
 // over keys j <= (Lk - Lq) + i (causal, aligned to the end of the keys: a
@@ -53,8 +54,6 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, half2_t));
 }
 
-constexpr int kD = 128;      // head size
-constexpr int kKRow = kD * 2;  // bytes of one K row in LDS (16 chunks of 16 B)
 constexpr int kBNmax = 128;    // largest tile (keys)
 
 struct PrefillParams {
@@ -80,9 +79,12 @@ __device__ __forceinline__ float sum32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int NW, int kBN>
+template <int kD, int NW, int kBN>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(PrefillParams p) {
+  constexpr int kKRow = kD * 2;       // bytes of one K row in LDS
+  constexpr int kCH = kD / 8;         // 16-byte chunks per K row
+  constexpr int kRPC = 1024 / kKRow;  // K rows per 1 KB copy
   constexpr int kBM = 32 * NW;  // query rows per workgroup
   constexpr int kVtRow = kBN * 2 + 8;  // bytes of one V^T row (kBN keys + 4 pad halves)
   constexpr int kNU = kBN / 32, kNS = kBN / 16;  // 32-key score blocks, 16-key PV steps
@@ -115,17 +117,17 @@ void prefill_kernel(PrefillParams p) {
     }
   }
 
-  // K copies: copy j (0..15) fills LDS bytes [1024 j, 1024 j + 1024) of a
-  // buffer = rows 4j .. 4j+3; lane l writes row 4j + l/16, physical chunk
-  // l%16, which holds logical chunk (l%16) ^ (row%16) of that key row.
-  // Wave w issues copies j = w + NW i.
-  constexpr int kKC = (kBN / 4) / NW;  // copies per wave and tile
+  // K copies: copy j fills LDS bytes [1024 j, 1024 j + 1024) of a buffer =
+  // rows kRPC j .. kRPC j + kRPC - 1; lane l writes row kRPC j + l / kCH,
+  // physical chunk l % kCH, which holds logical chunk (l % kCH) ^ (row % kCH)
+  // of that key row.  Wave w issues copies j = w + NW i.
+  constexpr int kKC = (kBN / kRPC) / NW;  // copies per wave and tile
   const int kst_b = (int)(p.k_st * 2);
   uint32_t koff[kKC];  // per-lane byte offsets of this wave's copies inside a tile
 #pragma unroll
   for (int i = 0; i < kKC; i++) {
-    const int j = w + NW * i, row = 4 * j + (lane >> 4);
-    koff[i] = (uint32_t)(row * kst_b + (((lane & 15) ^ (row & 15)) * 16));
+    const int j = w + NW * i, row = kRPC * j + lane / kCH;
+    koff[i] = (uint32_t)(row * kst_b + (((lane % kCH) ^ (row % kCH)) * 16));
   }
   // buffer resource over rows [kb, Lk) of a K or V tile (wave-uniform base
   // and size; rows past Lk read as zeros)
@@ -153,12 +155,14 @@ void prefill_kernel(PrefillParams p) {
 #endif
   };
   // V: thread (w, lane) loads keys 4a .. 4a+3 x dims 8b .. 8b+7 of a tile
-  // (a = lane/4, plus 16 for waves 4..7 of a 128-key tile; b = 4 (w % 4) +
-  // lane%4), then writes them transposed.  Four waves cover a 64-key tile
-  // (with eight waves the other four skip it: spreading it over all eight,
-  // 4 keys x 4 dims a lane, measured 2% slower); eight cover a 128-key tile.
-  const bool vmover = NW == 4 || w < 4 || kBN == 128;
-  const int va = (lane >> 2) + (kBN == 128 ? 16 * (w >> 2) : 0), vb = 4 * (w & 3) + (lane & 3);
+  // (b = 4 (w % kDW) + lane % 4, a = lane / 4 + 16 (w / kDW), kDW = D / 32
+  // waves per 64 keys), then writes them transposed; waves with a >= kBN/4
+  // skip it (at D = 128: four waves cover a 64-key tile, and with eight
+  // waves the other four skip it: spreading it over all eight, 4 keys x 4
+  // dims a lane, measured 2% slower; eight cover a 128-key tile)
+  constexpr int kDW = kD / 32;
+  const bool vmover = w / kDW < kBN / 64;
+  const int va = (lane >> 2) + 16 * (w / kDW), vb = 4 * (w % kDW) + (lane & 3);
   const int vst_b = (int)(p.v_st * 2);
   u32x4 vr[4];
   auto load_v = [&](int kt) {
@@ -210,7 +214,7 @@ void prefill_kernel(PrefillParams p) {
     auto kfrag = [&](int i) {
       const int u = i % kNU, s = i / kNU, row = 32 * u + n;
       return *reinterpret_cast<const u32x4*>(kbuf + row * kKRow +
-                                             (((2 * s + hh) ^ (row & 15)) * 16));
+                                             (((2 * s + hh) ^ (row % kCH)) * 16));
     };
     u32x4 fr[kKP];
 #pragma unroll
@@ -335,12 +339,13 @@ void prefill_kernel(PrefillParams p) {
   }
 }
 
-// the two workgroup shapes
+// the two workgroup shapes, at head size 64 or 128
+template <int D>
 hipError_t launch_prefill(int nw, int heads, hipStream_t st, const PrefillParams& p) {
   if (nw == 8)
-    hipLaunchKernelGGL((prefill_kernel<8, 128>), dim3(heads, p.nqb), dim3(512), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<D, 8, 128>), dim3(heads, p.nqb), dim3(512), 0, st, p);
   else
-    hipLaunchKernelGGL((prefill_kernel<4, 64>), dim3(heads, p.nqb), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<D, 4, 64>), dim3(heads, p.nqb), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -367,8 +372,8 @@ extern "C" int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
                                     int32_t num_kv_heads, int32_t head_dim, float sm_scale,
                                     tq_stream_t stream) {
   using namespace tq;
-  if (head_dim != kD) {
-    set_error("prefill_attention: head_dim %d unsupported (128 only)", head_dim);
+  if (head_dim != 64 && head_dim != 128) {
+    set_error("prefill_attention: head_dim %d unsupported (64 or 128 only)", head_dim);
     return kEinval;
   }
   if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads != 0) {
@@ -392,7 +397,7 @@ extern "C" int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
       return kEinval;
     }
   }
-  if (k_stride_tok < kD || v_stride_tok < kD ||
+  if (k_stride_tok < head_dim || v_stride_tok < head_dim ||
       (k_stride_tok > v_stride_tok ? k_stride_tok : v_stride_tok) * 2 * (int64_t)kBNmax > INT32_MAX) {
     set_error("prefill_attention: k / v token strides out of range");
     return kEinval;
@@ -426,8 +431,10 @@ extern "C" int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
   const int64_t nqb8 = (q_len + 255) / 256;
   if ((int64_t)num_qo_heads * nqb8 >= (int64_t)device_cus()) {
     p.nqb = (int)nqb8;
-    return (int)launch_prefill(8, num_qo_heads, st, p);
+    return (int)(head_dim == 64 ? launch_prefill<64>(8, num_qo_heads, st, p)
+                                : launch_prefill<128>(8, num_qo_heads, st, p));
   }
   p.nqb = (q_len + 127) / 128;
-  return (int)launch_prefill(4, num_qo_heads, st, p);
+  return (int)(head_dim == 64 ? launch_prefill<64>(4, num_qo_heads, st, p)
+                              : launch_prefill<128>(4, num_qo_heads, st, p));
 }

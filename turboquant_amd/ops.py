@@ -212,10 +212,11 @@ def decode_paged_balanced(q: torch.Tensor, kv_cache: torch.Tensor, indices: torc
 
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                       sm_scale: float) -> torch.Tensor:
-    """Causal GQA attention of q [Lq, Hq, 128] over k, v [Lk, Hkv, 128] (fp16,
-    Lq <= Lk), the queries aligned to the end of the keys (query i sees keys
-    <= Lk - Lq + i), written into o [Lq, Hq, 128] fp16.  Heads and dims of
-    every tensor contiguous; token strides free (multiples of 8)."""
+    """Causal GQA attention of q [Lq, Hq, D] over k, v [Lk, Hkv, D] (fp16,
+    D = 64 or 128, Lq <= Lk), the queries aligned to the end of the keys
+    (query i sees keys <= Lk - Lq + i), written into o [Lq, Hq, D] fp16.
+    Heads and dims of every tensor contiguous; token strides free (multiples
+    of 8)."""
     _require_gpu(q, k, v, o)
     for t, name in ((q, "q"), (k, "k"), (v, "v"), (o, "o")):
         if t.dtype != torch.float16 or t.dim() != 3 or t.stride(2) != 1:

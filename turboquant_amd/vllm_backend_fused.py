@@ -289,10 +289,11 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
     def _attend(self, q, k, v, ctx, out=None):
         """q [ql, Hq, D] over k, v [ctx + ql, Hkv, D] (fp16), causal with the
         queries at the end of the keys (lower-right alignment).  Head size
-        128: this library's prefill kernel (tq_prefill_attention), written
-        into `out` when given (fp16 [ql, Hq, D]); other head sizes: torch's
-        fused flash kernel with grouped heads (no expanded K/V, no mask)."""
-        if self.head_size == 128:
+        64 or 128: this library's prefill kernel (tq_prefill_attention),
+        written into `out` when given (fp16 [ql, Hq, D]); other head sizes:
+        torch's fused flash kernel with grouped heads (no expanded K/V, no
+        mask)."""
+        if self.head_size in (64, 128):
             from . import ops
             if out is None or out.dtype != torch.float16:
                 out = torch.empty(q.shape, dtype=torch.float16, device=q.device)
