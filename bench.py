@@ -39,7 +39,7 @@ HBM_PEAK_GBS = 8000.0
 # tokens), from rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), each scale
 # taken from a 256 MiB device copy (profiles/decode_partials_cfg3_hbm_traffic.md);
 # keyed by (op, num_splits, kv_chunk_size) so an overridden layout reports null.
-PROFILED_TRAFFIC = {("balanced", 64, 512): 342085000, ("static", 64, 512): 342244000}
+PROFILED_TRAFFIC = {("balanced", 64, 512): 342079000, ("static", 64, 512): 342252000}
 TRAFFIC_SOURCE = ("profiled constant: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel at "
                   "this layout, profiles/decode_partials_cfg3_hbm_traffic.md")
 
