@@ -28,13 +28,14 @@
 //    reduction order is the C layout's row order; V^T is read in the same
 //    order).  O^T's C layout again gives each lane its own query row, so the
 //    online-softmax rescale is a per-lane scalar.
-//  * K tiles (64 or 128 keys) stream into LDS with direct-to-LDS 16-byte
-//    copies whose 16-byte chunks are XOR-swizzled by row (conflict-free A
-//    reads, issued four MFMAs ahead of their use); V tiles
-//    are loaded into registers one tile ahead and written transposed
-//    ([dim][key], padded rows) with v_perm_b32 and 8-byte LDS stores.  Two
-//    buffers of each (distinct LDS arrays, so the compiler does not wait for
-//    the copies in flight into the other buffer), one barrier per tile.
+//  * K and V tiles (64 or 128 keys) stream into LDS as rows with
+//    direct-to-LDS 16-byte copies, their 16-byte chunks XOR-swizzled by row:
+//    the K reads (16 bytes of one row per lane, issued four MFMAs ahead of
+//    their use) and the V transpose reads (ds_read_b64_tr_b16: four keys of
+//    one dim per lane, the V^T operand without a transposing copy) are
+//    conflict-free.  Two buffers of each (distinct LDS arrays, so the
+//    compiler does not wait for the copies in flight into the other buffer),
+//    one barrier per tile.
 //  * Online softmax in the exp2 domain with a lazy rescale (the running max
 //    moves only when a tile exceeds it by more than 8 / scale); probabilities
 //    enter the PV MFMA as fp16 (round to nearest), accumulation is fp32.
@@ -51,6 +52,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 // two floats as an fp16 pair, round to nearest even (one v_cvt_pk_f16_f32)
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
@@ -89,12 +91,13 @@ void prefill_kernel(PrefillParams p) {
   constexpr int kCH = kD / 8;         // 16-byte chunks per K row
   constexpr int kRPC = 1024 / kKRow;  // K rows per 1 KB copy
   constexpr int kBM = 32 * NW;  // query rows per workgroup
-  constexpr int kVtRow = kBN * 2 + 8;  // bytes of one V^T row (kBN keys + 4 pad halves)
   constexpr int kNU = kBN / 32, kNS = kBN / 16;  // 32-key score blocks, 16-key PV steps
+  // 64-byte quarters of a row the V swizzle rotates over (D = 128: four; 64: two)
+  constexpr int kQS = kD == 128 ? 0 : 1;  // row % 4 >> kQS selects the quarter
   __shared__ __attribute__((aligned(16))) uint8_t kbuf0[kBN * kKRow];
   __shared__ __attribute__((aligned(16))) uint8_t kbuf1[kBN * kKRow];
-  __shared__ __attribute__((aligned(16))) uint8_t vt0[kD * kVtRow];
-  __shared__ __attribute__((aligned(16))) uint8_t vt1[kD * kVtRow];
+  __shared__ __attribute__((aligned(16))) uint8_t vbuf0[kBN * kKRow];
+  __shared__ __attribute__((aligned(16))) uint8_t vbuf1[kBN * kKRow];
 
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -120,17 +123,23 @@ void prefill_kernel(PrefillParams p) {
     }
   }
 
-  // K copies: copy j fills LDS bytes [1024 j, 1024 j + 1024) of a buffer =
-  // rows kRPC j .. kRPC j + kRPC - 1; lane l writes row kRPC j + l / kCH,
-  // physical chunk l % kCH, which holds logical chunk (l % kCH) ^ (row % kCH)
-  // of that key row.  Wave w issues copies j = w + NW i.
-  constexpr int kKC = (kBN / kRPC) / NW;  // copies per wave and tile
-  const int kst_b = (int)(p.k_st * 2);
-  uint32_t koff[kKC];  // per-lane byte offsets of this wave's copies inside a tile
+  // K and V copies: copy j fills LDS bytes [1024 j, 1024 j + 1024) of a
+  // buffer = rows kRPC j .. kRPC j + kRPC - 1; lane l writes row
+  // kRPC j + l / kCH, physical 16-byte chunk l % kCH.  K rows hold logical
+  // chunk (l % kCH) ^ (row % kCH) there (the score MFMAs' A reads, 16 bytes
+  // of one row per lane, hit distinct chunks); V rows hold logical chunk
+  // (l % kCH) ^ 4 ((row % 4) >> kQS), which moves the 64-byte quarters of
+  // four consecutive rows apart for the transpose reads of the PV MFMAs (and
+  // lets their addresses be a per-lane base xor 64 d plus an immediate).
+  // Wave w issues copies j = w + NW i of both.
+  constexpr int kKC = (kBN / kRPC) / NW;  // copies per wave, tile and tensor
+  const int kst_b = (int)(p.k_st * 2), vst_b = (int)(p.v_st * 2);
+  uint32_t koff[kKC], voff[kKC];  // per-lane byte offsets of this wave's copies in a tile
 #pragma unroll
   for (int i = 0; i < kKC; i++) {
     const int j = w + NW * i, row = kRPC * j + lane / kCH;
     koff[i] = (uint32_t)(row * kst_b + (((lane % kCH) ^ (row % kCH)) * 16));
+    voff[i] = (uint32_t)(row * vst_b + (((lane % kCH) ^ (4 * ((row & 3) >> kQS))) * 16));
   }
   // buffer resource over rows [kb, Lk) of a K or V tile (wave-uniform base
   // and size; rows past Lk read as zeros)
@@ -145,50 +154,32 @@ void prefill_kernel(PrefillParams p) {
   };
   const _Float16* const kbase = p.k + (int64_t)g * p.k_sh;
   const _Float16* const vbase = p.v + (int64_t)g * p.v_sh;
-  auto issue_k = [&](int kt, uint8_t* buf) {
+  auto issue = [&](int kt, uint8_t* kb, uint8_t* vb) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the LDS-copy builtin has no host form
-    const __amdgpu_buffer_rsrc_t r = tile_rsrc(kbase, p.k_st, kt * kBN);
+    const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase, p.k_st, kt * kBN);
+    const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase, p.v_st, kt * kBN);
 #pragma unroll
-    for (int i = 0; i < kKC; i++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (void*)(buf + 1024 * (w + NW * i)), 16,
+    for (int i = 0; i < kKC; i++) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (void*)(kb + 1024 * (w + NW * i)), 16,
                                                koff[i], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (void*)(vb + 1024 * (w + NW * i)), 16,
+                                               voff[i], 0, 0, 0);
+    }
 #else
     (void)kt;
-    (void)buf;
+    (void)kb;
+    (void)vb;
 #endif
   };
-  // V: thread (w, lane) loads keys 4a .. 4a+3 x dims 8b .. 8b+7 of a tile
-  // (b = 4 (w % kDW) + lane % 4, a = lane / 4 + 16 (w / kDW), kDW = D / 32
-  // waves per 64 keys), then writes them transposed; waves with a >= kBN/4
-  // skip it (at D = 128: four waves cover a 64-key tile, and with eight
-  // waves the other four skip it: spreading it over all eight, 4 keys x 4
-  // dims a lane, measured 2% slower; eight cover a 128-key tile)
-  constexpr int kDW = kD / 32;
-  const bool vmover = w / kDW < kBN / 64;
-  const int va = (lane >> 2) + 16 * (w / kDW), vb = 4 * (w % kDW) + (lane & 3);
-  const int vst_b = (int)(p.v_st * 2);
-  u32x4 vr[4];
-  auto load_v = [&](int kt) {
-    if (!vmover) return;
-    const __amdgpu_buffer_rsrc_t r = tile_rsrc(vbase, p.v_st, kt * kBN);
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            r, (uint32_t)((4 * va + i) * vst_b + 16 * vb), 0, 0));
-  };
-  auto store_vt = [&](uint8_t* vt) {
-    if (!vmover) return;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {  // dims 8vb + 2e, 8vb + 2e + 1
-      const uint32_t lo01 = __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x05040100u);
-      const uint32_t lo23 = __builtin_amdgcn_perm(vr[3][e], vr[2][e], 0x05040100u);
-      const uint32_t hi01 = __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x07060302u);
-      const uint32_t hi23 = __builtin_amdgcn_perm(vr[3][e], vr[2][e], 0x07060302u);
-      uint8_t* d = vt + (8 * vb + 2 * e) * kVtRow + 8 * va;
-      *reinterpret_cast<u32x2*>(d) = u32x2{lo01, lo23};
-      *reinterpret_cast<u32x2*>(d + kVtRow) = u32x2{hi01, hi23};
-    }
-  };
+  // PV transpose reads (ds_read_b64_tr_b16): in each 16-lane group gq, source
+  // lane s reads 4 halves V[K0 + s/4][D0 + 4 (s % 4) .. +3] and result lane i
+  // receives V^T[D0 + i][K0 .. K0 + 3] (D0 = 32 d + 16 (gq % 2), K0 = 16 st +
+  // 4 hh, plus 8 for the second read): the A operand of O^T = V^T P^T.
+  // vread_base is this lane's byte offset for d = 0, st = 0.
+  const int vgq = lane >> 4, vsl = lane & 15, vt4 = vsl >> 2;
+  const uint32_t vread_base =
+      (uint32_t)((4 * hh + vt4) * kKRow +
+                 ((2 * (vgq & 1) + ((vsl & 3) >> 1)) ^ (4 * (vt4 >> kQS))) * 16 + 8 * (vsl & 1));
 
   f32x16 oacc[kD / 32];
 #pragma unroll
@@ -290,9 +281,13 @@ void prefill_kernel(PrefillParams p) {
       const int key0 = 16 * st + 4 * hh;
 #pragma unroll
       for (int d = 0; d < kD / 32; d++) {
-        const uint8_t* vr0 = vt + (32 * d + n) * kVtRow + 2 * key0;
-        const u32x2 a0 = *reinterpret_cast<const u32x2*>(vr0);
-        const u32x2 a1 = *reinterpret_cast<const u32x2*>(vr0 + 16);
+        typedef __attribute__((address_space(3))) uint8_t lds_u8;
+        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+        lds_u8* const pd = (lds_u8*)vt + (vread_base ^ (uint32_t)(64 * d)) + 16 * st * kKRow;
+        const u32x2 a0 =
+            __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)pd));
+        const u32x2 a1 = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(pd + 8 * kKRow)));
         const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
         oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), pB[st],
                                                          oacc[d], 0, 0, 0);
@@ -300,30 +295,19 @@ void prefill_kernel(PrefillParams p) {
     }
   };
 
-  if (ntiles > 0) {
-    issue_k(0, kbuf0);
-    load_v(0);
-  }
+  if (ntiles > 0) issue(0, kbuf0, vbuf0);
   for (int kt = 0; kt < ntiles; kt += 2) {
     // tile kt: buffers 0
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): copies and loads of tile kt
-    store_vt(vt0);
-    __syncthreads();
-    if (kt + 1 < ntiles) {
-      issue_k(kt + 1, kbuf1);
-      load_v(kt + 1);
-    }
-    tile(kt, kbuf0, vt0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of tile kt
+    __syncthreads();                     // everyone's copies of tile kt
+    if (kt + 1 < ntiles) issue(kt + 1, kbuf1, vbuf1);
+    tile(kt, kbuf0, vbuf0);
     if (kt + 1 >= ntiles) break;
     // tile kt + 1: buffers 1
     __builtin_amdgcn_s_waitcnt(0x0f70);
-    store_vt(vt1);
     __syncthreads();
-    if (kt + 2 < ntiles) {
-      issue_k(kt + 2, kbuf0);
-      load_v(kt + 2);
-    }
-    tile(kt + 1, kbuf1, vt1);
+    if (kt + 2 < ntiles) issue(kt + 2, kbuf0, vbuf0);
+    tile(kt + 1, kbuf1, vbuf1);
   }
 
   // o = O / sum, lane (hh, n) holds dims 32d + 8jq + 4hh + 0..3 of row qrow
