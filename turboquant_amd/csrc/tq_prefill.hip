@@ -278,7 +278,6 @@ void prefill_kernel(PrefillParams p) {
     // 8 + 4hh + 0..3} (the C-layout rows of the lane's probabilities)
 #pragma unroll
     for (int st = 0; st < kNS; st++) {
-      const int key0 = 16 * st + 4 * hh;
 #pragma unroll
       for (int d = 0; d < kD / 32; d++) {
         typedef __attribute__((address_space(3))) uint8_t lds_u8;
