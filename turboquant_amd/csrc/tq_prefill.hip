@@ -169,6 +169,9 @@ void prefill_kernel(PrefillParams p) {
     (void)kt;
     (void)kb;
     (void)vb;
+    (void)tile_rsrc;
+    (void)kbase;
+    (void)vbase;
 #endif
   };
   // PV transpose reads (ds_read_b64_tr_b16): in each 16-lane group gq, source
