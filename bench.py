@@ -412,6 +412,33 @@ def bench_prefill_kernel(torch, seq_len=32768):
                           "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "flops": flops,
                           "torch_flash_us": round(ms_t * 1e3, 1),
                           "config": f"one {L}-token prompt, causal, 16q/4kv/64 fp16"}
+    del q, k, v, o, qt, kt, vt
+    # a short chunk over a long context (the keys split over workgroups),
+    # beside the same kernel without the split (no workspace)
+    from turboquant_amd import _lib
+    lib = _lib.load()
+    hq, hkv, d, lq = 32, 8, 128, 256
+    q = torch.randn((lq, hq, d), generator=g, device=dev).half()
+    k = torch.randn((L, hkv, d), generator=g, device=dev).half()
+    v = torch.randn((L, hkv, d), generator=g, device=dev).half()
+    o = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(d)
+    flops = 4 * hq * d * (lq * L - lq * (lq - 1) // 2)
+    ms = time_launches(torch, lambda: ops.prefill_attention(q, k, v, o, scale), 20, 3)
+
+    def unsplit():
+        _lib.check(lib.tq_prefill_attention(
+            q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+            v.data_ptr(), v.stride(0), v.stride(1), o.data_ptr(), o.stride(0), o.stride(1), lq, L,
+            hq, hkv, d, scale, torch.cuda.current_stream().cuda_stream), "prefill_attention")
+    ms_u = time_launches(torch, unsplit, 20, 3)
+    tf = flops / (ms * 1e-3) / 1e12
+    res["short_chunk"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                          "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "flops": flops,
+                          "unsplit_us": round(ms_u * 1e3, 1),
+                          "workspace_bytes": int(lib.tq_prefill_workspace_bytes(lq, L, hq, hkv, d)),
+                          "config": f"a {lq}-token chunk over {L} keys, causal, 32q/8kv/128 fp16, "
+                                    "keys split over workgroups and merged"}
     return res
 
 

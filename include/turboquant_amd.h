@@ -240,6 +240,28 @@ int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_h
                          tq_stream_t stream);
 
 /*
+ * tq_prefill_attention with a caller-owned workspace (no counterpart in the
+ * reference, whose flash-attn call allocates its own): when the grid of
+ * query blocks would leave CUs idle (a short chunk over a long context),
+ * the keys of each query block are split over several workgroups, whose
+ * unnormalised results (fp32 O plus the reference max and row sum of every
+ * row) go to `workspace` and are merged by a second kernel on the same
+ * stream.  tq_prefill_workspace_bytes gives the size the current device's
+ * plan needs (0: no split); with a null or smaller workspace the call runs
+ * unsplit (same result).  The workspace must be 16-byte aligned; calls that
+ * overlap on one workspace race.
+ */
+int tq_prefill_attention_ws(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                            const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                            const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                            void* o, int64_t o_stride_tok, int64_t o_stride_head,
+                            int32_t q_len, int32_t kv_len, int32_t num_qo_heads,
+                            int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                            void* workspace, int64_t workspace_bytes, tq_stream_t stream);
+int64_t tq_prefill_workspace_bytes(int32_t q_len, int32_t kv_len, int32_t num_qo_heads,
+                                   int32_t num_kv_heads, int32_t head_dim);
+
+/*
  * Diagnostic, no counterpart in the reference: tq_decode_partials at head
  * size 128 with 8 kv heads per workgroup (the configs[2] geometry) with parts
  * compiled out.  mode 1: the attention math (the same page walk, LDS copy

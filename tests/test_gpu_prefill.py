@@ -41,6 +41,9 @@ CASES = [
     # 256-row workgroups (q heads x 256-row blocks >= the CU count)
     (2085, 3000, 32, 8),
     (2048, 2048, 128, 16),
+    # short chunks over long contexts: keys split over workgroups, then merged
+    (256, 20000, 32, 8),
+    (17, 9000, 8, 2),
 ]
 # head size 64 (the configs[3] geometry: 16 q / 4 kv heads), both shapes
 CASES64 = [
@@ -96,7 +99,38 @@ def test_prefill_strided_rows_and_heavy_tails(lq, lk):
     assert (err <= 2e-3 + 1e-2 * ref.abs()).all(), f"max err {err.max().item():.3e}"
 
 
-@pytest.mark.parametrize("lq,lk", [(256, 512), (2048, 2300)])
+def test_prefill_split_plan_and_agreement():
+    """The split-KV plan engages for a short chunk over a long context (the
+    workspace query is positive) and gives what the unsplit kernel gives
+    (tq_prefill_attention without a workspace), within fp16 rounding of the
+    merged outputs; both within the float64 tolerance."""
+    print("case: prefill split vs unsplit lq=300 lk=16384", flush=True)
+    from turboquant_amd import _lib, ops
+    lib = _lib.load()
+    lq, lk, hq, hkv, d = 300, 16384, 32, 8, 128
+    assert lib.tq_prefill_workspace_bytes(lq, lk, hq, hkv, d) > 0
+    assert lib.tq_prefill_workspace_bytes(8192, 8192, hq, hkv, d) == 0  # full grid: no split
+    g = torch.Generator(device=DEV).manual_seed(21)
+    q = torch.randn((lq, hq, d), generator=g, device=DEV).half()
+    k = torch.randn((lk, hkv, d), generator=g, device=DEV).half()
+    v = torch.randn((lk, hkv, d), generator=g, device=DEV).half()
+    split = torch.empty_like(q)
+    ops.prefill_attention(q, k, v, split, 0.088)
+    whole = torch.empty_like(q)
+    rc = lib.tq_prefill_attention(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                                  k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
+                                  v.stride(1), whole.data_ptr(), whole.stride(0), whole.stride(1),
+                                  lq, lk, hq, hkv, d, 0.088,
+                                  torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "prefill_attention")
+    torch.cuda.synchronize()
+    assert (split.float() - whole.float()).abs().max().item() <= 2e-3
+    ref = ref_attention(q, k, v, 0.088)
+    for o in (split, whole):
+        assert ((o.double() - ref).abs() <= 2e-3 + 1e-2 * ref.abs()).all()
+
+
+@pytest.mark.parametrize("lq,lk", [(256, 512), (2048, 2300), (256, 8192)])
 def test_prefill_graph_replay_matches_eager(lq, lk):
     print(f"case: prefill graph replay lq={lq} lk={lk}", flush=True)
     from turboquant_amd import ops

@@ -21,7 +21,7 @@ HEADER = os.path.join(ROOT, "include", "turboquant_amd.h")
 
 def _header_symbols():
     text = open(HEADER).read()
-    return set(re.findall(r"^(?:int|int32_t|const char\*)\s+(tq_\w+)\(", text, re.M))
+    return set(re.findall(r"^(?:int|int32_t|int64_t|const char\*)\s+(tq_\w+)\(", text, re.M))
 
 
 def test_geometry_table():
@@ -150,6 +150,13 @@ def test_cabi_argument_errors_without_gpu():
     rc = lib.tq_prefill_attention(null, 0, 0, null, 0, 0, null, 0, 0, null, 0, 0, 5, 4, 32, 8,
                                   128, 0.1, null)
     assert rc == -22 and b"q_len" in lib.tq_last_error()
+    # prefill workspace query: invalid shapes need none
+    assert lib.tq_prefill_workspace_bytes(0, 10, 32, 8, 128) == 0
+    assert lib.tq_prefill_workspace_bytes(10, 5, 32, 8, 128) == 0
+    assert lib.tq_prefill_workspace_bytes(10, 100, 32, 8, 96) == 0
+    rc = lib.tq_prefill_attention_ws(null, 0, 0, null, 0, 0, null, 0, 0, null, 0, 0, 4, 4, 32, 8,
+                                     96, 0.1, null, 0, null)
+    assert rc == -22 and b"head_dim" in lib.tq_last_error()
     # an empty batch is a no-op that succeeds
     assert lib.tq_combine_splits(null, null, 0, 1, 32, 128, null, null, null) == 0
     # the stream-read diagnostic: null source, size not a multiple of 16

@@ -45,6 +45,10 @@ SIGNATURES = {
                                 _P, _I64, _P]),
     "tq_prefill_attention": (_I32, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64,
                                     _I64, _I32, _I32, _I32, _I32, _I32, _F32, _P]),
+    "tq_prefill_attention_ws": (_I32, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P,
+                                       _I64, _I64, _I32, _I32, _I32, _I32, _I32, _F32, _P, _I64,
+                                       _P]),
+    "tq_prefill_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_abi_version": (_I32, []),
 }

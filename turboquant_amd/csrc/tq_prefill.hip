@@ -36,6 +36,10 @@
 //    conflict-free.  Two buffers of each (distinct LDS arrays, so the
 //    compiler does not wait for the copies in flight into the other buffer),
 //    one barrier per tile.
+//  * Short chunks over long contexts (too few query blocks to fill the
+//    CUs): each query block's tiles are split over several workgroups
+//    (grid z), which leave unnormalised O, reference max and row sum in a
+//    caller-owned workspace; prefill_merge_kernel combines them.
 //  * Online softmax in the exp2 domain with a lazy rescale (the running max
 //    moves only when a tile exceeds it by more than 8 / scale); probabilities
 //    enter the PV MFMA as fp16 (round to nearest), accumulation is fp32.
@@ -53,6 +57,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
 
 // two floats as an fp16 pair, round to nearest even (one v_cvt_pk_f16_f32)
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
@@ -69,6 +74,12 @@ struct PrefillParams {
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;  // strides in elements
   int lq, lk, ratio, nqb;
   float c;  // sm_scale * log2(e)
+  // split-KV mode: workgroup z of a (head, query block) covers its tiles
+  // [z tps, (z + 1) tps) and leaves unnormalised O and (reference max in
+  // log2 units, row sum) per row in the workspace for prefill_merge_kernel
+  int nsplit, tps;
+  float* ws_o;   // [nsplit][lq][Hq][D]
+  float* ws_ml;  // [nsplit][lq][Hq][2]
 };
 
 // max / sum of x over lanes l and l ^ 32: v_permlane32_swap of x with
@@ -84,7 +95,7 @@ __device__ __forceinline__ float sum32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int kD, int NW, int kBN>
+template <int kD, int NW, int kBN, bool SPLIT>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(PrefillParams p) {
   constexpr int kKRow = kD * 2;       // bytes of one K row in LDS
@@ -297,19 +308,44 @@ void prefill_kernel(PrefillParams p) {
     }
   };
 
-  if (ntiles > 0) issue(0, kbuf0, vbuf0);
-  for (int kt = 0; kt < ntiles; kt += 2) {
+  // this workgroup's tiles: all of them, or split z's share
+  int t0 = 0, t1 = ntiles;
+  if constexpr (SPLIT) {
+    t0 = (int)blockIdx.z * p.tps;
+    t1 = min(ntiles, t0 + p.tps);
+  }
+  if (t0 < t1) issue(t0, kbuf0, vbuf0);
+  for (int kt = t0; kt < t1; kt += 2) {
     // tile kt: buffers 0
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of tile kt
     __syncthreads();                     // everyone's copies of tile kt
-    if (kt + 1 < ntiles) issue(kt + 1, kbuf1, vbuf1);
+    if (kt + 1 < t1) issue(kt + 1, kbuf1, vbuf1);
     tile(kt, kbuf0, vbuf0);
-    if (kt + 1 >= ntiles) break;
+    if (kt + 1 >= t1) break;
     // tile kt + 1: buffers 1
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
-    if (kt + 2 < ntiles) issue(kt + 2, kbuf0, vbuf0);
+    if (kt + 2 < t1) issue(kt + 2, kbuf0, vbuf0);
     tile(kt + 1, kbuf1, vbuf1);
+  }
+
+  if constexpr (SPLIT) {
+    // unnormalised O (relative to the reference max mc) and (mc, row sum);
+    // a split that held no visible key leaves mc = -inf, sum 0, O = 0
+    lsum = sum32(lsum);
+    if (qrow < p.lq) {
+      const int64_t r = ((int64_t)blockIdx.z * p.lq + qrow) * gridDim.x + head;
+      float* const wo = p.ws_o + r * kD + 4 * hh;
+#pragma unroll
+      for (int d = 0; d < kD / 32; d++)
+#pragma unroll
+        for (int jq = 0; jq < 4; jq++)
+          *reinterpret_cast<float4_t*>(wo + 32 * d + 8 * jq) =
+              float4_t{oacc[d][4 * jq], oacc[d][4 * jq + 1], oacc[d][4 * jq + 2],
+                       oacc[d][4 * jq + 3]};
+      if (hh == 0) *reinterpret_cast<f32x2*>(p.ws_ml + 2 * r) = f32x2{mc, lsum};
+    }
+    return;
   }
 
   // o = O / sum, lane (hh, n) holds dims 32d + 8jq + 4hh + 0..3 of row qrow
@@ -328,13 +364,55 @@ void prefill_kernel(PrefillParams p) {
   }
 }
 
-// the two workgroup shapes, at head size 64 or 128
+// Merge of the splits of split-KV mode: one wave per (query row, q head),
+// o = sum_z 2^(mc_z - M) O_z / sum_z 2^(mc_z - M) l_z, fp16 out.
+template <int kD>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p, int hq) {
+  constexpr int V = kD / 64;  // dims per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t idx = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // row * hq + head
+  if (idx >= (int64_t)p.lq * hq) return;
+  const int row = (int)(idx / hq), head = (int)(idx % hq);
+  const int64_t zs = (int64_t)p.lq * hq;  // rows of one split
+  float mx = -INFINITY;
+  for (int z = 0; z < p.nsplit; z++) mx = fmaxf(mx, p.ws_ml[2 * (z * zs + idx)]);
+  float den = 0.0f, acc[V];
+#pragma unroll
+  for (int i = 0; i < V; i++) acc[i] = 0.0f;
+  for (int z = 0; z < p.nsplit; z++) {
+    const f32x2 ml = *reinterpret_cast<const f32x2*>(p.ws_ml + 2 * (z * zs + idx));
+    if (ml[0] == -INFINITY) continue;  // no visible key in this split
+    const float wgt = __builtin_amdgcn_exp2f(ml[0] - mx);
+    den += wgt * ml[1];
+    const float* const src = p.ws_o + (z * zs + idx) * kD + V * lane;
+#pragma unroll
+    for (int i = 0; i < V; i++) acc[i] += wgt * src[i];
+  }
+  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+  _Float16* const op = p.o + (int64_t)row * p.o_st + (int64_t)head * p.o_sh + V * lane;
+#pragma unroll
+  for (int i = 0; i < V; i++) op[i] = (_Float16)(acc[i] * inv);
+}
+
+// the workgroup shapes, at head size 64 or 128: eight waves, 128-key tiles;
+// four waves, 64-key tiles; four waves split over the keys (then merged)
 template <int D>
 hipError_t launch_prefill(int nw, int heads, hipStream_t st, const PrefillParams& p) {
-  if (nw == 8)
-    hipLaunchKernelGGL((prefill_kernel<D, 8, 128>), dim3(heads, p.nqb), dim3(512), 0, st, p);
-  else
-    hipLaunchKernelGGL((prefill_kernel<D, 4, 64>), dim3(heads, p.nqb), dim3(256), 0, st, p);
+  if (nw == 8) {
+    hipLaunchKernelGGL((prefill_kernel<D, 8, 128, false>), dim3(heads, p.nqb), dim3(512), 0, st,
+                       p);
+  } else if (p.nsplit <= 1) {
+    hipLaunchKernelGGL((prefill_kernel<D, 4, 64, false>), dim3(heads, p.nqb), dim3(256), 0, st,
+                       p);
+  } else {
+    hipLaunchKernelGGL((prefill_kernel<D, 4, 64, true>), dim3(heads, p.nqb, p.nsplit), dim3(256),
+                       0, st, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t waves = (int64_t)p.lq * heads;
+    hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)((waves + 3) / 4)), dim3(256),
+                       0, st, p, heads);
+  }
   return hipGetLastError();
 }
 
@@ -350,16 +428,59 @@ int device_cus() {
   return c;
 }
 
+// Launch plan of one call: the workgroup shape and, when the grid would
+// leave CUs idle (short chunks over long contexts), a split of the keys.
+struct PrefillPlan {
+  int nw = 4, nqb = 0, nsplit = 1, tps = 0;
+  int64_t ws_bytes = 0;  // workspace the split needs (0: none)
+};
+PrefillPlan plan_prefill(int q_len, int kv_len, int heads, int head_dim) {
+  PrefillPlan sp;
+  const int cus = device_cus();
+  const int64_t nqb8 = (q_len + 255) / 256;
+  if ((int64_t)heads * nqb8 >= (int64_t)cus) {
+    // 256-row workgroups (8 waves, one per CU) when they still give every CU one
+    sp.nw = 8;
+    sp.nqb = (int)nqb8;
+    return sp;
+  }
+  // else 128-row workgroups (4 waves, two per CU); with fewer than two per
+  // CU, the keys of each query block are split so that the grid fills the
+  // chip, each split at least 8 tiles (512 keys)
+  sp.nqb = (q_len + 127) / 128;
+  const int64_t wgs = (int64_t)heads * sp.nqb;
+  const int ntl = (kv_len + 63) / 64;  // tiles of the last (longest) query block
+  if (cus > 0 && wgs < 2LL * cus && ntl >= 16) {
+    int64_t S = (2LL * cus + wgs - 1) / wgs;
+    if (S > ntl / 8) S = ntl / 8;
+    if (S > 64) S = 64;
+    if (S >= 2) {
+      sp.tps = (int)((ntl + S - 1) / S);
+      sp.nsplit = (ntl + sp.tps - 1) / sp.tps;
+      sp.ws_bytes = (int64_t)sp.nsplit * q_len * heads * (head_dim + 2) * 4;
+    }
+  }
+  return sp;
+}
+
 }  // namespace
 }  // namespace tq
 
-extern "C" int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
-                                    const void* k, int64_t k_stride_tok, int64_t k_stride_head,
-                                    const void* v, int64_t v_stride_tok, int64_t v_stride_head,
-                                    void* o, int64_t o_stride_tok, int64_t o_stride_head,
-                                    int32_t q_len, int32_t kv_len, int32_t num_qo_heads,
-                                    int32_t num_kv_heads, int32_t head_dim, float sm_scale,
-                                    tq_stream_t stream) {
+extern "C" int64_t tq_prefill_workspace_bytes(int32_t q_len, int32_t kv_len, int32_t num_qo_heads,
+                                              int32_t num_kv_heads, int32_t head_dim) {
+  if (q_len <= 0 || kv_len < q_len || num_qo_heads <= 0 || num_kv_heads <= 0 ||
+      (head_dim != 64 && head_dim != 128))
+    return 0;
+  (void)num_kv_heads;
+  return tq::plan_prefill(q_len, kv_len, num_qo_heads, head_dim).ws_bytes;
+}
+
+extern "C" int tq_prefill_attention_ws(
+    const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
+    int64_t k_stride_tok, int64_t k_stride_head, const void* v, int64_t v_stride_tok,
+    int64_t v_stride_head, void* o, int64_t o_stride_tok, int64_t o_stride_head, int32_t q_len,
+    int32_t kv_len, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+    void* workspace, int64_t workspace_bytes, tq_stream_t stream) {
   using namespace tq;
   if (head_dim != 64 && head_dim != 128) {
     set_error("prefill_attention: head_dim %d unsupported (64 or 128 only)", head_dim);
@@ -414,16 +535,34 @@ extern "C" int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
   p.lk = kv_len;
   p.ratio = num_qo_heads / num_kv_heads;
   p.c = sm_scale * 1.4426950408889634f;
-  // 256-row workgroups (8 waves, one per CU) when they still give every CU
-  // one, else 128-row workgroups (4 waves, two per CU)
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int64_t nqb8 = (q_len + 255) / 256;
-  if ((int64_t)num_qo_heads * nqb8 >= (int64_t)device_cus()) {
-    p.nqb = (int)nqb8;
-    return (int)(head_dim == 64 ? launch_prefill<64>(8, num_qo_heads, st, p)
-                                : launch_prefill<128>(8, num_qo_heads, st, p));
+  const PrefillPlan sp = plan_prefill(q_len, kv_len, num_qo_heads, head_dim);
+  p.nqb = sp.nqb;
+  p.nsplit = 1;
+  p.tps = 0;
+  p.ws_o = p.ws_ml = nullptr;
+  // the split runs only with a workspace that holds it (else one workgroup
+  // per query block, the same result)
+  if (sp.nsplit > 1 && workspace && workspace_bytes >= sp.ws_bytes &&
+      ((uintptr_t)workspace & 15) == 0) {
+    p.nsplit = sp.nsplit;
+    p.tps = sp.tps;
+    p.ws_o = static_cast<float*>(workspace);
+    p.ws_ml = p.ws_o + (int64_t)sp.nsplit * q_len * num_qo_heads * head_dim;
   }
-  p.nqb = (q_len + 127) / 128;
-  return (int)(head_dim == 64 ? launch_prefill<64>(4, num_qo_heads, st, p)
-                              : launch_prefill<128>(4, num_qo_heads, st, p));
+  return (int)(head_dim == 64 ? launch_prefill<64>(sp.nw, num_qo_heads, st, p)
+                              : launch_prefill<128>(sp.nw, num_qo_heads, st, p));
+}
+
+extern "C" int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                    const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                                    const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                                    void* o, int64_t o_stride_tok, int64_t o_stride_head,
+                                    int32_t q_len, int32_t kv_len, int32_t num_qo_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                                    tq_stream_t stream) {
+  return tq_prefill_attention_ws(q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head,
+                                 v, v_stride_tok, v_stride_head, o, o_stride_tok, o_stride_head,
+                                 q_len, kv_len, num_qo_heads, num_kv_heads, head_dim, sm_scale,
+                                 nullptr, 0, stream);
 }

@@ -227,11 +227,17 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torc
         raise RuntimeError("prefill_attention: q/k/v/o shapes disagree")
     lib = _lib.load()
     with torch.cuda.device(q.device):
-        rc = lib.tq_prefill_attention(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
-                                      k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
-                                      v.stride(1), o.data_ptr(), o.stride(0), o.stride(1),
-                                      int(lq), int(lk), int(hq), int(hkv), int(d),
-                                      float(sm_scale), _stream_ptr(q.device))
+        # a short chunk over a long context splits its keys over workgroups;
+        # the split's workspace comes from torch's allocator (graph-safe)
+        nbytes = int(lib.tq_prefill_workspace_bytes(int(lq), int(lk), int(hq), int(hkv), int(d)))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes > 0 else None
+        rc = lib.tq_prefill_attention_ws(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                                         k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
+                                         v.stride(1), o.data_ptr(), o.stride(0), o.stride(1),
+                                         int(lq), int(lk), int(hq), int(hkv), int(d),
+                                         float(sm_scale),
+                                         ws.data_ptr() if ws is not None else None, nbytes,
+                                         _stream_ptr(q.device))
     _lib.check(rc, "prefill_attention")
     return o
 

@@ -360,8 +360,10 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
           reference attends the fresh chunk only and so drops the cached
           context; its decode path already attends over the dequantized
           cache, which this extends to chunks.
-        Attention runs in this library's prefill kernel (head size 128) or
-        torch's fused flash kernel with grouped kv heads (other sizes).
+        Attention runs in this library's prefill kernel (head sizes 64 and
+        128; short chunks over long contexts split their keys over
+        workgroups) or torch's fused flash kernel with grouped kv heads
+        (other sizes).
         """
         from . import ops
         self._ensure_kernels_loaded()
