@@ -244,7 +244,7 @@ int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_h
  * reference, whose flash-attn call allocates its own): when the grid of
  * query blocks would leave CUs idle (a short chunk over a long context),
  * the keys of each query block are split over several workgroups, whose
- * unnormalised results (fp32 O plus the reference max and row sum of every
+ * results (fp16 O / row sum plus the reference max and row sum of every
  * row) go to `workspace` and are merged by a second kernel on the same
  * stream.  tq_prefill_workspace_bytes gives the size the current device's
  * plan needs (0: no split); with a null or smaller workspace the call runs

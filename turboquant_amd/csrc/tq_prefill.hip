@@ -75,11 +75,12 @@ struct PrefillParams {
   int lq, lk, ratio, nqb;
   float c;  // sm_scale * log2(e)
   // split-KV mode: workgroup z of a (head, query block) covers its tiles
-  // [z tps, (z + 1) tps) and leaves unnormalised O and (reference max in
-  // log2 units, row sum) per row in the workspace for prefill_merge_kernel
+  // [z tps, (z + 1) tps) and leaves its rows' O / row sum (fp16) and
+  // (reference max in log2 units, row sum) in the workspace for
+  // prefill_merge_kernel
   int nsplit, tps;
-  float* ws_o;   // [nsplit][lq][Hq][D]
-  float* ws_ml;  // [nsplit][lq][Hq][2]
+  _Float16* ws_o;  // [nsplit][lq][Hq][D]
+  float* ws_ml;    // [nsplit][lq][Hq][2]
 };
 
 // max / sum of x over lanes l and l ^ 32: v_permlane32_swap of x with
@@ -330,19 +331,22 @@ void prefill_kernel(PrefillParams p) {
   }
 
   if constexpr (SPLIT) {
-    // unnormalised O (relative to the reference max mc) and (mc, row sum);
-    // a split that held no visible key leaves mc = -inf, sum 0, O = 0
+    // this split's O / row sum (a convex combination of V rows: fp16 is
+    // safe) and (mc, row sum); a split that held no visible key for a row
+    // leaves mc = -inf, sum 0, O = 0
     lsum = sum32(lsum);
     if (qrow < p.lq) {
       const int64_t r = ((int64_t)blockIdx.z * p.lq + qrow) * gridDim.x + head;
-      float* const wo = p.ws_o + r * kD + 4 * hh;
+      const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+      _Float16* const wo = p.ws_o + r * kD + 4 * hh;
 #pragma unroll
       for (int d = 0; d < kD / 32; d++)
 #pragma unroll
-        for (int jq = 0; jq < 4; jq++)
-          *reinterpret_cast<float4_t*>(wo + 32 * d + 8 * jq) =
-              float4_t{oacc[d][4 * jq], oacc[d][4 * jq + 1], oacc[d][4 * jq + 2],
-                       oacc[d][4 * jq + 3]};
+        for (int jq = 0; jq < 4; jq++) {
+          const uint32_t lo = pack_h2(oacc[d][4 * jq] * inv, oacc[d][4 * jq + 1] * inv);
+          const uint32_t hi = pack_h2(oacc[d][4 * jq + 2] * inv, oacc[d][4 * jq + 3] * inv);
+          *reinterpret_cast<u32x2*>(wo + 32 * d + 8 * jq) = u32x2{lo, hi};
+        }
       if (hh == 0) *reinterpret_cast<f32x2*>(p.ws_ml + 2 * r) = f32x2{mc, lsum};
     }
     return;
@@ -365,7 +369,7 @@ void prefill_kernel(PrefillParams p) {
 }
 
 // Merge of the splits of split-KV mode: one wave per (query row, q head),
-// o = sum_z 2^(mc_z - M) O_z / sum_z 2^(mc_z - M) l_z, fp16 out.
+// o = sum_z w_z (O_z / l_z) / sum_z w_z, w_z = 2^(mc_z - M) l_z, fp16 out.
 template <int kD>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p, int hq) {
   constexpr int V = kD / 64;  // dims per lane
@@ -382,11 +386,11 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p, int
   for (int z = 0; z < p.nsplit; z++) {
     const f32x2 ml = *reinterpret_cast<const f32x2*>(p.ws_ml + 2 * (z * zs + idx));
     if (ml[0] == -INFINITY) continue;  // no visible key in this split
-    const float wgt = __builtin_amdgcn_exp2f(ml[0] - mx);
-    den += wgt * ml[1];
-    const float* const src = p.ws_o + (z * zs + idx) * kD + V * lane;
+    const float wgt = __builtin_amdgcn_exp2f(ml[0] - mx) * ml[1];
+    den += wgt;
+    const _Float16* const src = p.ws_o + (z * zs + idx) * kD + V * lane;
 #pragma unroll
-    for (int i = 0; i < V; i++) acc[i] += wgt * src[i];
+    for (int i = 0; i < V; i++) acc[i] += wgt * (float)src[i];
   }
   const float inv = den > 0.0f ? 1.0f / den : 0.0f;
   _Float16* const op = p.o + (int64_t)row * p.o_st + (int64_t)head * p.o_sh + V * lane;
@@ -457,7 +461,7 @@ PrefillPlan plan_prefill(int q_len, int kv_len, int heads, int head_dim) {
     if (S >= 2) {
       sp.tps = (int)((ntl + S - 1) / S);
       sp.nsplit = (ntl + sp.tps - 1) / sp.tps;
-      sp.ws_bytes = (int64_t)sp.nsplit * q_len * heads * (head_dim + 2) * 4;
+      sp.ws_bytes = (int64_t)sp.nsplit * q_len * heads * (head_dim * 2 + 8);
     }
   }
   return sp;
@@ -540,15 +544,17 @@ extern "C" int tq_prefill_attention_ws(
   p.nqb = sp.nqb;
   p.nsplit = 1;
   p.tps = 0;
-  p.ws_o = p.ws_ml = nullptr;
+  p.ws_o = nullptr;
+  p.ws_ml = nullptr;
   // the split runs only with a workspace that holds it (else one workgroup
   // per query block, the same result)
   if (sp.nsplit > 1 && workspace && workspace_bytes >= sp.ws_bytes &&
       ((uintptr_t)workspace & 15) == 0) {
     p.nsplit = sp.nsplit;
     p.tps = sp.tps;
-    p.ws_o = static_cast<float*>(workspace);
-    p.ws_ml = p.ws_o + (int64_t)sp.nsplit * q_len * num_qo_heads * head_dim;
+    p.ws_o = static_cast<_Float16*>(workspace);
+    p.ws_ml = reinterpret_cast<float*>(p.ws_o + (int64_t)sp.nsplit * q_len * num_qo_heads *
+                                                    head_dim);
   }
   return (int)(head_dim == 64 ? launch_prefill<64>(sp.nw, num_qo_heads, st, p)
                               : launch_prefill<128>(sp.nw, num_qo_heads, st, p));
