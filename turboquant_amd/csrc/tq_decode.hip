@@ -437,7 +437,10 @@ struct SoftmaxState {
 // configs[3] (B = 64 ragged): head size 256 with 2 kv heads 174 -> 158 us and
 // head size 128 with 4 kv heads 170 -> 146 us with 16 copies; head size 64
 // with 4 kv heads 97 -> 109 us, so it keeps 32, as does the 8-head group of
-// configs[2] (its two workgroups per CU are already bound by the ring).
+// configs[2] (its two workgroups per CU are already bound by the ring); 8
+// copies at head size 256, 2 kv heads, compiled for three waves per SIMD (168
+// VGPRs, five workgroups per CU instead of four) measured 166.5 against
+// 147 us: the lookups' bank conflicts cost more than the occupancy gains.
 __host__ __device__ constexpr int lut_copies(int pd, int g) {
   return pd == 64 || (pd == 128 && g == 8) ? 32 : 16;
 }
