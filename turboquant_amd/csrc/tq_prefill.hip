@@ -38,11 +38,12 @@
 //    one barrier per tile.
 //  * Short chunks over long contexts (too few query blocks to fill the
 //    CUs): each query block's tiles are split over several workgroups
-//    (grid z), which leave unnormalised O, reference max and row sum in a
-//    caller-owned workspace; prefill_merge_kernel combines them.
+//    (grid z), which leave their normalised O (fp16), reference max and row
+//    sum in a caller-owned workspace; prefill_merge_kernel combines them.
 //  * Online softmax in the exp2 domain with a lazy rescale (the running max
 //    moves only when a tile exceeds it by more than 8 / scale); probabilities
-//    enter the PV MFMA as fp16 (round to nearest), accumulation is fp32.
+//    enter the PV MFMA as fp16 (round to nearest), accumulation is fp32;
+//    at head size 64 the row sum is taken from those fp16 values.
 #include <atomic>
 
 #include "tq_common.h"
@@ -281,12 +282,21 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
           pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[u][8 * t + i], p.c, -mc));
-          lsum += pr[i];
+          if constexpr (kD != 64) lsum += pr[i];
         }
         u32x4 pk;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-          pk[i] = pack_h2(pr[2 * i], pr[2 * i + 1]);
+        for (int i = 0; i < 4; i++) {
+          const half2_t h = __builtin_convertvector(f32x2{pr[2 * i], pr[2 * i + 1]}, half2_t);
+          // head size 64 (two scores per MFMA, the softmax weighs more): the
+          // row sum of the fp16 probabilities the PV MFMAs take, two per
+          // v_dot2 against (1, 1) with an fp32 accumulator.  (Dot2 of an
+          // element extracted from a u32x4 miscompiled here: the same source
+          // register for all four; the sum reads the half2 values.)
+          if constexpr (kD == 64)
+            lsum = __builtin_amdgcn_fdot2(h, half2_t{(_Float16)1.0f, (_Float16)1.0f}, lsum, false);
+          pk[i] = __builtin_bit_cast(uint32_t, h);
+        }
         pB[2 * u + t] = __builtin_bit_cast(half8_t, pk);
       }
     // O^T += V^T P^T: k-step (u, t) reduces keys 32u + 16t + {4hh + 0..3,
