@@ -436,7 +436,9 @@ struct SoftmaxState {
 // l + 16 may share a bank) so that more workgroups fit a CU.  Measured on
 // configs[3] (B = 64 ragged): head size 256 with 2 kv heads 174 -> 158 us and
 // head size 128 with 4 kv heads 170 -> 146 us with 16 copies; head size 64
-// with 4 kv heads 97 -> 109 us, so it keeps 32, as does the 8-head group of
+// with 4 kv heads 97 -> 109 us (re-measured with the current kernel: head
+// size 256 160.5 -> 150 us with 16 copies, head size 64 90 -> 109 us), so
+// head size 64 keeps 32, as does the 8-head group of
 // configs[2] (its two workgroups per CU are already bound by the ring); 8
 // copies at head size 256, 2 kv heads, compiled for three waves per SIMD (168
 // VGPRs, five workgroups per CU instead of four) measured 166.5 against
