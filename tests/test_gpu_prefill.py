@@ -51,6 +51,8 @@ CASES64 = [
     (129, 400, 16, 4),
     (1000, 1000, 16, 4),
     (4100, 4500, 16, 4),
+    # short chunk over a long context: keys split over workgroups, then merged
+    (256, 8000, 16, 4),
 ]
 
 
