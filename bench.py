@@ -179,7 +179,7 @@ def cpu_baseline(torch, w):
     write = the configs[1] write as whole-tensor torch ops.  One warm-up run,
     then the median of 5, on the host cores in this process."""
     from oracle import torch_ref
-    from tests import workloads as W
+    from turboquant_amd import workloads as W
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     torch.set_num_threads(threads)
     cache = w["cache"].cpu()
@@ -217,16 +217,15 @@ def bench_ragged(torch, steps, warmup):
     op against the reference's max_len-based static splits, same cache."""
     import numpy as np
 
-    from tests import gpu_cases as G
-    from tests import workloads as W
+    from turboquant_amd import workloads as W
     from turboquant_amd import ops
     from turboquant_amd.geometry import choose_splits, hadamard_signs
     out = []
     lens = np.random.default_rng(4).integers(1024, 32768 + 1, size=64)
     for hd in (128, 64, 256):
         hq, hkv = {64: (16, 4), 128: (32, 8), 256: (16, 2)}[hd]
-        case, cache, pd = G.device_case(4 + 1000 * hd, lens, hq, hkv, hd, k_dist="t3")
-        d = G.decode_inputs(case, pd)
+        case, cache, pd = W.device_case(4 + 1000 * hd, lens, hq, hkv, hd, k_dist="t3")
+        d = W.decode_inputs(case, pd)
         b = len(lens)
         dev = cache.device
         signs = hadamard_signs(pd, dev)
@@ -285,7 +284,7 @@ def bench_write(torch, steps, warmup):
     (2 kv heads); graph-timed, algorithmic bytes as in workloads."""
     import numpy as np
 
-    from tests import workloads as W
+    from turboquant_amd import workloads as W
     from turboquant_amd import ops
     from turboquant_amd.geometry import hadamard_signs
     dev = torch.device("cuda:0")

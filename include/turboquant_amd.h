@@ -218,7 +218,7 @@ int tq_dequant_paged(const uint8_t* k_slab, const uint8_t* v_slab,
                      tq_stream_t stream);
 
 /*
- * Causal GQA attention of a prefill chunk over fp16 K/V (head_dim 64 or 128):
+ * Causal GQA attention of a prefill chunk over fp16 K/V (head_dim 64, 128 or 256):
  * o[i, h] = softmax_j(q[i, h] . k[j, h / r] * sm_scale) v[j, h / r] over keys
  * j <= (kv_len - q_len) + i, r = num_qo_heads / num_kv_heads.  q, o: fp16
  * element (i, h, d) at base + i*stride_tok + h*stride_head + d; k, v: fp16

@@ -61,7 +61,7 @@ def kat_rows(hd: int, rng) -> np.ndarray:
 
 def main():
     import oracle
-    from tests import workloads as W
+    from turboquant_amd import workloads as W
     oracle.build()
     signs = signs_fixture()
     with open(os.path.join(HERE, "signs.json"), "w") as f:

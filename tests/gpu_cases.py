@@ -8,34 +8,21 @@ import torch
 from turboquant_amd import ops
 from turboquant_amd.geometry import choose_splits, hadamard_signs
 
-from . import workloads as W
+from turboquant_amd import workloads as W
 
 DEV = torch.device("cuda:0")
 
 
-def build_cache(case, block=W.BLOCK):
-    hkv, hd = case["num_kv_heads"], case["head_dim"]
-    shape, pd = W.cache_bytes(case["num_blocks"], hkv, hd)
-    cache = torch.zeros(shape, dtype=torch.uint8, device=DEV)
-    k = torch.from_numpy(case["k"]).to(DEV)
-    v = torch.from_numpy(case["v"]).to(DEV)
-    if k.shape[0]:
-        ops.quantize_write_kv_cache(cache, k, v, hadamard_signs(pd, DEV),
-                                    torch.from_numpy(case["slots"]).to(DEV), hd, pd)
-    return cache, pd
+def build_cache(case):
+    return W.build_cache(case, DEV)
 
 
 def decode_inputs(case, pd):
-    """Device tensors of a case: padded q, strided page table, seq_lens."""
-    q = case["q"]
-    b, hq, hd = q.shape
-    qp = np.zeros((b, hq, pd), np.float16)
-    qp[:, :, :hd] = q
-    bt = torch.from_numpy(case["block_table"]).to(DEV)
-    return dict(
-        qp=qp, q=torch.from_numpy(qp).to(DEV), indices=bt.reshape(-1).contiguous(),
-        indptr=(torch.arange(b + 1, dtype=torch.int32, device=DEV) * bt.shape[1]).contiguous(),
-        seq=torch.from_numpy(np.asarray(case["seq_lens"], np.int32)).to(DEV))
+    return W.decode_inputs(case, pd, DEV)
+
+
+def device_case(seed, seq_lens, hq, hkv, hd, k_dist="normal", chunk_tokens=1 << 16):
+    return W.device_case(seed, seq_lens, hq, hkv, hd, k_dist, chunk_tokens, DEV)
 
 
 def run_balanced(case, cache, pd, signs=True, rows=None):
@@ -101,40 +88,6 @@ def assert_close(got, ref, what=""):
     bad = err > lim
     assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} outside atol {ATOL} / "
                            f"rtol {RTOL}; max abs err {err.max():.3e}")
-
-
-def device_case(seed, seq_lens, hq, hkv, hd, k_dist="normal", chunk_tokens=1 << 16):
-    """A decode case too large for host-generated K/V: q, page table and slot
-    mapping from numpy (seeded), K/V drawn on the GPU (seeded torch generator;
-    K ~ Student-t(3) for k_dist "t3") and written through the write kernel,
-    whose bytes are pinned against the oracle by the write tests.  Returns
-    (case, cache, pd); case has no "k"/"v"."""
-    rng = np.random.default_rng(seed)
-    seq_lens = np.asarray(seq_lens, np.int32)
-    b = len(seq_lens)
-    q = rng.standard_normal((b, hq, hd)).astype(np.float16)
-    bt, slots, nb = W.paged_layout(rng, seq_lens)
-    shape, pd = W.cache_bytes(nb, hkv, hd)
-    cache = torch.zeros(shape, dtype=torch.uint8, device=DEV)
-    g = torch.Generator(device=DEV)
-    g.manual_seed(seed)
-    signs = hadamard_signs(pd, DEV)
-    st = torch.from_numpy(slots).to(DEV)
-    for a in range(0, len(slots), chunk_tokens):
-        n = min(chunk_tokens, len(slots) - a)
-        if k_dist == "t3":
-            # Student-t(3) = N(0,1) / sqrt(chi2_3 / 3), chi2_3 = sum of 3 squared normals
-            z = torch.randn((n, hkv, hd), generator=g, device=DEV)
-            c2 = torch.randn((3, n, hkv, hd), generator=g, device=DEV).square().sum(0)
-            k = (z / torch.sqrt(c2 / 3.0)).half()
-        else:
-            k = torch.randn((n, hkv, hd), generator=g, device=DEV).half()
-        v = torch.randn((n, hkv, hd), generator=g, device=DEV).half()
-        ops.quantize_write_kv_cache(cache, k, v, signs, st[a:a + n], hd, pd)
-    torch.cuda.synchronize()
-    case = dict(q=q, slots=slots, block_table=bt, seq_lens=seq_lens, num_blocks=nb,
-                num_kv_heads=hkv, head_dim=hd)
-    return case, cache, pd
 
 
 def expected_plan(seq_lens, units):

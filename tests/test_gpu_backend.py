@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from tests import gpu_cases as G
-from tests import workloads as W
+from turboquant_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
 
@@ -85,7 +85,8 @@ def test_backend_prefill_fresh_attention():
 
 
 @pytest.mark.parametrize("hq,hkv,hd,cpu_copies", [(32, 8, 128, False), (8, 2, 64, False),
-                                                   (32, 8, 128, True)])
+                                                   (32, 8, 128, True), (16, 2, 256, False),
+                                                   (16, 2, 96, False)])
 def test_backend_mixed_batch_with_cached_context(hq, hkv, hd, cpu_copies):
     """A max_query_len > 1 batch: a fresh prompt, two chunks of longer prompts
     whose earlier tokens are already cached, and a decode row.  Chunks attend

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from tests import gpu_cases as G
-from tests import workloads as W
+from turboquant_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
 

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from tests import gpu_cases as G
-from tests import workloads as W
+from turboquant_amd import workloads as W
 from turboquant_amd import _lib
 from turboquant_amd.geometry import hadamard_signs
 

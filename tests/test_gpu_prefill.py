@@ -56,8 +56,20 @@ CASES64 = [
 ]
 
 
+# head size 256 (the configs[3] geometry: 16 q / 2 kv heads): one shape, split
+# and unsplit
+CASES256 = [
+    (1, 1, 16, 2),
+    (129, 400, 16, 2),
+    (1000, 1000, 16, 2),
+    (2100, 2500, 16, 2),
+    (256, 8000, 16, 2),
+    (17, 9000, 8, 2),
+]
+
+
 @pytest.mark.parametrize("lq,lk,hq,hkv,d", [c + (128,) for c in CASES] +
-                         [c + (64,) for c in CASES64])
+                         [c + (64,) for c in CASES64] + [c + (256,) for c in CASES256])
 def test_prefill_matches_float64(lq, lk, hq, hkv, d):
     print(f"case: prefill lq={lq} lk={lk} hq={hq} hkv={hkv} d={d}", flush=True)
     from turboquant_amd import ops
@@ -154,3 +166,47 @@ def test_prefill_graph_replay_matches_eager(lq, lk):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(o, eager)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_prefill_split_workspace_rows_without_visible_keys(d):
+    """Split mode, where a split's tiles can lie wholly beyond a query row's
+    last key: such rows must leave a finite workspace entry (O = 0, row sum
+    0, max -inf) rather than NaN, and the merged output stays within the
+    float64 tolerance.  The workspace is the caller's, so it is read back."""
+    print(f"case: prefill split workspace, masked splits d={d}", flush=True)
+    from turboquant_amd import _lib
+    lib = _lib.load()
+    # 2 q heads: 8 query blocks of 128 rows, 65 key tiles split 8 ways (9
+    # tiles each); the keys start 3088 = 16 mod 32 before the chunk, so the
+    # split starting at key 3456 begins inside the 32 rows of one wave (rows
+    # 352..367 see none of its keys, rows 368..383 do)
+    lq, lk, hq, hkv = 1024, 4112, 2, 1
+    nbytes = int(lib.tq_prefill_workspace_bytes(lq, lk, hq, hkv, d))
+    assert nbytes > 0
+    g = torch.Generator(device=DEV).manual_seed(31 + d)
+    q = torch.randn((lq, hq, d), generator=g, device=DEV).half()
+    k = torch.randn((lk, hkv, d), generator=g, device=DEV).half()
+    v = torch.randn((lk, hkv, d), generator=g, device=DEV).half()
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=DEV)  # NaN pattern
+    o = torch.empty((lq, hq, d), dtype=torch.float16, device=DEV)
+    rc = lib.tq_prefill_attention_ws(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                                     k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
+                                     v.stride(1), o.data_ptr(), o.stride(0), o.stride(1),
+                                     lq, lk, hq, hkv, d, 0.05, ws.data_ptr(), nbytes,
+                                     torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "prefill_attention_ws")
+    torch.cuda.synchronize()
+    per_split = lq * hq * (2 * d + 8)
+    nsplit = nbytes // per_split
+    assert nsplit * per_split == nbytes and nsplit >= 2
+    wo = ws[:nsplit * lq * hq * d * 2].view(torch.float16).view(nsplit, lq, hq, d)
+    ml = ws[nsplit * lq * hq * d * 2:].view(torch.float32).view(nsplit, lq, hq, 2)
+    assert torch.isfinite(wo).all()
+    masked = ml[..., 0] == float("-inf")
+    assert masked.any(), "no split without visible keys: the case does not test it"
+    assert (ml[..., 1][masked] == 0).all()
+    assert (wo[masked] == 0).all()
+    assert torch.isfinite(ml[..., 1]).all()
+    ref = ref_attention(q, k, v, 0.05)
+    assert ((o.double() - ref).abs() <= 2e-3 + 1e-2 * ref.abs()).all()

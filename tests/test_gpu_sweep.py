@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from tests import gpu_cases as G
-from tests import workloads as W
+from turboquant_amd import workloads as W
 from tests.test_gpu_write import _diff_report, _gpu_cache, _oracle_cache
 
 pytestmark = pytest.mark.gpu

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import oracle
-from tests import workloads as W
+from turboquant_amd import workloads as W
 from turboquant_amd import ops
 from turboquant_amd.geometry import hadamard_signs
 

@@ -140,7 +140,7 @@ def test_cabi_argument_errors_without_gpu():
     assert rc == -22 and lib.tq_last_error()
     rc = lib.tq_combine_splits(null, null, 1, 0, 32, 128, null, null, null)
     assert rc == -22
-    # prefill attention: head size 64 or 128 only, GQA ratio must divide, q_len <= kv_len
+    # prefill attention: head size 64, 128 or 256 only, GQA ratio must divide, q_len <= kv_len
     rc = lib.tq_prefill_attention(null, 0, 0, null, 0, 0, null, 0, 0, null, 0, 0, 4, 4, 32, 8,
                                   96, 0.1, null)
     assert rc == -22 and b"head_dim" in lib.tq_last_error()
@@ -295,3 +295,36 @@ def test_impl_hadamard_helpers_match_the_matrix(hd):
     assert got.dtype == q.dtype and torch.allclose(got, want, rtol=0, atol=1e-5)
     back = impl._hadamard_inverse(got)
     assert torch.allclose(back, q, rtol=0, atol=1e-5)
+
+
+def test_balanced_op_schema_declares_its_writes():
+    """decode_paged_balanced_ws writes o_ws, the partial rows, the LSEs and
+    the row table: its schema marks them (a!)..(d!) and returns nothing, and
+    an exported, functionalized graph keeps the call, with the caller's use
+    of o_ws reading the op's written value (so neither is dead code)."""
+    from turboquant_amd import ops
+    ops.register_ops()
+    op = torch.ops.turboquant_v5.decode_paged_balanced_ws
+    sch = op.default._schema
+    written = {a.name for a in sch.arguments if a.alias_info is not None and a.alias_info.is_write}
+    assert written == {"o_ws", "partition_o_ws", "partition_lse_ws", "split_indptr"}
+    assert len(sch.returns) == 0
+
+    class Step(torch.nn.Module):
+        def forward(self, q, cache, i, sl, o, po, pl, si, signs):
+            op(q, cache, i, i, sl, 8, 128, 128, 0.1, signs, o, po, pl, si)
+            return o * 2
+
+    args = (torch.empty(8, 32, 128, dtype=torch.float16),
+            torch.empty(2, 10, 16, 8, 80, dtype=torch.uint8), torch.empty(10, dtype=torch.int32),
+            torch.empty(10, dtype=torch.int32), torch.empty(8, 32, 128, dtype=torch.float16),
+            torch.empty(16, 32, 128), torch.empty(16, 32), torch.empty(10, dtype=torch.int32),
+            torch.empty(128))
+    ep = torch.export.export(Step(), args).run_decompositions()
+    nodes = list(ep.graph.nodes)
+    fn = [n for n in nodes if n.op == "call_function" and "auto_functionalized" in str(n.target)]
+    assert len(fn) == 1, ep.graph_module.code
+    mul = [n for n in nodes if n.op == "call_function" and "mul" in str(n.target)]
+    assert len(mul) == 1
+    src = mul[0].args[0]  # getitem of the functionalized op: o_ws as written
+    assert src.op == "call_function" and src.args[0] is fn[0], ep.graph_module.code

@@ -28,7 +28,7 @@ from scipy.linalg import hadamard
 
 import oracle
 from tests import npref
-from tests import workloads as W
+from turboquant_amd import workloads as W
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 

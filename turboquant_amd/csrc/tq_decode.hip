@@ -273,10 +273,12 @@ __device__ __forceinline__ int wave_max_i(int v) {
   r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
   return max((int)r[0], (int)r[1]);
 }
-// ceil(a / d) for 0 <= a < 2^24, d > 0: a float estimate (off by at most one
-// for these ranges) corrected both ways in integers
+// ceil(a / d) for a >= 0, d > 0, a + d < 2^31: below 2^24 a float estimate
+// (off by at most one there) corrected both ways in integers; from 2^24 on
+// (a sequence of 16M tokens or more) an integer division
 __device__ __forceinline__ int ceil_div_est(int a, int d, float rd) {
   const int x = a + d - 1;
+  if (x >= (1 << 24)) return x / d;
   int f = (int)((float)x * rd);
   f -= (f * d > x) ? 1 : 0;
   f += ((f + 1) * d <= x) ? 1 : 0;

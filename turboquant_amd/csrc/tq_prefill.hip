@@ -1,5 +1,5 @@
 // tq_prefill.hip -- causal GQA flash attention of a prefill chunk (fp16 K/V,
-// head size 64 or 128).
+// head size 64, 128 or 256).
 //
 // Semantics: o[i, h] = softmax_j(q[i, h] . k[j, h / ratio] * sm_scale) v[j, h / ratio]
 // over keys j <= (Lk - Lq) + i (causal, aligned to the end of the keys: a
@@ -97,16 +97,20 @@ __device__ __forceinline__ float sum32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int kD, int NW, int kBN, bool SPLIT>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// WPE: waves per SIMD the register budget is sized for (2 at head size 64
+// and 128; 1 at 256, whose q operand and output accumulators alone take 192
+// registers per lane)
+template <int kD, int NW, int kBN, bool SPLIT, int WPE = 2>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void prefill_kernel(PrefillParams p) {
   constexpr int kKRow = kD * 2;       // bytes of one K row in LDS
   constexpr int kCH = kD / 8;         // 16-byte chunks per K row
   constexpr int kRPC = 1024 / kKRow;  // K rows per 1 KB copy
   constexpr int kBM = 32 * NW;  // query rows per workgroup
   constexpr int kNU = kBN / 32, kNS = kBN / 16;  // 32-key score blocks, 16-key PV steps
-  // 64-byte quarters of a row the V swizzle rotates over (D = 128: four; 64: two)
-  constexpr int kQS = kD == 128 ? 0 : 1;  // row % 4 >> kQS selects the quarter
+  // 64-byte quarters of a row the V swizzle rotates over (D >= 128: four;
+  // 64: two)
+  constexpr int kQS = kD >= 128 ? 0 : 1;  // row % 4 >> kQS selects the quarter
   __shared__ __attribute__((aligned(16))) uint8_t kbuf0[kBN * kKRow];
   __shared__ __attribute__((aligned(16))) uint8_t kbuf1[kBN * kKRow];
   __shared__ __attribute__((aligned(16))) uint8_t vbuf0[kBN * kKRow];
@@ -273,6 +277,12 @@ void prefill_kernel(PrefillParams p) {
       m = m_new;
       mc = m_new * p.c;
     }
+    // a row with no visible key yet (possible in split mode, where a split's
+    // first tiles can lie wholly beyond a row) keeps mc = -inf while the
+    // wave's ballot above may fire for other rows: its exponent offset is
+    // then 0, so its probabilities are exp2(-inf) = 0 instead of NaN, and
+    // the split leaves sum 0 and O = 0 for it
+    const float mce = mc == -INFINITY ? 0.0f : mc;
     half8_t pB[kNS];  // B operand of O^T = V^T P^T for k-steps (u, t)
 #pragma unroll
     for (int u = 0; u < kNU; u++)
@@ -281,7 +291,7 @@ void prefill_kernel(PrefillParams p) {
         float pr[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-          pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[u][8 * t + i], p.c, -mc));
+          pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[u][8 * t + i], p.c, -mce));
           if constexpr (kD != 64) lsum += pr[i];
         }
         u32x4 pk;
@@ -409,10 +419,26 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p, int
 }
 
 // the workgroup shapes, at head size 64 or 128: eight waves, 128-key tiles;
-// four waves, 64-key tiles; four waves split over the keys (then merged)
+// four waves, 64-key tiles; four waves split over the keys (then merged).
+// Head size 256: four waves, 64-key tiles (128 KB of LDS for the K and V
+// double buffers), one wave per SIMD, split or not.
 template <int D>
 hipError_t launch_prefill(int nw, int heads, hipStream_t st, const PrefillParams& p) {
-  if (nw == 8) {
+  if constexpr (D == 256) {
+    (void)nw;
+    if (p.nsplit <= 1) {
+      hipLaunchKernelGGL((prefill_kernel<D, 4, 64, false, 1>), dim3(heads, p.nqb), dim3(256), 0,
+                         st, p);
+    } else {
+      hipLaunchKernelGGL((prefill_kernel<D, 4, 64, true, 1>), dim3(heads, p.nqb, p.nsplit),
+                         dim3(256), 0, st, p);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const int64_t waves = (int64_t)p.lq * heads;
+      hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)((waves + 3) / 4)), dim3(256),
+                         0, st, p, heads);
+    }
+  } else if (nw == 8) {
     hipLaunchKernelGGL((prefill_kernel<D, 8, 128, false>), dim3(heads, p.nqb), dim3(512), 0, st,
                        p);
   } else if (p.nsplit <= 1) {
@@ -452,14 +478,14 @@ PrefillPlan plan_prefill(int q_len, int kv_len, int heads, int head_dim) {
   PrefillPlan sp;
   const int cus = device_cus();
   const int64_t nqb8 = (q_len + 255) / 256;
-  if ((int64_t)heads * nqb8 >= (int64_t)cus) {
+  if (head_dim != 256 && (int64_t)heads * nqb8 >= (int64_t)cus) {
     // 256-row workgroups (8 waves, one per CU) when they still give every CU one
     sp.nw = 8;
     sp.nqb = (int)nqb8;
     return sp;
   }
-  // else 128-row workgroups (4 waves, two per CU); with fewer than two per
-  // CU, the keys of each query block are split so that the grid fills the
+  // else 128-row workgroups (4 waves, two per CU; one at head size 256);
+  // with fewer than two per CU, the keys of each query block are split so that the grid fills the
   // chip, each split at least 8 tiles (512 keys)
   sp.nqb = (q_len + 127) / 128;
   const int64_t wgs = (int64_t)heads * sp.nqb;
@@ -483,7 +509,7 @@ PrefillPlan plan_prefill(int q_len, int kv_len, int heads, int head_dim) {
 extern "C" int64_t tq_prefill_workspace_bytes(int32_t q_len, int32_t kv_len, int32_t num_qo_heads,
                                               int32_t num_kv_heads, int32_t head_dim) {
   if (q_len <= 0 || kv_len < q_len || num_qo_heads <= 0 || num_kv_heads <= 0 ||
-      (head_dim != 64 && head_dim != 128))
+      (head_dim != 64 && head_dim != 128 && head_dim != 256))
     return 0;
   (void)num_kv_heads;
   return tq::plan_prefill(q_len, kv_len, num_qo_heads, head_dim).ws_bytes;
@@ -496,8 +522,8 @@ extern "C" int tq_prefill_attention_ws(
     int32_t kv_len, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale,
     void* workspace, int64_t workspace_bytes, tq_stream_t stream) {
   using namespace tq;
-  if (head_dim != 64 && head_dim != 128) {
-    set_error("prefill_attention: head_dim %d unsupported (64 or 128 only)", head_dim);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) {
+    set_error("prefill_attention: head_dim %d unsupported (64, 128 or 256 only)", head_dim);
     return kEinval;
   }
   if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads != 0) {
@@ -566,8 +592,9 @@ extern "C" int tq_prefill_attention_ws(
     p.ws_ml = reinterpret_cast<float*>(p.ws_o + (int64_t)sp.nsplit * q_len * num_qo_heads *
                                                     head_dim);
   }
-  return (int)(head_dim == 64 ? launch_prefill<64>(sp.nw, num_qo_heads, st, p)
-                              : launch_prefill<128>(sp.nw, num_qo_heads, st, p));
+  if (head_dim == 64) return (int)launch_prefill<64>(sp.nw, num_qo_heads, st, p);
+  if (head_dim == 128) return (int)launch_prefill<128>(sp.nw, num_qo_heads, st, p);
+  return (int)launch_prefill<256>(sp.nw, num_qo_heads, st, p);
 }
 
 extern "C" int tq_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,

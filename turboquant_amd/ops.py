@@ -213,7 +213,7 @@ def decode_paged_balanced(q: torch.Tensor, kv_cache: torch.Tensor, indices: torc
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                       sm_scale: float) -> torch.Tensor:
     """Causal GQA attention of q [Lq, Hq, D] over k, v [Lk, Hkv, D] (fp16,
-    D = 64 or 128, Lq <= Lk), the queries aligned to the end of the keys
+    D = 64, 128 or 256, Lq <= Lk), the queries aligned to the end of the keys
     (query i sees keys <= Lk - Lq + i), written into o [Lq, Hq, D] fp16.
     Heads and dims of every tensor contiguous; token strides free (multiples
     of 8)."""
@@ -420,11 +420,22 @@ def decode_v5_from_cache(q, kv_cache, indices, indptr, last_page_len, seq_lens, 
                                 splits, chunk)
 
 
+def _balanced_ws(q, kv_cache, indices, indptr, seq_lens, num_kv_heads, head_dim, padded_dim,
+                 sm_scale, hadamard_signs, o_ws, partition_o_ws, partition_lse_ws,
+                 split_indptr) -> None:
+    """turboquant_v5::decode_paged_balanced_ws: decode_paged_balanced, its
+    result in o_ws (the schema returns nothing)."""
+    decode_paged_balanced(q, kv_cache, indices, indptr, seq_lens, num_kv_heads, head_dim,
+                          padded_dim, sm_scale, hadamard_signs, o_ws, partition_o_ws,
+                          partition_lse_ws, split_indptr)
+
+
 def _register_fakes() -> None:
     """Meta ("fake") kernels, so that torch.compile and vLLM's graph capture
     can trace the ops without running them: the write mutates its cache
-    argument and returns nothing; the decode ops return a tensor shaped like
-    o_ws (fp16 [B, Hq, padded_dim])."""
+    argument and returns nothing; the reference's decode ops return a tensor
+    shaped like o_ws (fp16 [B, Hq, padded_dim]); the balanced op writes
+    o_ws, which its schema marks, and returns nothing."""
     from torch.library import register_fake
 
     @register_fake("turboquant_write::quantize_write_kv_cache", lib=_libs[0])
@@ -435,8 +446,14 @@ def _register_fakes() -> None:
         return q.new_empty((q.size(0), q.size(1), q.size(2)), dtype=torch.float16)
 
     for name in ("decode_v5_from_cache_paged_splitkv_ws", "decode_v5_from_cache_ws",
-                 "decode_v5_from_cache_splitkv_ws", "decode_paged_balanced_ws"):
+                 "decode_v5_from_cache_splitkv_ws"):
         register_fake(f"turboquant_v5::{name}", _decode_fake, lib=_libs[1])
+
+    @register_fake("turboquant_v5::decode_paged_balanced_ws", lib=_libs[1])
+    def _balanced_fake(q, kv_cache, indices, indptr, seq_lens, num_kv_heads, head_dim,
+                       padded_dim, sm_scale, hadamard_signs, o_ws, partition_o_ws,
+                       partition_lse_ws, split_indptr):
+        return None
 
 
 def register_ops() -> None:
@@ -479,11 +496,16 @@ def register_ops() -> None:
     d.impl("decode_v5_from_cache_splitkv_ws", _from_cache_splitkv_ws, "CUDA")
     # this build's balanced-split decode (no reference counterpart: the
     # reference plans splits on the host from max_len)
+    # it writes its result into o_ws, and the partial rows, LSEs and row table
+    # into the other workspaces, and says so in its schema (returning
+    # nothing: functionalization refuses aliased outputs of custom ops), so
+    # functionalization and torch.compile keep the call and its writes
     d.define("decode_paged_balanced_ws(Tensor q, Tensor kv_cache, Tensor indices, "
              "Tensor indptr, Tensor seq_lens, int num_kv_heads, int head_dim, "
-             "int padded_dim, float sm_scale, Tensor hadamard_signs, Tensor o_ws, "
-             "Tensor partition_o_ws, Tensor partition_lse_ws, Tensor split_indptr) -> Tensor")
-    d.impl("decode_paged_balanced_ws", decode_paged_balanced, "CUDA")
+             "int padded_dim, float sm_scale, Tensor hadamard_signs, Tensor(a!) o_ws, "
+             "Tensor(b!) partition_o_ws, Tensor(c!) partition_lse_ws, "
+             "Tensor(d!) split_indptr) -> ()")
+    d.impl("decode_paged_balanced_ws", _balanced_ws, "CUDA")
     _libs.extend([w, d])
     _register_fakes()
     _registered = True

@@ -288,28 +288,26 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
 
     def _attend(self, q, k, v, ctx, out=None):
         """q [ql, Hq, D] over k, v [ctx + ql, Hkv, D] (fp16), causal with the
-        queries at the end of the keys (lower-right alignment).  Head size
-        64 or 128: this library's prefill kernel (tq_prefill_attention),
-        written into `out` when given (fp16 [ql, Hq, D]); other head sizes:
-        torch's fused flash kernel with grouped heads (no expanded K/V, no
-        mask)."""
-        if self.head_size in (64, 128):
-            from . import ops
+        queries at the end of the keys (lower-right alignment), in this
+        library's prefill kernel (tq_prefill_attention).  Head sizes 64, 128
+        and 256 run as they are, written into `out` when given (fp16
+        [ql, Hq, D]); a head size below its padded size (96, 80, ...) runs
+        zero-padded to it: zero dims add nothing to q.k and give zero output
+        dims, which are dropped.  The reference runs flash-attn here for
+        every head size (vllm_backend_fused.py:335-371)."""
+        from . import ops
+        d, pd = self.head_size, self._pd
+        if pd > 256:
+            raise RuntimeError(f"prefill: head_size {d} unsupported (padded size {pd} > 256)")
+        if d == pd:
             if out is None or out.dtype != torch.float16:
                 out = torch.empty(q.shape, dtype=torch.float16, device=q.device)
             return ops.prefill_attention(q, k, v, out, self.scale)
-        from torch.nn.attention.bias import causal_lower_right
-        qt = q.transpose(0, 1).unsqueeze(0)
-        kt = k.transpose(0, 1).unsqueeze(0)
-        vt = v.transpose(0, 1).unsqueeze(0)
-        ql, kl = q.shape[0], k.shape[0]
-        if ctx == 0:
-            o = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True, scale=self.scale,
-                                               enable_gqa=True)
-        else:
-            o = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=causal_lower_right(ql, kl),
-                                               scale=self.scale, enable_gqa=True)
-        return o.squeeze(0).transpose(0, 1)
+        pad = (0, pd - d)
+        qp, kp, vp = F.pad(q, pad), F.pad(k, pad), F.pad(v, pad)
+        op = torch.empty(qp.shape, dtype=torch.float16, device=q.device)
+        ops.prefill_attention(qp, kp, vp, op, self.scale)
+        return op[:, :, :d]
 
     def _prefill_fresh(self, query, key, value, attn_metadata, output):
         """Causal attention of each prompt chunk over its own fresh K/V."""
@@ -360,10 +358,9 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
           reference attends the fresh chunk only and so drops the cached
           context; its decode path already attends over the dequantized
           cache, which this extends to chunks.
-        Attention runs in this library's prefill kernel (head sizes 64 and
-        128; short chunks over long contexts split their keys over
-        workgroups) or torch's fused flash kernel with grouped kv heads
-        (other sizes).
+        Attention runs in this library's prefill kernel (head sizes 64, 128
+        and 256, smaller sizes zero-padded to their padded size; short chunks
+        over long contexts split their keys over workgroups).
         """
         from . import ops
         self._ensure_kernels_loaded()
@@ -482,10 +479,12 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
                       and out3.is_contiguous())
             o_ws = out3 if direct else ws["o"]
             if self._decode_op_name == KERNEL_NAME:
-                result = self._decode_op(
+                # the op writes o_ws (declared in its schema) and returns nothing
+                self._decode_op(
                     q_fp16, kv_cache, kv_indices, kv_indptr, sl, self.num_kv_heads,
                     self.head_size, self._pd, self.scale, self._signs, o_ws,
                     ws["partition_o"], ws["partition_lse"], ws["split_indptr"])
+                result = o_ws
             else:
                 num_pages = (seq_lens + block_size - 1) // block_size
                 kv_last_page_len = seq_lens - (num_pages - 1) * block_size
@@ -495,7 +494,12 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
                     self._signs, self._qbytes, self._nbytes, o_ws, max_len,
                     ws["partition_o"], ws["partition_lse"], ws["request_indices"],
                     ws["kv_tile_indices"], ws["split_indptr"], ws["kv_chunk_size"], num_splits)
-            if not direct:
+            # the reference's op returns its result (o_ws itself when run
+            # eagerly, so no copy then; its schema declares no write)
+            if direct:
+                if result.data_ptr() != out3.data_ptr():
+                    out3.copy_(result[:num_actual])
+            else:
                 if self.head_size < self._pd:
                     out3.copy_(result[:num_actual, :, :self.head_size])
                 else:

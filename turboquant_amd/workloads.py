@@ -1,4 +1,5 @@
-"""Seeded synthetic inputs for the BASELINE configurations (numpy PCG64).
+"""Seeded synthetic workloads of the benchmark configurations (numpy PCG64),
+shared by bench.py and the tests.
 
 cfg1: q [1,32,128], K/V [1024,8,128] ~ N(0,1), seed 1, contiguous pages.
 cfg2: K/V [8192,8,128] ~ N(0,1) with 4 fixed outlier channels per head x20,
@@ -7,7 +8,8 @@ cfg3: q [8,32,128]; 8 x 32768 tokens of N(0,1) K/V; 16384 pages assigned by
       a seeded permutation, seed 3.
 cfg4: B=64, L ~ U[1024, 32768], K Student-t(3), V N(0,1), seed 4; also
       hd 64 (16q/4kv) and hd 256 (16q/2kv).
-All arrays are host numpy; the caller moves them to the device.
+The generators return host numpy arrays; build_cache, decode_inputs and
+device_case put a workload on a GPU through this package's write kernel.
 """
 from __future__ import annotations
 
@@ -116,3 +118,79 @@ def algorithmic_write_bytes(n: int, h: int, hd: int, in_bytes: int = 2) -> int:
     pd = max(64, 1 << (hd - 1).bit_length())
     per = pd // 2 + 2 * (pd // 64)
     return int(2 * n * h * hd * in_bytes + n * 4 + 2 * n * h * per)
+
+
+# ----------------------------------------------------------- on the device
+
+def build_cache(case, device="cuda:0"):
+    """The case's K/V written into a fresh cache on `device` by the write
+    kernel; returns (cache, padded_dim)."""
+    import torch
+
+    from . import ops
+    from .geometry import hadamard_signs
+    dev = torch.device(device)
+    hkv, hd = case["num_kv_heads"], case["head_dim"]
+    shape, pd = cache_bytes(case["num_blocks"], hkv, hd)
+    cache = torch.zeros(shape, dtype=torch.uint8, device=dev)
+    k = torch.from_numpy(case["k"]).to(dev)
+    v = torch.from_numpy(case["v"]).to(dev)
+    if k.shape[0]:
+        ops.quantize_write_kv_cache(cache, k, v, hadamard_signs(pd, dev),
+                                    torch.from_numpy(case["slots"]).to(dev), hd, pd)
+    return cache, pd
+
+
+def decode_inputs(case, pd, device="cuda:0"):
+    """Device tensors of a case: padded q, strided page table, seq_lens."""
+    import torch
+    dev = torch.device(device)
+    q = case["q"]
+    b, hq, hd = q.shape
+    qp = np.zeros((b, hq, pd), np.float16)
+    qp[:, :, :hd] = q
+    bt = torch.from_numpy(case["block_table"]).to(dev)
+    return dict(
+        qp=qp, q=torch.from_numpy(qp).to(dev), indices=bt.reshape(-1).contiguous(),
+        indptr=(torch.arange(b + 1, dtype=torch.int32, device=dev) * bt.shape[1]).contiguous(),
+        seq=torch.from_numpy(np.asarray(case["seq_lens"], np.int32)).to(dev))
+
+
+def device_case(seed, seq_lens, hq, hkv, hd, k_dist="normal", chunk_tokens=1 << 16,
+                device="cuda:0"):
+    """A decode case too large for host-generated K/V: q, page table and slot
+    mapping from numpy (seeded), K/V drawn on the GPU (seeded torch generator;
+    K ~ Student-t(3) for k_dist "t3") and written through the write kernel,
+    whose bytes are pinned against the oracle by the write tests.  Returns
+    (case, cache, pd); case has no "k"/"v"."""
+    import torch
+
+    from . import ops
+    from .geometry import hadamard_signs
+    dev = torch.device(device)
+    rng = np.random.default_rng(seed)
+    seq_lens = np.asarray(seq_lens, np.int32)
+    b = len(seq_lens)
+    q = rng.standard_normal((b, hq, hd)).astype(np.float16)
+    bt, slots, nb = paged_layout(rng, seq_lens)
+    shape, pd = cache_bytes(nb, hkv, hd)
+    cache = torch.zeros(shape, dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    signs = hadamard_signs(pd, dev)
+    st = torch.from_numpy(slots).to(dev)
+    for a in range(0, len(slots), chunk_tokens):
+        n = min(chunk_tokens, len(slots) - a)
+        if k_dist == "t3":
+            # Student-t(3) = N(0,1) / sqrt(chi2_3 / 3), chi2_3 = sum of 3 squared normals
+            z = torch.randn((n, hkv, hd), generator=g, device=dev)
+            c2 = torch.randn((3, n, hkv, hd), generator=g, device=dev).square().sum(0)
+            k = (z / torch.sqrt(c2 / 3.0)).half()
+        else:
+            k = torch.randn((n, hkv, hd), generator=g, device=dev).half()
+        v = torch.randn((n, hkv, hd), generator=g, device=dev).half()
+        ops.quantize_write_kv_cache(cache, k, v, signs, st[a:a + n], hd, pd)
+    torch.cuda.synchronize()
+    case = dict(q=q, slots=slots, block_table=bt, seq_lens=seq_lens, num_blocks=nb,
+                num_kv_heads=hkv, head_dim=hd)
+    return case, cache, pd
