@@ -394,24 +394,25 @@ def bench_prefill_kernel(torch, seq_len=32768):
            "config": f"one {L}-token prompt, causal, 32q/8kv/128 fp16 (configs[4] prefill "
                      "attention per layer)"}
     del q, k, v, o, qt, kt, vt
-    # the same prompt at head size 64 (configs[3]'s 16 q / 4 kv geometry)
-    hq, hkv, d = 16, 4, 64
-    q = torch.randn((L, hq, d), generator=g, device=dev).half()
-    k = torch.randn((L, hkv, d), generator=g, device=dev).half()
-    v = torch.randn((L, hkv, d), generator=g, device=dev).half()
-    o = torch.empty_like(q)
-    scale = 1.0 / math.sqrt(d)
-    flops = 4 * hq * d * (L * (L + 1) // 2)
-    ms = time_launches(torch, lambda: ops.prefill_attention(q, k, v, o, scale), 10, 2)
-    qt, kt, vt = (t.transpose(0, 1).unsqueeze(0) for t in (q, k, v))
-    ms_t = time_launches(torch, lambda: F.scaled_dot_product_attention(
-        qt, kt, vt, is_causal=True, scale=scale, enable_gqa=True), 10, 2)
-    tf = flops / (ms * 1e-3) / 1e12
-    res["head_dim_64"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
-                          "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "flops": flops,
-                          "torch_flash_us": round(ms_t * 1e3, 1),
-                          "config": f"one {L}-token prompt, causal, 16q/4kv/64 fp16"}
-    del q, k, v, o, qt, kt, vt
+    # the same prompt at head sizes 64 and 256 (configs[3]'s 16 q / 4 kv and
+    # 16 q / 2 kv geometries)
+    for hq, hkv, d in ((16, 4, 64), (16, 2, 256)):
+        q = torch.randn((L, hq, d), generator=g, device=dev).half()
+        k = torch.randn((L, hkv, d), generator=g, device=dev).half()
+        v = torch.randn((L, hkv, d), generator=g, device=dev).half()
+        o = torch.empty_like(q)
+        scale = 1.0 / math.sqrt(d)
+        flops = 4 * hq * d * (L * (L + 1) // 2)
+        ms = time_launches(torch, lambda: ops.prefill_attention(q, k, v, o, scale), 10, 2)
+        qt, kt, vt = (t.transpose(0, 1).unsqueeze(0) for t in (q, k, v))
+        ms_t = time_launches(torch, lambda: F.scaled_dot_product_attention(
+            qt, kt, vt, is_causal=True, scale=scale, enable_gqa=True), 10, 2)
+        tf = flops / (ms * 1e-3) / 1e12
+        res[f"head_dim_{d}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                                "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "flops": flops,
+                                "torch_flash_us": round(ms_t * 1e3, 1),
+                                "config": f"one {L}-token prompt, causal, {hq}q/{hkv}kv/{d} fp16"}
+        del q, k, v, o, qt, kt, vt
     # a short chunk over a long context (the keys split over workgroups),
     # beside the same kernel without the split (no workspace)
     from turboquant_amd import _lib

@@ -178,7 +178,8 @@ class Runner:
         self.out_buf = None
         self.step_idx = torch.zeros(1, dtype=torch.int64, device=dev)
         self.graph = None
-        self.probe = None  # list collecting (layer, q, out) of decode attention, eager only
+        # list collecting (layer, q, k, v, out) of decode attention, eager only
+        self.probe = None
 
     # ------------------------------------------------------------ layers
     def _attn_qkv(self, lw, x, cs):
@@ -261,7 +262,7 @@ class Runner:
             o = impl.forward(None, q2, k.reshape(self.batch, -1), v.reshape(self.batch, -1),
                              self.caches[li], meta)
             if self.probe is not None:
-                self.probe.append((li, q.clone(), o.clone()))
+                self.probe.append((li, q.clone(), k.clone(), v.clone(), o.clone()))
             x = x + F.linear(o, lw["o"])
             x = self._mlp(lw, x)
         nxt = greedy(self._logits(x))
@@ -319,6 +320,25 @@ class Runner:
         return self.out_buf[:steps]
 
     # ------------------------------------------------------- fp16 reference
+    @torch.no_grad()
+    def fp16_attention(self, li: int, q: torch.Tensor, k: torch.Tensor,
+                       v: torch.Tensor) -> torch.Tensor:
+        """Decode attention of layer li over fp16 K/V (no quantization): q
+        [B, Hq, D] of one decode step whose new token's k, v [B, Hkv, D] sit
+        at position pos - 1 (after the step), the earlier tokens from the
+        fp16 copies the prefill kept.  Equal sequence lengths only.
+        Returns [B, Hq, D] fp16."""
+        assert self.kv16 is not None
+        p = int(self.pos[0]) - 1
+        assert bool((self.pos == p + 1).all()), "fp16_attention needs equal lengths"
+        kvl = self.kv16[li]
+        kk = torch.cat([kvl[0, :, :, :p], k[:, :, None, :]], dim=2)
+        vv = torch.cat([kvl[1, :, :, :p], v[:, :, None, :]], dim=2)
+        o = F.scaled_dot_product_attention(q[:, :, None, :], kk, vv,
+                                           scale=1.0 / math.sqrt(self.shape.head_dim),
+                                           enable_gqa=True)
+        return o[:, :, 0, :]
+
     @torch.no_grad()
     def decode_fp16_reference(self, steps: int, forced: torch.Tensor | None = None,
                               kv: str = "fp16"):
@@ -391,6 +411,35 @@ class Runner:
             pos = pos + 1
         return out if forced is None else (out, rank)
 
+@torch.no_grad()
+def attention_vs_fp16(r: Runner) -> dict:
+    """The quantization error where it enters the model: one eager decode
+    step from the prefill's state, every layer's decode attention output
+    (fused kernel over the quantized cache) against attention over the fp16
+    K/V of the same step (Runner.fp16_attention); per (sequence, q head) row
+    the cosine similarity and the relative L2 error.  The decode state is
+    restored afterwards."""
+    pos0, tok0 = r.pos.clone(), r.tok.clone()
+    r.probe = []
+    r.decode_eager(1)
+    probe, r.probe = r.probe, None
+    cos, rel = [], []
+    for li, q, k, v, o in probe:
+        ref = r.fp16_attention(li, q, k, v).float().flatten(0, 1)
+        got = o.float().reshape(ref.shape)
+        cos.append(F.cosine_similarity(got, ref, dim=-1))
+        rel.append((got - ref).norm(dim=-1) / ref.norm(dim=-1).clamp_min(1e-30))
+    r.pos.copy_(pos0)
+    r.tok.copy_(tok0)
+    cos = torch.stack(cos)
+    rel = torch.stack(rel)
+    return {"layers": len(probe), "rows_per_layer": int(cos.shape[1]),
+            "cosine_min": round(cos.min().item(), 6), "cosine_mean": round(cos.mean().item(), 6),
+            "rel_l2_err_mean": round(rel.mean().item(), 6),
+            "rel_l2_err_max": round(rel.max().item(), 6),
+            "reference": "same step's attention over fp16 K/V (torch SDPA), no quantization"}
+
+
 def run(shape: ModelShape, batch: int = 8, prompt_len: int = 32768, new_tokens: int = 256,
         seed: int = 0, compare_steps: int = 0, device: str = "cuda:0", log=None) -> dict:
     """Prefill `batch` random prompts of `prompt_len` tokens one after another,
@@ -431,6 +480,7 @@ def run(shape: ModelShape, batch: int = 8, prompt_len: int = 32768, new_tokens: 
     first = r.tok.clone()
     res = {}
     if compare_steps > 0:
+        res["attention_vs_fp16"] = attention_vs_fp16(r)
         free = r.decode_fp16_reference(compare_steps)
         free_dq = r.decode_fp16_reference(compare_steps, kv="dequant")
         torch.cuda.synchronize()
