@@ -442,6 +442,29 @@ def bench_prefill_kernel(torch, seq_len=32768):
     return res
 
 
+def bench_mse(torch, steps, warmup, n=1 << 20, dim=128, bits=4):
+    """The algorithm library's TurboQuantMSE on the GPU (tq_mse_quantize /
+    tq_mse_dequantize): n fp32 vectors of dim 128 at 4 bits.  Algorithmic
+    bytes: quantize reads 4 dim and writes pd b / 8 + 4 per vector;
+    dequantize the reverse."""
+    from turboquant_amd import algorithm as A
+    dev = torch.device("cuda:0")
+    q = A.TurboQuantMSE(dim, bits, device=dev)
+    x = torch.randn((n, dim), device=dev, generator=torch.Generator(device=dev).manual_seed(3))
+    packed, norms = q.quantize(x)
+    pd = q.rotation.padded_dim
+    code_bytes = pd * bits // 8 + 4
+    ms_q = time_graph(torch, lambda: q.quantize(x), steps, warmup)
+    ms_d = time_graph(torch, lambda: q.dequantize(packed, norms), steps, warmup)
+    bq = n * (4 * dim + code_bytes)
+    return {"quantize_us": round(ms_q * 1e3, 2),
+            "quantize_GB/s": round(bq / (ms_q * 1e-3) / 1e9, 1),
+            "dequantize_us": round(ms_d * 1e3, 2),
+            "dequantize_GB/s": round(bq / (ms_d * 1e-3) / 1e9, 1), "alg_bytes": bq,
+            "config": f"TurboQuantMSE({dim}, {bits}) on {n} fp32 vectors (algorithm library, "
+                      "HIP kernels; allocation of the outputs inside the timed calls)"}
+
+
 def bench_dequant(torch, w, steps, warmup):
     """tq_dequant_paged (the read-back of cached context for a prefill chunk)
     over one configs[2] sequence: 32768 tokens x 8 heads of K and V back to
@@ -545,8 +568,10 @@ def main():
     step = step_static if args.static else step_balanced
     op_name = ("turboquant_v5::decode_v5_from_cache_paged_splitkv_ws (static splits)"
                if args.static else "turboquant_v5::decode_paged_balanced_ws (balanced plan)")
-    wr = dq = pf = pk = cpu = None
+    wr = dq = pf = pk = cpu = mse = None
     if not quick:
+        mse = bench_mse(torch, args.steps, args.warmup)
+        log(f"algorithm MSE quantize {mse['quantize_us']} us, dequantize {mse['dequantize_us']} us")
         wr = bench_write(torch, args.steps, args.warmup)
         log(f"write kernel {wr['us']} us -> {wr['GB/s']} GB/s")
         dq = bench_dequant(torch, w, args.steps, args.warmup)
@@ -692,6 +717,7 @@ def main():
         "e2e": e2e_res,
         "write_kernel": wr,
         "dequant_kernel": dq,
+        "algorithm_mse": mse,
         "prefill_chunk": pf,
         "prefill_kernel": pk,
         "stream_ref": stream_ref,

@@ -262,6 +262,31 @@ int64_t tq_prefill_workspace_bytes(int32_t q_len, int32_t kv_len, int32_t num_qo
                                    int32_t num_kv_heads, int32_t head_dim);
 
 /*
+ * The algorithm library's TurboQuantMSE quantizer (reference
+ * turboquant/quantizer.py:63-118, TurboQuantMSE.quantize / .dequantize) on
+ * the GPU, for fp32 vectors of dim <= padded_dim = next_pow2(dim) in
+ * 64..1024 and bit_width 1..4.
+ *
+ * tq_mse_quantize: x fp32 [num_vectors, dim] (rows contiguous) ->
+ *   norms fp32 [num_vectors] = max(||x||, 1e-8) and packed uint8
+ *   [num_vectors, padded_dim / per] (per = 8 / bit_width, 2 for 3 bits;
+ *   code i of a byte at bits i*bit_width), the codes being
+ *   #{j : boundaries[j] < y_d} for y = FWHT(signs * pad(x / norm)) /
+ *   sqrt(padded_dim).  boundaries: HOST fp32 array of 2^bit_width - 1
+ *   values (the Codebook's, already scaled by 1/sqrt(padded_dim)).
+ * tq_mse_dequantize: packed, norms -> out fp32 [num_vectors, dim] =
+ *   (FWHT(centroids[code]) / sqrt(padded_dim) * signs)[:dim] * norm.
+ *   centroids: HOST fp32 array of 2^bit_width values.
+ * signs: device fp32 [padded_dim] of +-1.
+ */
+int tq_mse_quantize(const float* x, int64_t num_vectors, int32_t dim, int32_t padded_dim,
+                    int32_t bit_width, const float* signs, const float* boundaries,
+                    uint8_t* packed, float* norms, tq_stream_t stream);
+int tq_mse_dequantize(const uint8_t* packed, const float* norms, int64_t num_vectors,
+                      int32_t dim, int32_t padded_dim, int32_t bit_width, const float* signs,
+                      const float* centroids, float* out, tq_stream_t stream);
+
+/*
  * Diagnostic, no counterpart in the reference: tq_decode_partials at head
  * size 128 with 8 kv heads per workgroup (the configs[2] geometry) with parts
  * compiled out.  mode 1: the attention math (the same page walk, LDS copy

@@ -328,3 +328,23 @@ def test_balanced_op_schema_declares_its_writes():
     assert len(mul) == 1
     src = mul[0].args[0]  # getitem of the functionalized op: o_ws as written
     assert src.op == "call_function" and src.args[0] is fn[0], ep.graph_module.code
+
+
+def test_mse_entry_points_refuse_bad_arguments():
+    """tq_mse_quantize / tq_mse_dequantize argument checks (no GPU call)."""
+    from turboquant_amd import _lib
+    lib = _lib.load()
+    null = None
+    tab = (ctypes.c_float * 16)()
+    # bit width out of range
+    assert lib.tq_mse_quantize(null, 4, 128, 128, 5, null, tab, null, null, null) == -22
+    assert b"bit_width" in lib.tq_last_error()
+    # padded size not the power of two next to dim, or out of 64..1024
+    assert lib.tq_mse_quantize(null, 4, 60, 128, 4, null, tab, null, null, null) == -22
+    assert lib.tq_mse_quantize(null, 4, 32, 32, 4, null, tab, null, null, null) == -22
+    assert lib.tq_mse_dequantize(null, null, 4, 2048, 2048, 4, null, tab, null, null) == -22
+    assert b"padded_dim" in lib.tq_last_error()
+    # null pointers with work to do
+    assert lib.tq_mse_dequantize(null, null, 4, 128, 128, 4, null, tab, null, null) == -22
+    # nothing to do: success without touching a pointer
+    assert lib.tq_mse_quantize(null, 0, 128, 128, 4, null, tab, null, null, null) == 0

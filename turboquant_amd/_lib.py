@@ -49,6 +49,8 @@ SIGNATURES = {
                                        _I64, _I64, _I32, _I32, _I32, _I32, _I32, _F32, _P, _I64,
                                        _P]),
     "tq_prefill_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
+    "tq_mse_quantize": (_I32, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
+    "tq_mse_dequantize": (_I32, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P]),
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_abi_version": (_I32, []),
 }

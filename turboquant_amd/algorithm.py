@@ -15,7 +15,10 @@ compression.  The serving path (the paged 4-bit cache) is the HIP kernels in
   (turboquant/qjl.py:15-56).
 * ``TurboQuantMSE`` (Algorithm 1) and ``TurboQuantProd`` (Algorithm 2)
   (turboquant/quantizer.py:63-158), with bit-packing low bits first
-  (quantizer.py:17-60).
+  (quantizer.py:17-60).  On a GPU, fp32 vectors of padded size 64..1024 are
+  quantized and dequantized by this package's HIP kernels
+  (ops.mse_quantize / ops.mse_dequantize, tq_mse.hip); TurboQuantProd's MSE
+  stage goes through them too, its QJL stage is a GEMM.
 
 Random tensors (signs, QJL matrix) come from seeded CPU torch generators, so
 the same seeds give the reference's values.
@@ -183,15 +186,37 @@ class TurboQuantMSE:
         self.rotation = RandomHadamardRotation(dim, device=device, seed=seed)
         self.codebook = Codebook(self.rotation.padded_dim, bit_width, device=device)
 
+    def _hip(self, t: torch.Tensor) -> bool:
+        """The HIP kernels serve fp32 vectors on a GPU with padded size 64..1024
+        (tq_mse_quantize / tq_mse_dequantize); anything else runs as torch
+        ops on its own device."""
+        pd = self.rotation.padded_dim
+        return t.is_cuda and 64 <= pd <= 1024 and self.rotation.signs.is_cuda
+
+    def _host_tables(self):
+        if getattr(self, "_tables", None) is None:
+            self._tables = (self.codebook.boundaries.cpu().tolist(),
+                            self.codebook.centroids.cpu().tolist())
+        return self._tables
+
     @torch.no_grad()
     def quantize(self, x: torch.Tensor):
         """x [..., dim] -> (packed uint8 [..., ceil(pd / (8 // b))], norms [...])."""
+        if x.dtype == torch.float32 and self._hip(x):
+            from . import ops
+            return ops.mse_quantize(x, self.rotation.padded_dim, self.bit_width,
+                                    self.rotation.signs, self._host_tables()[0])
         norms = torch.linalg.vector_norm(x, dim=-1, keepdim=True).clamp_min(1e-8)
         idx = self.codebook.quantize(self.rotation.rotate(x / norms))
         return pack_bits(idx, self.bit_width), norms.squeeze(-1)
 
     @torch.no_grad()
     def dequantize(self, packed: torch.Tensor, norms: torch.Tensor) -> torch.Tensor:
+        if self._hip(packed) and norms.dtype == torch.float32:
+            from . import ops
+            return ops.mse_dequantize(packed, norms, self.dim, self.rotation.padded_dim,
+                                      self.bit_width, self.rotation.signs,
+                                      self._host_tables()[1])
         idx = unpack_bits(packed, self.bit_width, self.rotation.padded_dim)
         return self.rotation.inverse_rotate(self.codebook.dequantize(idx)) * norms.unsqueeze(-1)
 

@@ -285,6 +285,65 @@ def dequant_paged(kv_cache: torch.Tensor, pages: torch.Tensor, num_tokens: int,
     _lib.check(rc, "dequant_paged")
 
 
+def _host_f32(values) -> "ctypes.Array":
+    import ctypes
+    vals = [float(v) for v in values]
+    return (ctypes.c_float * max(1, len(vals)))(*vals)
+
+
+def mse_quantize(x: torch.Tensor, padded_dim: int, bit_width: int, signs: torch.Tensor,
+                 boundaries) -> tuple[torch.Tensor, torch.Tensor]:
+    """TurboQuantMSE.quantize on the GPU (tq_mse_quantize): x fp32
+    [..., dim] -> (packed uint8 [..., padded_dim / per], norms fp32 [...]).
+    `boundaries` are the codebook's 2^b - 1 scaled boundaries as host
+    floats."""
+    _require_gpu(x, signs)
+    if x.dtype != torch.float32:
+        raise RuntimeError("mse_quantize: x must be fp32")
+    if signs.dtype != torch.float32 or signs.numel() < padded_dim:
+        raise RuntimeError("mse_quantize: signs must be fp32 [padded_dim]")
+    x = x.contiguous()
+    dim = x.shape[-1]
+    lead = x.shape[:-1]
+    n = x.numel() // dim if dim else 0
+    per = 2 if bit_width == 3 else 8 // bit_width
+    packed = torch.empty((*lead, padded_dim // per), dtype=torch.uint8, device=x.device)
+    norms = torch.empty(lead, dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        rc = lib.tq_mse_quantize(x.data_ptr(), n, dim, int(padded_dim), int(bit_width),
+                                 signs.data_ptr(), _host_f32(boundaries), packed.data_ptr(),
+                                 norms.data_ptr(), _stream_ptr(x.device))
+    _lib.check(rc, "mse_quantize")
+    return packed, norms
+
+
+def mse_dequantize(packed: torch.Tensor, norms: torch.Tensor, dim: int, padded_dim: int,
+                   bit_width: int, signs: torch.Tensor, centroids) -> torch.Tensor:
+    """TurboQuantMSE.dequantize on the GPU (tq_mse_dequantize): packed uint8
+    [..., padded_dim / per] and norms [...] -> fp32 [..., dim].  `centroids`
+    are the codebook's 2^b scaled levels as host floats."""
+    _require_gpu(packed, norms, signs)
+    per = 2 if bit_width == 3 else 8 // bit_width
+    if packed.dtype != torch.uint8 or packed.shape[-1] != padded_dim // per:
+        raise RuntimeError("mse_dequantize: packed must be uint8 [..., padded_dim / per]")
+    if tuple(norms.shape) != tuple(packed.shape[:-1]):
+        raise RuntimeError("mse_dequantize: norms must match packed's leading dims")
+    packed = packed.contiguous()
+    nf = norms.to(torch.float32).contiguous()
+    lead = packed.shape[:-1]
+    n = nf.numel()
+    out = torch.empty((*lead, dim), dtype=torch.float32, device=packed.device)
+    lib = _lib.load()
+    with torch.cuda.device(packed.device):
+        rc = lib.tq_mse_dequantize(packed.data_ptr(), nf.data_ptr(), n, int(dim),
+                                   int(padded_dim), int(bit_width), signs.data_ptr(),
+                                   _host_f32(centroids), out.data_ptr(),
+                                   _stream_ptr(packed.device))
+    _lib.check(rc, "mse_dequantize")
+    return out
+
+
 # --------------------------------------------------------------------------
 # torch.library registration under the reference's namespaces and schemas
 # --------------------------------------------------------------------------
