@@ -86,6 +86,10 @@ def assert_close(got, ref, what=""):
     err = np.abs(got - ref)
     lim = ATOL + RTOL * np.abs(ref)
     bad = err > lim
+    big = np.abs(ref) > 1e-2
+    rel = float((err[big] / np.abs(ref[big])).max()) if big.any() else 0.0
+    print(f"  {what}: max abs err {err.max():.3e}, rms {np.sqrt(np.mean(err ** 2)):.3e}, "
+          f"max rel err (|ref| > 1e-2) {rel:.3e}, |ref| max {np.abs(ref).max():.3e}", flush=True)
     assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} outside atol {ATOL} / "
                            f"rtol {RTOL}; max abs err {err.max():.3e}")
 

@@ -826,6 +826,26 @@ __device__ __forceinline__ uint32_t mix_pair(float a, uint32_t na, float b, uint
   return r;
 }
 
+// The fp16 remainders of two products: fp16(a * nv_a - h_a), h_a the low half
+// of hw (mix_pair's result for a), and likewise for b with the high half;
+// one fma with one rounding each, so hi + lo carries the fp32 product to
+// about 22 bits
+__device__ __forceinline__ uint32_t mix_pair_lo(float a, uint32_t na, float b, uint32_t nb,
+                                                uint32_t hw) {
+  uint32_t r;
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm("v_fma_mixlo_f16 %0, %1, %2, -%5 op_sel:[0,1,0] op_sel_hi:[0,1,1]\n\t"
+      "v_fma_mixhi_f16 %0, %3, %4, -%5 op_sel:[0,1,1] op_sel_hi:[0,1,1]"
+      : "=&v"(r)
+      : "v"(a), "v"(na), "v"(b), "v"(nb), "v"(hw));
+#else
+  const float ha = lo_half(hw), hb = hi_half(hw);
+  r = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(a * hi_half(na) - ha)) |
+      ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(b * hi_half(nb) - hb)) << 16);
+#endif
+  return r;
+}
+
 // Online softmax over the NV score values this lane holds for one step
 // (PACK 2: 4 values, tile (l%16)/8, head l%8; PACK 1: 8 values, tile 0 then
 // tile 1, head l%16; tokens 4*q4 + r), already scaled by the K norms.  nvr:
@@ -833,10 +853,11 @@ __device__ __forceinline__ uint32_t mix_pair(float a, uint32_t na, float b, uint
 // all are valid (uniform); hmask: the lanes of real heads (head < ratio).
 // Writes p * nv as fp16 pairs to pw; the running
 // max only moves when the step exceeds it by more than 2^3, so p <= 8.
-template <int PD, int NV>
+template <int PD, int NV, bool LO = false>
 __device__ __forceinline__ void softmax_step(float* sc, const uint32_t* nvr, bool full,
                                              const bool* valid, bool rot8, uint64_t hmask,
-                                             float lpv, SoftmaxState<PD>& st, uint32_t* pw) {
+                                             float lpv, SoftmaxState<PD>& st, uint32_t* pw,
+                                             uint32_t* pl = nullptr) {
   constexpr int NO = PD / 16;
   if (!full) {
 #pragma unroll
@@ -866,6 +887,11 @@ __device__ __forceinline__ void softmax_step(float* sc, const uint32_t* nvr, boo
     if constexpr (NV == 8) ls += (pr[4] + pr[5]) + (pr[6] + pr[7]);
 #pragma unroll
     for (int r = 0; r < NV; r += 2) pw[r / 2] = mix_pair(pr[r], nvr[r], pr[r + 1], nvr[r + 1]);
+    if constexpr (LO) {
+#pragma unroll
+      for (int r = 0; r < NV; r += 2)
+        pl[r / 2] = mix_pair_lo(pr[r], nvr[r], pr[r + 1], nvr[r + 1], pw[r / 2]);
+    }
   } else {
     // masked entries: p = 0, and their norm bits may be anything (0 * inf
     // is NaN), so their products are zeroed too
@@ -877,8 +903,12 @@ __device__ __forceinline__ void softmax_step(float* sc, const uint32_t* nvr, boo
     for (int r = 0; r < NV; r += 2) {
       const float x0 = valid[r] ? pr[r] * hi_half(nvr[r]) : 0.0f;
       const float x1 = valid[r + 1] ? pr[r + 1] * hi_half(nvr[r + 1]) : 0.0f;
-      pw[r / 2] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x0) |
-                  ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16);
+      const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+      pw[r / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+                  ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+      if constexpr (LO)
+        pl[r / 2] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(x0 - (float)h0)) |
+                    ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(x1 - (float)h1)) << 16);
     }
   }
   st.lsum += ls;
@@ -889,6 +919,24 @@ __device__ __forceinline__ void softmax_step(float* sc, const uint32_t* nvr, boo
 __device__ __forceinline__ uint32_t shl8(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x108, 0xf, 0xf, false);
 }
+// value of lane n ^ 8 within each row of 16 (DPP row_ror:8)
+__device__ __forceinline__ uint32_t ror8u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false);
+}
+
+// Build option (-DTQ_PV_LO=1): the PV probabilities as fp16 hi + lo parts.
+// With GQA ratio <= 8 (QC) the B operand's columns 8..15 carry no head, so
+// they take the lo parts of heads 0..7 and the output adds column n + 8 to
+// column n at the end; the products p * nv then enter the PV MFMAs to about
+// 22 bits, as the reference's fp32 probabilities do.  Off by default:
+// measured on the B = 64 ragged batches (Student-t keys) it lowers the rms
+// error against the fp64 oracle by 16% (3.1e-4 -> 2.6e-4) but not the
+// largest errors, which the fp16 partial rows and the fp16 output set, and
+// costs 0.4 us per launch at configs[2] and 1.7% on the ragged batches.
+#ifndef TQ_PV_LO
+#define TQ_PV_LO 0
+#endif
+constexpr bool kPvLo = TQ_PV_LO != 0;
 
 // Split-KV partials.  Workgroup = (sequence b, split s, group hg of G kv
 // heads), one wave per kv head.  The workgroup streams its heads' cache rows
@@ -917,6 +965,7 @@ void decode_partials_kernel(DecodeParams p) {
   constexpr int ECH = RG::ECH;
   constexpr int CPT = RG::CPT;
   constexpr int NI = RG::NI;
+  constexpr bool PLO = QC && kPvLo && MATH >= 2;  // PV probabilities as hi + lo
   // LDS: the dequant table at address 0 (the table reads rely on it), then
   // the ring of tile slots
   struct __attribute__((aligned(16))) Lds {
@@ -1412,11 +1461,20 @@ void decode_partials_kernel(DecodeParams p) {
           valid[i] = okT[T] && t >= c0 && t < c1;
         }
       }
-      uint32_t pw[NV / 2];
-      softmax_step<PD, NV>(sc, nvr, full, valid, PACK == 2, hmask, lpv, st, pw);
+      uint32_t pw[NV / 2], pl[NV / 2];
+      softmax_step<PD, NV, PLO>(sc, nvr, full, valid, PACK == 2, hmask, lpv, st, pw, pl);
       half8_t p8;
-      if constexpr (PACK == 2) {
+      if constexpr (PACK == 2 && PLO) {
+        // lanes n < 8: hi parts of tile 0 (own) and tile 1 (lane n + 8);
+        // lanes n >= 8: lo parts of tile 0 (lane n - 8) and tile 1 (own)
+        const bool up = n >= 8;
+        const uint32_t r0 = ror8u(up ? pw[0] : pl[0]), r1 = ror8u(up ? pw[1] : pl[1]);
+        p8 = up ? as_half8(r0, r1, pl[0], pl[1]) : as_half8(pw[0], pw[1], r0, r1);
+      } else if constexpr (PACK == 2) {
         p8 = as_half8(pw[0], pw[1], shl8(pw[0]), shl8(pw[1]));
+      } else if constexpr (PLO) {
+        // lanes n >= 8 hold the same scores as lane n - 8: their lo parts
+        p8 = n >= 8 ? as_half8(pl[0], pl[1], pl[2], pl[3]) : as_half8(pw[0], pw[1], pw[2], pw[3]);
       } else {
         p8 = as_half8(pw[0], pw[1], pw[2], pw[3]);
       }
@@ -1457,6 +1515,14 @@ void decode_partials_kernel(DecodeParams p) {
 
   if constexpr (MATH == 0) return;  // the bare ring stores nothing
   // ---- finish: O[i][r] = o[h = n][dim (4*q4 + r)*NO + i]
+  if constexpr (PLO) {
+    // column n + 8 accumulated the lo parts of head n's probabilities
+#pragma unroll
+    for (int i = 0; i < NO; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        st.O[i][r] = st.O[i][r] + __uint_as_float(ror8u(__float_as_uint(st.O[i][r])));
+  }
   float lt = st.lsum;
   if constexpr (PACK == 2) lt = lt + __int_as_float(__builtin_amdgcn_mov_dpp(
                                          __float_as_int(lt), 0x128, 0xf, 0xf, false));
