@@ -11,15 +11,22 @@
 //               (2 for b = 3).
 //   dequantize: y_d = centroid[code_d]; x = (FWHT(y) / sqrt(pd) * s)[:dim] * n.
 // The FWHT butterflies run in ascending stride, each stage (a + b, a - b),
-// as the reference's, so the rotation carries the same fp32 bits; only the
-// norm's summation order differs from torch's reduction (it can move a
-// coordinate that sits within an ulp of a boundary).
+// as the reference's, so the rotation carries the same fp32 bits; x / n is
+// correctly rounded (below); only the norm's summation order differs from
+// torch's reduction (it can move a coordinate that sits within an ulp of a
+// boundary).
 //
-// gfx950 layout: one wave64 per vector, lane l holding dims l*E .. l*E+E-1
-// (E = pd / 64, pd = 64 .. 1024): stages of stride < E run in-lane, the
-// others across lanes (lane xor h/E).  The codes go through LDS to be packed
-// by bytes, so every bit width packs the same way.  The codebook sits in
-// LDS.  HBM-bound: 4 dim + pd*b/8 + 4 bytes per vector.
+// gfx950 layout: P lanes per vector (8, or pd / 32 from pd 512 up), each
+// holding E = pd / P dims as NC = E / 8 chunks of 8 consecutive dims, chunk
+// i of lane p being dims 8 (p + P i) .. + 7 (so the lanes of a vector read
+// and write neighbouring 32-byte pieces of its row); a wave serves 64 / P
+// vectors.  FWHT stages of stride 1, 2, 4 run inside a chunk, strides 8 ..
+// 4P across lanes as one fma each, z = sg * z + partner with sg = -1 on the
+// upper lane (the same rounding as a + b or a - b), and the larger strides
+// between a lane's chunks.  The per-vector work (the
+// norm's sqrt and its correctly rounded reciprocal) is shared by the P lanes
+// and each lane's codes pack in its own registers.  HBM-bound in bytes:
+// 4 dim + pd*b/8 + 4 per vector.
 #include <cmath>
 
 #include "tq_common.h"
@@ -27,7 +34,7 @@
 namespace tq {
 namespace {
 
-constexpr int kMseWaves = 4;  // vectors per workgroup
+constexpr int kMseThreads = 256;
 
 struct MseParams {
   const float* x;      // quantize in: [n, dim]
@@ -42,10 +49,22 @@ struct MseParams {
   int levels;
 };
 
-template <int E>
-__device__ __forceinline__ void fwht_wave(float (&v)[E], int lane) {
+template <int PD>
+struct MseGeom {
+  static constexpr int P = PD <= 256 ? 8 : PD / 32;  // lanes per vector
+  static constexpr int E = PD / P;                   // dims per lane (8 .. 32)
+  static constexpr int VPB = kMseThreads / P;        // vectors per workgroup
+};
+
+// value of lane l ^ m (m < 64) through ds_bpermute
+__device__ __forceinline__ float lane_xor(float v, int m) { return __shfl_xor(v, m); }
+
+// Walsh-Hadamard transform (unnormalised, ascending stride) of the PD dims
+// the P lanes of a vector hold: v[8 i + c] = dim 8 (p + P i) + c.
+template <int E, int P>
+__device__ __forceinline__ void fwht_group(float (&v)[E], int p) {
 #pragma unroll
-  for (int h = 1; h < E; h <<= 1)
+  for (int h = 1; h < 8; h <<= 1)
 #pragma unroll
     for (int i = 0; i < E; i++)
       if ((i & h) == 0) {
@@ -54,106 +73,169 @@ __device__ __forceinline__ void fwht_wave(float (&v)[E], int lane) {
         v[i + h] = a - b;
       }
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const bool lower = (lane & m) == 0;
+  for (int m = 1; m < P; m <<= 1) {
+    const float sg = (p & m) ? -1.0f : 1.0f;  // upper lane keeps partner - own
 #pragma unroll
-    for (int i = 0; i < E; i++) {
-      const float o = __shfl_xor(v[i], m);
-      v[i] = lower ? v[i] + o : o - v[i];
-    }
+    for (int i = 0; i < E; i++) v[i] = __builtin_fmaf(sg, v[i], lane_xor(v[i], m));
   }
+#pragma unroll
+  for (int h = 8; h < E; h <<= 1)  // chunk index bits: stride 8 P h / 8
+#pragma unroll
+    for (int i = 0; i < E; i++)
+      if ((i & h) == 0) {
+        const float a = v[i], b = v[i + h];
+        v[i] = a + b;
+        v[i + h] = a - b;
+      }
 }
 
-template <int E, int BITS>
-__global__ __launch_bounds__(64 * kMseWaves) void mse_quantize_kernel(MseParams p) {
-  constexpr int PD = 64 * E;
-  constexpr int PER = BITS == 3 ? 2 : 8 / BITS;
-  __shared__ uint8_t codes[kMseWaves][PD];
+// fp32 value with the sign of a +-1 sign value folded in (exact: s * v)
+__device__ __forceinline__ float apply_sign(float v, float s) {
+  return __uint_as_float(__float_as_uint(v) ^ (__float_as_uint(s) & 0x80000000u));
+}
+
+template <int PD, int BITS>
+__global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) {
+#pragma clang fp contract(off)
+  using MG = MseGeom<PD>;
+  constexpr int P = MG::P, E = MG::E, NC = E / 8;
+  constexpr int PER = BITS == 3 ? 2 : 8 / BITS;  // codes per byte
+  constexpr int CB = 8 / PER;                    // packed bytes per 8-dim chunk
   __shared__ float bnd[16];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (threadIdx.x < 16) bnd[threadIdx.x] = p.table[threadIdx.x];
   __syncthreads();
-  const int64_t row = (int64_t)blockIdx.x * kMseWaves + w;
-  if (row >= p.n) return;
-  const float* xr = p.x + row * p.dim;
+  const int lane = threadIdx.x & 63, sub = lane % P;
+  const int64_t row = (int64_t)blockIdx.x * MG::VPB + threadIdx.x / P;
+  const bool live = row < p.n;
   float v[E];
+  if (live && p.dim == PD) {
 #pragma unroll
-  for (int i = 0; i < E; i++) {
-    const int d = lane * E + i;
-    v[i] = d < p.dim ? xr[d] : 0.0f;
+    for (int i = 0; i < NC; i++) {
+      const float4* src = reinterpret_cast<const float4*>(p.x + row * PD + 8 * (sub + P * i));
+      const float4 f0 = src[0], f1 = src[1];
+      v[8 * i] = f0.x; v[8 * i + 1] = f0.y; v[8 * i + 2] = f0.z; v[8 * i + 3] = f0.w;
+      v[8 * i + 4] = f1.x; v[8 * i + 5] = f1.y; v[8 * i + 6] = f1.z; v[8 * i + 7] = f1.w;
+    }
+  } else {
+    const float* src = p.x + (live ? row : 0) * p.dim;
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const int d = 8 * (sub + P * (i / 8)) + i % 8;
+      v[i] = (live && d < p.dim) ? src[d] : 0.0f;
+    }
   }
+  // ||x||: the lane's squares, then across the vector's lanes
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < E; i++) ss = __builtin_fmaf(v[i], v[i], ss);
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+  for (int m = 1; m < P; m <<= 1) ss += lane_xor(ss, m);
   const float sq = sqrtf(ss);
   const float nrm = sq < 1e-8f ? 1e-8f : sq;  // torch's clamp(min=1e-8), NaN kept
+  // x / n correctly rounded without a division per element: with y the
+  // correctly rounded 1/n, q = RN(x y) and the exact remainder r = x - q n
+  // (one fma), RN(q + r y) is the correctly rounded quotient (Markstein's
+  // theorem, IBM J. Res. Dev. 34(1), 1990), for every finite x here (|x / n|
+  // <= 1, no overflow; x = 0 gives +-0 as x / n does)
+  const float yr = 1.0f / nrm;
 #pragma unroll
-  for (int i = 0; i < E; i++) v[i] = (v[i] / nrm) * p.signs[lane * E + i];
-  fwht_wave<E>(v, lane);
-  const int nb = p.levels - 1;
+  for (int i = 0; i < E; i++) {
+    const float q = v[i] * yr;
+    const float r = __builtin_fmaf(-q, nrm, v[i]);
+    v[i] = apply_sign(__builtin_fmaf(r, yr, q), p.signs[8 * (sub + P * (i / 8)) + i % 8]);
+  }
+  fwht_group<E, P>(v, sub);
+  // code = #{j : b_j < y}: a binary search over the sorted boundaries in LDS
+  constexpr int NBND = (1 << BITS) - 1;
+  uint32_t word[NC] = {};
 #pragma unroll
   for (int i = 0; i < E; i++) {
     const float y = v[i] * p.inv_sqrt_pd;
     int c = 0;
-    for (int j = 0; j < nb; j++) c += bnd[j] < y ? 1 : 0;
-    if (y != y) c = nb;  // NaN: torch.bucketize's top index
-    codes[w][lane * E + i] = (uint8_t)c;
-  }
-  if (lane == 0) p.norms[row] = nrm;
-  // the wave's codes, written by every lane, are read by other lanes below
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  uint8_t* pr = p.packed + row * p.nbytes;
-  for (int k = lane; k < p.nbytes; k += 64) {
-    uint32_t byte = 0;
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int d = k * PER + i;
-      if (d < PD) byte |= (uint32_t)codes[w][d] << (i * BITS);
+    for (int s = BITS - 1; s >= 0; s--) {
+      const int cand = c + (1 << s);
+      c = bnd[cand - 1] < y ? cand : c;
     }
-    pr[k] = (uint8_t)byte;
+    if (y != y) c = NBND;  // NaN: torch.bucketize's top index
+    const int k = i % 8;   // chunk byte k / PER, slot k % PER
+    word[i / 8] |= (uint32_t)c << (8 * (k / PER) + BITS * (k % PER));
+  }
+  if (!live) return;
+  if (sub == 0) p.norms[row] = nrm;
+#pragma unroll
+  for (int i = 0; i < NC; i++) {
+    uint8_t* dst = p.packed + row * p.nbytes + (sub + P * i) * CB;
+    if constexpr (CB == 1) *dst = (uint8_t)word[i];
+    else if constexpr (CB == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word[i];
+    else *reinterpret_cast<uint32_t*>(dst) = word[i];
   }
 }
 
-template <int E, int BITS>
-__global__ __launch_bounds__(64 * kMseWaves) void mse_dequantize_kernel(MseParams p) {
+template <int PD, int BITS>
+__global__ __launch_bounds__(kMseThreads) void mse_dequantize_kernel(MseParams p) {
+#pragma clang fp contract(off)
+  using MG = MseGeom<PD>;
+  constexpr int P = MG::P, E = MG::E, NC = E / 8;
   constexpr int PER = BITS == 3 ? 2 : 8 / BITS;
+  constexpr int CB = 8 / PER;
   constexpr uint32_t kMask = (1u << BITS) - 1u;
   __shared__ float cen[16];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (threadIdx.x < 16) cen[threadIdx.x] = p.table[threadIdx.x];
   __syncthreads();
-  const int64_t row = (int64_t)blockIdx.x * kMseWaves + w;
-  if (row >= p.n) return;
-  const uint8_t* pr = p.packed + row * p.nbytes;
+  const int lane = threadIdx.x & 63, sub = lane % P;
+  const int64_t row = (int64_t)blockIdx.x * MG::VPB + threadIdx.x / P;
+  const bool live = row < p.n;
+  uint32_t word[NC] = {};
+  float nrm = 0.0f;
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+      const uint8_t* src = p.packed + row * p.nbytes + (sub + P * i) * CB;
+      if constexpr (CB == 1) word[i] = *src;
+      else if constexpr (CB == 2) word[i] = *reinterpret_cast<const uint16_t*>(src);
+      else word[i] = *reinterpret_cast<const uint32_t*>(src);
+    }
+    nrm = p.norms[row];
+  }
   float v[E];
 #pragma unroll
   for (int i = 0; i < E; i++) {
-    const int d = lane * E + i;
-    const uint32_t c = ((uint32_t)pr[d / PER] >> ((d % PER) * BITS)) & kMask;
-    v[i] = cen[c];
+    const int k = i % 8;
+    v[i] = cen[(word[i / 8] >> (8 * (k / PER) + BITS * (k % PER))) & kMask];
   }
-  fwht_wave<E>(v, lane);
-  const float nrm = p.norms[row];
+  fwht_group<E, P>(v, sub);
+  if (!live) return;
   float* orow = p.out + row * p.dim;
+  auto val = [&](int i) {
+    return apply_sign(v[i] * p.inv_sqrt_pd, p.signs[8 * (sub + P * (i / 8)) + i % 8]) * nrm;
+  };
+  if (p.dim == PD) {
 #pragma unroll
-  for (int i = 0; i < E; i++) {
-    const int d = lane * E + i;
-    if (d < p.dim) orow[d] = ((v[i] * p.inv_sqrt_pd) * p.signs[d]) * nrm;
+    for (int i = 0; i < NC; i++) {
+      float4* o4 = reinterpret_cast<float4*>(orow + 8 * (sub + P * i));
+      o4[0] = float4{val(8 * i), val(8 * i + 1), val(8 * i + 2), val(8 * i + 3)};
+      o4[1] = float4{val(8 * i + 4), val(8 * i + 5), val(8 * i + 6), val(8 * i + 7)};
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const int d = 8 * (sub + P * (i / 8)) + i % 8;
+      if (d < p.dim) orow[d] = val(i);
+    }
   }
 }
 
-template <int E>
+template <int PD>
 hipError_t launch_mse(bool quant, int bits, const MseParams& p, hipStream_t st) {
-  const dim3 grid((unsigned)((p.n + kMseWaves - 1) / kMseWaves)), block(64 * kMseWaves);
+  const dim3 grid((unsigned)((p.n + MseGeom<PD>::VPB - 1) / MseGeom<PD>::VPB));
+  const dim3 block(kMseThreads);
 #define TQ_MSE_CASE(B)                                                              \
   case B:                                                                           \
     if (quant)                                                                      \
-      hipLaunchKernelGGL((mse_quantize_kernel<E, B>), grid, block, 0, st, p);       \
+      hipLaunchKernelGGL((mse_quantize_kernel<PD, B>), grid, block, 0, st, p);      \
     else                                                                            \
-      hipLaunchKernelGGL((mse_dequantize_kernel<E, B>), grid, block, 0, st, p);     \
+      hipLaunchKernelGGL((mse_dequantize_kernel<PD, B>), grid, block, 0, st, p);    \
     break;
   switch (bits) {
     TQ_MSE_CASE(1)
@@ -190,6 +272,14 @@ int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* o
     set_error("%s: null pointer", what);
     return kEinval;
   }
+  // full-width rows are read / written as float4, packed rows as dwords
+  const uintptr_t al = (uintptr_t)(quant ? (const void*)x : (const void*)out) |
+                       (uintptr_t)packed;
+  if ((al & 15) != 0) {
+    set_error("%s: x / out and packed must be 16-byte aligned", what);
+    return kEinval;
+  }
+  const int per = bit_width == 3 ? 2 : 8 / bit_width;
   MseParams p;
   p.x = x;
   p.packed = packed;
@@ -198,7 +288,6 @@ int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* o
   p.signs = signs;
   p.n = n;
   p.dim = dim;
-  const int per = bit_width == 3 ? 2 : 8 / bit_width;
   p.nbytes = padded_dim / per;
   p.inv_sqrt_pd = (float)(1.0 / std::sqrt((double)padded_dim));
   p.levels = 1 << bit_width;
@@ -206,12 +295,12 @@ int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* o
   for (int i = 0; i < (quant ? p.levels - 1 : p.levels); i++) p.table[i] = table[i];
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
-  switch (padded_dim / 64) {
-    case 1: e = launch_mse<1>(quant, bit_width, p, st); break;
-    case 2: e = launch_mse<2>(quant, bit_width, p, st); break;
-    case 4: e = launch_mse<4>(quant, bit_width, p, st); break;
-    case 8: e = launch_mse<8>(quant, bit_width, p, st); break;
-    default: e = launch_mse<16>(quant, bit_width, p, st); break;
+  switch (padded_dim) {
+    case 64: e = launch_mse<64>(quant, bit_width, p, st); break;
+    case 128: e = launch_mse<128>(quant, bit_width, p, st); break;
+    case 256: e = launch_mse<256>(quant, bit_width, p, st); break;
+    case 512: e = launch_mse<512>(quant, bit_width, p, st); break;
+    default: e = launch_mse<1024>(quant, bit_width, p, st); break;
   }
   if (e != hipSuccess) set_error("%s: launch failed: %s", what, hipGetErrorString(e));
   return (int)e;

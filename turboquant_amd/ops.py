@@ -303,6 +303,8 @@ def mse_quantize(x: torch.Tensor, padded_dim: int, bit_width: int, signs: torch.
     if signs.dtype != torch.float32 or signs.numel() < padded_dim:
         raise RuntimeError("mse_quantize: signs must be fp32 [padded_dim]")
     x = x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()  # the kernel reads whole rows as float4
     dim = x.shape[-1]
     lead = x.shape[:-1]
     n = x.numel() // dim if dim else 0
@@ -330,6 +332,8 @@ def mse_dequantize(packed: torch.Tensor, norms: torch.Tensor, dim: int, padded_d
     if tuple(norms.shape) != tuple(packed.shape[:-1]):
         raise RuntimeError("mse_dequantize: norms must match packed's leading dims")
     packed = packed.contiguous()
+    if packed.data_ptr() % 16:
+        packed = packed.clone()  # the kernel reads a lane's codes as dwords
     nf = norms.to(torch.float32).contiguous()
     lead = packed.shape[:-1]
     n = nf.numel()
