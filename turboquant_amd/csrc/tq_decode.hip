@@ -938,6 +938,9 @@ __device__ __forceinline__ uint32_t ror8u(uint32_t v) {
 #endif
 constexpr bool kPvLo = TQ_PV_LO != 0;
 
+#ifndef TQ_DECODE_MATH
+#define TQ_DECODE_MATH 2
+#endif
 // Split-KV partials.  Workgroup = (sequence b, split s, group hg of G kv
 // heads), one wave per kv head.  The workgroup streams its heads' cache rows
 // tile by tile (16 tokens x G entries of both slabs) into a ring of
@@ -950,11 +953,12 @@ constexpr bool kPvLo = TQ_PV_LO != 0;
 // registers, barrier, then the copies of the tiles kRingSlots ahead are
 // issued into the two slots just read, and the math runs while they are in
 // flight.  Slot bases are runtime values (advanced by two slots per step).
-// MATH: 2 = the kernel; 1 and 0 are diagnostics of its data movement: 1 =
+// MATH: 2 = the kernel (TQ_DECODE_MATH, a build option for measurement
+// builds only, sets the default); 1 and 0 are diagnostics of its data movement: 1 =
 // the attention math compiled out (q' setup, table build and partial-row
 // stores kept), 0 = the bare copy ring (page walk, copies, waits, barriers
 // and slot reads only).
-template <int PD, int G, int PACK, bool QC, bool PLAN, int MATH = 2>
+template <int PD, int G, int PACK, bool QC, bool PLAN, int MATH = TQ_DECODE_MATH>
 __global__ __launch_bounds__(64 * G)
 __attribute__((amdgpu_waves_per_eu(PD == 256 ? 2 : (PACK == 1 ? 3 : 4))))
 void decode_partials_kernel(DecodeParams p) {
