@@ -166,3 +166,14 @@ def test_graph_replay_with_changing_seq_lens():
         c2["seq_lens"] = np.array(lens, np.int32)
         ref = G.oracle_decode(c2, cache.cpu().numpy(), d["qp"], pd, scale)
         G.assert_close(got, ref, f"replay {i} vs oracle")
+
+
+def test_sequence_longer_than_2_pow_24_tokens():
+    """A sequence of 2^24 + 777 tokens beside a short one (1 kv head, head
+    size 64): the plan's unit counts take the integer division past 2^24
+    tokens (a float estimate alone could be off by more than one there), the
+    row table covers every token, and the output matches the oracle."""
+    lens = [(1 << 24) + 777, 3000]
+    print(f"case: balanced B=2 lens={lens} 4/1/64", flush=True)
+    case, cache, pd = G.device_case(61, lens, 4, 1, 64, chunk_tokens=1 << 20)
+    _check(case, cache, pd, "balanced 2^24+ tokens")
