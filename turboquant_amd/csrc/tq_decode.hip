@@ -1639,6 +1639,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
     r0 = split_rows[b];
     S = split_rows[b + 1] - r0;
   }
+
   const int64_t row0 = (int64_t)r0 * Hq + h;
   const int64_t rs = Hq;
 
