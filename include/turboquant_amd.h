@@ -169,9 +169,10 @@ int tq_decode_balanced_rows(int32_t batch, int32_t num_qo_heads, int32_t num_kv_
 
 /*
  * The first kernel of tq_decode_paged_splitkv alone (the reference's v5 split
- * kernel, v5_tc.cuh:106-795): writes the partial rows (normalised, rotated
- * domain, fp16 [batch*num_splits, num_qo_heads, pd] at the start of
- * partition_o) and partition_lse (natural log; -inf for an empty split) of
+ * kernel, v5_tc.cuh:106-795): writes the partial rows (normalised and,
+ * when signs != NULL, rotated back to the original domain per split as
+ * v5_tc.cuh:712-765 does; fp16 [batch*num_splits, num_qo_heads, pd] at the
+ * start of partition_o) and partition_lse (natural log; -inf for an empty split) of
  * split s = tokens [s * kv_chunk_size, min((s + 1) * kv_chunk_size, seq_len)).
  */
 int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -186,11 +187,12 @@ int tq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 
 /*
  * The second kernel alone (reads the fp16 partial rows tq_decode_partials
- * leaves in partition_o): LSE merge of the splits of each sequence, inverse
- * rotation (s * FWHT(o) / sqrt(pd)) and the fp16 store into o.  Replaces
- * SplitKVCombineKernel (combine.cuh:18-79) plus the per-split inverse FWHT of
- * v5_tc.cuh:712-765.  Splits with lse == -inf are skipped; a sequence with
- * no tokens gets zeros.
+ * leaves in partition_o, already in the original domain): LSE merge of the
+ * splits of each sequence and the fp16 store into o.  Replaces
+ * SplitKVCombineKernel (combine.cuh:18-79).  Splits with lse == -inf are
+ * skipped; a sequence with no tokens gets zeros.  `signs` is not read (the
+ * partials kernel applied the rotation); it stays in the signature for
+ * callers of earlier versions.
  */
 int tq_combine_splits(const float* partition_o, const float* partition_lse,
                       int32_t batch, int32_t num_splits, int32_t num_qo_heads,

@@ -54,7 +54,7 @@ SIGNATURES = {
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_abi_version": (_I32, []),
 }
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 

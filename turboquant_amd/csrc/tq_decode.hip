@@ -1088,6 +1088,9 @@ void decode_partials_kernel(DecodeParams p) {
   constexpr int NQL = 2;
   const bool qreg = ratio * PD <= 512 * NQL;  // uniform
   float qx[NQL][8];
+  // sign bits of dims (8 lane) % PD .. + 7 (bit k: dim + k), for the inverse
+  // rotation of the partial rows at the end (the same dims for every pass)
+  [[maybe_unused]] uint32_t sgnbits = 0;
 #if defined(__HIP_DEVICE_COMPILE__)
   if constexpr (MATH >= 1) {
     const _Float16* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)kvh * ratio * p.q_sh;
@@ -1105,6 +1108,10 @@ void decode_partials_kernel(DecodeParams p) {
       const u32x4 s0 = __builtin_amdgcn_raw_buffer_load_b128(rsg, (uint32_t)(d * 4), 0, 0);
       const u32x4 s1 = __builtin_amdgcn_raw_buffer_load_b128(rsg, (uint32_t)(d * 4 + 16), 0, 0);
       const uint32_t sw[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+      if (j == 0) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) sgnbits |= (sw[k] >> 31) << k;
+      }
 #pragma unroll
       for (int k = 0; k < 8; k++) {
         const float x = k & 1 ? hi_half(qv[k / 2]) : lo_half(qv[k / 2]);
@@ -1566,71 +1573,74 @@ void decode_partials_kernel(DecodeParams p) {
   // writes above
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  // rows are stored as fp16 (the combine reads them so): half the bytes of
-  // fp32 rows, and their rounding (relative 2^-11 on normalised outputs) is
-  // far inside the output tolerance
+  // Each row goes back to the original domain here, o = s * FWHT(o') /
+  // sqrt(pd), per split as the reference's v5 kernel does
+  // (flashinfer_decode_turboquant_v5_tc.cuh:712-765): the merge of the
+  // splits is linear, so the combine then needs no rotation and no exchange
+  // across its waves.  Lane l holds 8 consecutive dims of one row (PD / 8
+  // lanes per row, whole rows per pass): butterflies 1, 2, 4 in-lane, the
+  // rest between the row's lanes.  Rows are stored as fp16 (the combine
+  // reads them so): half the bytes of fp32 rows, and their rounding
+  // (relative 2^-11 on normalised outputs) is far inside the output
+  // tolerance.
   _Float16* const out = reinterpret_cast<_Float16*>(p.po) + orow0 * PD;
   for (int e = 8 * lane; e < ratio * PD; e += 512) {
     const float4_t a = *reinterpret_cast<const float4_t*>(stage + e);
     const float4_t c = *reinterpret_cast<const float4_t*>(stage + e + 4);
-    const half8_t h = {(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
-                       (_Float16)c[0], (_Float16)c[1], (_Float16)c[2], (_Float16)c[3]};
+    float x[8] = {a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
+    if constexpr (MATH >= 2) {
+      if (p.signs) {  // uniform
+#pragma unroll
+        for (int hh = 1; hh < 8; hh <<= 1)
+#pragma unroll
+          for (int k = 0; k < 8; k++)
+            if (!(k & hh)) {
+              const float u = x[k], v = x[k + hh];
+              x[k] = u + v;
+              x[k + hh] = u - v;
+            }
+#pragma unroll
+        for (int m = 1; m < PD / 8; m <<= 1) {
+          const float sgn = (lane & m) ? -1.0f : 1.0f;  // upper lane: partner - own
+#pragma unroll
+          for (int k = 0; k < 8; k++) x[k] = __builtin_fmaf(sgn, x[k], xor_lane(x[k], m));
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+          x[k] = __uint_as_float(__float_as_uint(x[k] * p.inv_sqrt_pd) ^
+                                 (((sgnbits >> k) & 1u) << 31));
+      }
+    }
+    const half8_t h = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3],
+                       (_Float16)x[4], (_Float16)x[5], (_Float16)x[6], (_Float16)x[7]};
     *reinterpret_cast<half8_t*>(out + e) = h;
   }
 }
-// LSE merge of the splits of one (sequence, q head), inverse rotation, fp16
-// store.  256 threads: split weights are computed once into LDS, then
-// 256/(PD/4) split groups each sum a strided subset of the splits for one
-// float4 column, a tree in LDS adds the groups, and wave 0 runs the inverse
-// FWHT across its 64 lanes.
-// The six cross-lane stages of a 64-lane Walsh-Hadamard transform (lane l
-// ends with sum_j (-1)^popcount(l & j) x_j): at each partner distance d the
-// lower lane keeps x + partner and the upper partner - x, the partner fetched
-// by DPP (d = 1, 2: quad permutes; 4: row shifts; 8: row rotate) or a lane
-// swap (d = 16, 32: the swap returns the lower and the upper lane's value).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
-}
-__device__ __forceinline__ float fwht_lanes(float x, int lane) {
-  float p = dpp_f<0xb1>(x);  // quad_perm [1, 0, 3, 2]
-  x = (lane & 1) ? p - x : x + p;
-  p = dpp_f<0x4e>(x);        // quad_perm [2, 3, 0, 1]
-  x = (lane & 2) ? p - x : x + p;
-  {
-    const float up = dpp_f<0x104>(x), dn = dpp_f<0x114>(x);  // row_shl:4, row_shr:4
-    p = (lane & 4) ? dn : up;
-  }
-  x = (lane & 4) ? p - x : x + p;
-  p = dpp_f<0x128>(x);       // row_ror:8
-  x = (lane & 8) ? p - x : x + p;
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = (lane & 16) ? __uint_as_float(r[0]) - __uint_as_float(r[1])
-                  : __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = (lane & 32) ? __uint_as_float(r[0]) - __uint_as_float(r[1])
-                  : __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  return x;
-}
-
 // four fp16 partial-row values as fp32
 __device__ __forceinline__ float4_t load_half4(const _Float16* src) {
   const half4_t h = *reinterpret_cast<const half4_t*>(src);
   return float4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
 }
 
+// LSE merge of the splits of one (sequence, q head) and the fp16 store:
+// o = sum_s e^(lse_s - M) o_s / sum_s e^(lse_s - M), splits with lse = -inf
+// (no tokens) skipped.  The partial rows arrive in the original domain (the
+// partials kernel applies the inverse rotation per split), so the four waves
+// of a workgroup are independent: wave w merges dims [w PD/4, (w+1) PD/4),
+// lane (c, g) the float4 column c of the wave's dims over the splits g,
+// g + NG, ... (NG = 64 / (PD/16) split groups), with a running max per lane;
+// the groups then meet through lane swaps (no LDS, no barrier), and the lanes
+// of group 0 store.
 template <int PD>
 __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict__ po,
                                                       const float* __restrict__ plse, int S_fixed,
                                                       const int32_t* __restrict__ split_rows,
-                                                      int Hq, const float* __restrict__ signs,
-                                                      float inv_sqrt_pd, _Float16* __restrict__ o) {
-  constexpr int C = PD / 4;        // float4 columns
-  constexpr int NG = 256 / C;      // split groups
-  constexpr int V = PD / 64;       // dims per lane in the FWHT
-  extern __shared__ float sm[];    // [S] weights or group maxima, then [NG][PD] sums + [NG] denominators
-  __shared__ float red[8];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+                                                      int Hq, _Float16* __restrict__ o) {
+  constexpr int CW = PD / 16;      // float4 columns per wave (PD / 4 dims)
+  constexpr int NG = 64 / CW;      // split groups per wave
+  constexpr int R = 8;             // splits per lane per round trip
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int c = lane % CW, g = lane / CW;
   const int b = blockIdx.x / Hq, h = blockIdx.x % Hq;
   // the splits of sequence b are the partial rows r0 .. r0 + S - 1: b * S_fixed
   // onwards, or split_rows[b] .. split_rows[b + 1] (a balanced plan)
@@ -1639,100 +1649,61 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
     r0 = split_rows[b];
     S = split_rows[b + 1] - r0;
   }
-
   const int64_t row0 = (int64_t)r0 * Hq + h;
-  const int64_t rs = Hq;
-
-  const int col = tid % C, grp = tid / C;
+  const int col = wv * (PD / 4) + 4 * c;  // first dim of this lane's column
+  float m = -INFINITY, den = 0.f;
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
-  float den = 0.f;
-  constexpr int R = 16;  // splits per thread held in registers on the fast path
-  if (S <= NG * R) {
-    // one round trip: the LSEs and partial rows of this thread's splits
-    // (grp, grp + NG, ...) are all loaded before any is used
+  for (int s0 = 0; s0 < S; s0 += NG * R) {
+    // this round's LSEs and rows, all loaded before any is used
     float l[R];
     float4_t v[R];
 #pragma unroll
     for (int j = 0; j < R; j++) {
-      const int s = grp + NG * j;
+      const int sj = s0 + g + NG * j;
       l[j] = -INFINITY;
       v[j] = float4_t{0.f, 0.f, 0.f, 0.f};
-      if (s < S) {
-        l[j] = plse[row0 + (int64_t)s * rs];
-        v[j] = load_half4(po + (row0 + (int64_t)s * rs) * PD + col * 4);
+      if (sj < S) {
+        const int64_t r = row0 + (int64_t)sj * Hq;
+        l[j] = plse[r];
+        v[j] = load_half4(po + r * PD + col);
       }
     }
-    float mx = -INFINITY;
+    float mr = m;
 #pragma unroll
-    for (int j = 0; j < R; j++) mx = fmaxf(mx, l[j]);
-    // the groups hold disjoint splits: max over the groups through LDS
-    if (col == 0) sm[grp] = mx;
-    __syncthreads();
-    mx = -INFINITY;
-    for (int g = 0; g < NG; g++) mx = fmaxf(mx, sm[g]);
+    for (int j = 0; j < R; j++) mr = fmaxf(mr, l[j]);
+    if (mr > -INFINITY) {
+      const float sc = m > -INFINITY ? __expf(m - mr) : 0.0f;
+      den *= sc;
+      acc *= sc;
 #pragma unroll
-    for (int j = 0; j < R; j++) {
-      const float wgt = (l[j] > -INFINITY && mx > -INFINITY) ? __expf(l[j] - mx) : 0.0f;
-      den += wgt;
-      acc += wgt != 0.0f ? wgt * v[j] : float4_t{0.f, 0.f, 0.f, 0.f};  // skipped rows may hold any bits
+      for (int j = 0; j < R; j++) {
+        const float wgt = l[j] > -INFINITY ? __expf(l[j] - mr) : 0.0f;
+        den += wgt;
+        // a skipped split's row may hold any bits: it adds nothing
+        acc += wgt != 0.0f ? wgt * v[j] : float4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      m = mr;
     }
-    __syncthreads();  // the group maxima are read; LDS is reused below
-  } else {
-    float mx = -INFINITY;
-    for (int s = tid; s < S; s += 256) mx = fmaxf(mx, plse[row0 + (int64_t)s * rs]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (lane == 0) red[wv] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int s = tid; s < S; s += 256) {
-      const float l = plse[row0 + (int64_t)s * rs];
-      sm[s] = (l > -INFINITY && mx > -INFINITY) ? __expf(l - mx) : 0.0f;
-    }
-    __syncthreads();  // weights visible
-    for (int s = grp; s < S; s += NG) {
-      const float wgt = sm[s];
-      den += wgt;
-      if (wgt != 0.0f)
-        acc += wgt * load_half4(po + (row0 + (int64_t)s * rs) * PD + col * 4);
-    }
-    __syncthreads();  // weights no longer needed; reuse LDS for group sums
   }
-  // den: each group summed its own splits (identical in all C lanes of the group)
-  float* part = sm;
-  *reinterpret_cast<float4_t*>(part + grp * PD + col * 4) = acc;
-  if (col == 0) part[NG * PD + grp] = den;
-  __syncthreads();
-  if (wv == 0) {
-    den = 0.f;
-    for (int g = 0; g < NG; g++) den += part[NG * PD + g];
+  // the split groups of a column: lanes c + CW g, g = 0 .. NG-1, met by lane
+  // xors CW .. 32 (a common max first, then the rescaled sums)
+  float mx = m;
+#pragma unroll
+  for (int d = CW; d < 64; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+  const float sc = (m > -INFINITY) ? __expf(m - mx) : 0.0f;
+  den *= sc;
+  acc *= sc;
+#pragma unroll
+  for (int d = CW; d < 64; d <<= 1) {
+    den += __shfl_xor(den, d);
+#pragma unroll
+    for (int k = 0; k < 4; k++) acc[k] += __shfl_xor(acc[k], d);
+  }
+  if (g == 0) {
     const float inv = den > 0.f ? 1.0f / den : 0.0f;
-    float x[V];
-#pragma unroll
-    for (int i = 0; i < V; i++) {
-      float t = 0.f;
-      for (int g = 0; g < NG; g++) t += part[g * PD + lane * V + i];
-      x[i] = t * inv;
-    }
-    if (signs) {
-#pragma unroll
-      for (int hh = 1; hh < V; hh <<= 1)
-#pragma unroll
-        for (int i = 0; i < V; i += 2 * hh)
-#pragma unroll
-          for (int k = 0; k < hh; k++) {
-            const float a = x[i + k], c = x[i + k + hh];
-            x[i + k] = a + c;
-            x[i + k + hh] = a - c;
-          }
-#pragma unroll
-      for (int i = 0; i < V; i++) x[i] = fwht_lanes(x[i], lane);
-#pragma unroll
-      for (int i = 0; i < V; i++) x[i] = x[i] * inv_sqrt_pd * signs[lane * V + i];
-    }
-    _Float16* dst = o + ((int64_t)b * Hq + h) * PD + lane * V;
-#pragma unroll
-    for (int i = 0; i < V; i++) dst[i] = (_Float16)x[i];
+    const half4_t hv = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv),
+                        (_Float16)(acc[2] * inv), (_Float16)(acc[3] * inv)};
+    *reinterpret_cast<half4_t*>(o + ((int64_t)b * Hq + h) * PD + col) = hv;
   }
 }
 
@@ -2026,29 +1997,23 @@ static int combine_splits(const float* partition_o, const float* partition_lse,
     return kEinval;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const float isq = 1.0f / sqrtf((float)pd);
   _Float16* out = static_cast<_Float16*>(o);
-  // LDS: the weights of a sequence's splits, or the group sums [NG][pd] plus
-  // the group denominators
-  const int max_splits = split_rows ? max_rows : num_splits;
-  const size_t lds = sizeof(float) * (size_t)(max_splits > 1024 + 64 ? max_splits : 1024 + 64);
-  if (lds > 60 * 1024) {
-    set_error("combine: %d splits per sequence is too many", max_splits);
-    return kEinval;
-  }
+  (void)signs;  // the partial rows come rotated back from the partials kernel
+  (void)max_rows;
   dim3 grid((unsigned)blocks), block(256);
+  const _Float16* prow = reinterpret_cast<const _Float16*>(partition_o);
   switch (pd) {
     case 64:
-      hipLaunchKernelGGL(combine_kernel<64>, grid, block, lds, st, reinterpret_cast<const _Float16*>(partition_o), partition_lse,
-                         num_splits, split_rows, num_qo_heads, signs, isq, out);
+      hipLaunchKernelGGL(combine_kernel<64>, grid, block, 0, st, prow, partition_lse, num_splits,
+                         split_rows, num_qo_heads, out);
       break;
     case 128:
-      hipLaunchKernelGGL(combine_kernel<128>, grid, block, lds, st, reinterpret_cast<const _Float16*>(partition_o), partition_lse,
-                         num_splits, split_rows, num_qo_heads, signs, isq, out);
+      hipLaunchKernelGGL(combine_kernel<128>, grid, block, 0, st, prow, partition_lse, num_splits,
+                         split_rows, num_qo_heads, out);
       break;
     default:
-      hipLaunchKernelGGL(combine_kernel<256>, grid, block, lds, st, reinterpret_cast<const _Float16*>(partition_o), partition_lse,
-                         num_splits, split_rows, num_qo_heads, signs, isq, out);
+      hipLaunchKernelGGL(combine_kernel<256>, grid, block, 0, st, prow, partition_lse, num_splits,
+                         split_rows, num_qo_heads, out);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
