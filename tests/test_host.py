@@ -348,3 +348,21 @@ def test_mse_entry_points_refuse_bad_arguments():
     assert lib.tq_mse_dequantize(null, null, 4, 128, 128, 4, null, tab, null, null) == -22
     # nothing to do: success without touching a pointer
     assert lib.tq_mse_quantize(null, 0, 128, 128, 4, null, tab, null, null, null) == 0
+
+
+def test_ops_refuse_tensors_on_two_devices():
+    """The ops check that every tensor is on one GPU before any launch (CPU
+    tensors are refused the same way)."""
+    from turboquant_amd import ops
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ops._require_gpu(torch.zeros(1))
+
+    class FakeCuda:
+        is_cuda = True
+
+        def __init__(self, i):
+            self.device = torch.device("cuda", i)
+
+    ops._require_gpu(FakeCuda(0), FakeCuda(0))
+    with pytest.raises(RuntimeError, match="one GPU"):
+        ops._require_gpu(FakeCuda(0), FakeCuda(1))

@@ -31,9 +31,16 @@ def _stream_ptr(device: torch.device) -> int:
 
 
 def _require_gpu(*tensors: torch.Tensor) -> None:
+    """Every tensor on a GPU, and all on the same one (the kernels launch on
+    the first tensor's device and read the others' addresses there)."""
+    dev = None
     for t in tensors:
         if not t.is_cuda:
             raise RuntimeError("TurboQuant ops run on the GPU only; got a CPU tensor")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"TurboQuant ops need all tensors on one GPU: {dev} and {t.device}")
 
 
 def quantize_write_kv_cache(kv_cache: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
@@ -119,7 +126,7 @@ def decode_paged_splitkv(q: torch.Tensor, kv_cache: torch.Tensor, indices: torch
     if signs is not None and signs.numel() > 0:
         if signs.dtype != torch.float32 or signs.numel() < pd:
             raise RuntimeError("hadamard_signs must be fp32 [padded_dim]")
-        _require_gpu(signs)
+        _require_gpu(q, signs)
         sp = signs.data_ptr()
     lib = _lib.load()
     base = kv_cache.data_ptr()
@@ -194,7 +201,7 @@ def decode_paged_balanced(q: torch.Tensor, kv_cache: torch.Tensor, indices: torc
     if signs is not None and signs.numel() > 0:
         if signs.dtype != torch.float32 or signs.numel() < pd:
             raise RuntimeError("hadamard_signs must be fp32 [padded_dim]")
-        _require_gpu(signs)
+        _require_gpu(q, signs)
         sp = signs.data_ptr()
     lib = _lib.load()
     base = kv_cache.data_ptr()
@@ -272,7 +279,7 @@ def dequant_paged(kv_cache: torch.Tensor, pages: torch.Tensor, num_tokens: int,
     if signs is not None and signs.numel() > 0:
         if signs.dtype != torch.float32 or signs.numel() < padded_dim:
             raise RuntimeError("signs must be fp32 [padded_dim]")
-        _require_gpu(signs)
+        _require_gpu(kv_cache, signs)
         sp = signs.data_ptr()
     lib = _lib.load()
     base = kv_cache.data_ptr()
