@@ -262,11 +262,15 @@ void prefill_kernel(PrefillParams p) {
         }
     }
     float tmax = -INFINITY;
+#if defined(TQ_PREFILL_PROBE) && TQ_PREFILL_PROBE >= 2
+    tmax = sacc[0][0];  // measurement probe: no row max
+#else
 #pragma unroll
     for (int u = 0; u < kNU; u++)
 #pragma unroll
       for (int j = 0; j < 16; j++) tmax = fmaxf(tmax, sacc[u][j]);
     tmax = max32(tmax);
+#endif
     const float m_new = fmaxf(m, tmax);
     // lazy rescale: p = exp2((s - m) c) stays below 2^8 between rescales
     if (__builtin_amdgcn_ballot_w64(m_new * p.c > mc + 8.0f) != 0) {
@@ -291,7 +295,11 @@ void prefill_kernel(PrefillParams p) {
         float pr[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
+#if defined(TQ_PREFILL_PROBE) && TQ_PREFILL_PROBE >= 1
+          pr[i] = __builtin_fmaf(sacc[u][8 * t + i], p.c, -mce);  // measurement probe: no exp2
+#else
           pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[u][8 * t + i], p.c, -mce));
+#endif
           if constexpr (kD != 64) lsum += pr[i];
         }
         u32x4 pk;
