@@ -31,7 +31,7 @@ def _decode_geometry(seed):
     return hd, hkv, ratio, b, lens.astype(np.int32), ("t3" if seed % 3 == 0 else "normal")
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(40))
 def test_decode_sweep(seed):
     hd, hkv, ratio, b, lens, kd = _decode_geometry(seed)
     hq = hkv * ratio
@@ -49,7 +49,7 @@ def test_decode_sweep(seed):
     assert np.all(got_b[empty] == 0) and np.all(got_s[empty] == 0)
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(20))
 def test_write_sweep(seed):
     rng = np.random.default_rng(9000 + seed)
     hd = int(rng.choice([64, 80, 96, 128, 192, 256]))
