@@ -17,8 +17,8 @@ from turboquant_amd.geometry import hadamard_signs
 pytestmark = pytest.mark.gpu
 
 
-def _runner(batch=4, prompt=200, new=9, keep16=False):
-    shape = e2e.ModelShape.tiny(2)
+def _runner(batch=4, prompt=200, new=9, keep16=False, shape=None):
+    shape = shape or e2e.ModelShape.tiny(2)
     r = e2e.Runner(shape, batch, prompt + new, G.DEV, seed=5, keep_fp16_kv=keep16)
     g = torch.Generator(device="cpu")
     g.manual_seed(7)
@@ -29,27 +29,36 @@ def _runner(batch=4, prompt=200, new=9, keep16=False):
     return r
 
 
-def test_e2e_decode_attention_matches_oracle_per_layer():
-    print("case: e2e tiny 2 layers B=4 prompt 200, per-layer oracle", flush=True)
+@pytest.mark.parametrize("hq,hkv,hd", [(32, 8, 128), (16, 2, 256), (16, 4, 64), (8, 2, 96)])
+def test_e2e_decode_attention_matches_oracle_per_layer(hq, hkv, hd):
+    """The whole backend flow (write, fresh-prompt prefill, balanced decode)
+    at the configs[4] head geometry and at head sizes 256, 64 and 96 (the
+    last padded to 128 in the cache and the kernels)."""
+    print(f"case: e2e tiny 2 layers B=4 prompt 200 {hq}/{hkv}/{hd}, per-layer oracle", flush=True)
     import oracle
-    r = _runner()
+    from turboquant_amd.geometry import padded_dim
+    shape = e2e.ModelShape(layers=2, hidden=512, heads=hq, kv_heads=hkv, head_dim=hd,
+                           intermediate=1024, vocab=4096)
+    r = _runner(shape=shape)
     r.probe = []
     r.decode_eager(1)
     torch.cuda.synchronize()
     probe, r.probe = r.probe, None
     assert len(probe) == r.shape.layers
     b = r.batch
+    pd = padded_dim(hd)
     bt = r.block_table.cpu().numpy()
     indptr = np.arange(b + 1, dtype=np.int32) * bt.shape[1]
     seq = r.seq_lens.cpu().numpy()
     assert np.all(seq == 201)
-    signs = hadamard_signs(128).numpy()
+    signs = hadamard_signs(pd).numpy()
     for li, q, _, _, o in probe:
-        qp = q.to(torch.float16).cpu().numpy()
-        ref = oracle.decode(qp, r.caches[li].cpu().numpy(), bt.reshape(-1), indptr, seq, 8, 128,
-                            1.0 / math.sqrt(128), signs)
-        got = o.float().cpu().numpy().reshape(b, 32, 128)
-        G.assert_close(got, ref, f"e2e layer {li}")
+        qp = np.zeros((b, hq, pd), np.float16)
+        qp[:, :, :hd] = q.to(torch.float16).cpu().numpy()
+        ref = oracle.decode(qp, r.caches[li].cpu().numpy(), bt.reshape(-1), indptr, seq, hkv, pd,
+                            1.0 / math.sqrt(hd), signs)[:, :, :hd]
+        got = o.float().cpu().numpy().reshape(b, hq, hd)
+        G.assert_close(got, ref, f"e2e {hq}/{hkv}/{hd} layer {li}")
 
 
 def test_e2e_graph_replays_equal_eager_tokens():
