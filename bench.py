@@ -465,6 +465,42 @@ def bench_mse(torch, steps, warmup, n=1 << 20, dim=128, bits=4):
                       "HIP kernels; allocation of the outputs inside the timed calls)"}
 
 
+def bench_prod(torch, steps, warmup, n=1 << 20, dim=128, bits=4):
+    """TurboQuantProd on the GPU: n fp32 vectors of dim 128 at 4 bits (MSE
+    stage at 3).  Kernel rows: tq_prod_quantize reads 4 dim and writes the
+    codes, norm, 4 dim of unit residual and its norm per vector;
+    tq_prod_dequantize reads the codes, norm, 4 dim of QJL term and the
+    residual norm and writes 4 dim.  The API rows add the two d x d fp32
+    QJL GEMMs (library BLAS) and the sign."""
+    from turboquant_amd import algorithm as A
+    from turboquant_amd import ops
+    dev = torch.device("cuda:0")
+    q = A.TurboQuantProd(dim, bits, device=dev)
+    x = torch.randn((n, dim), device=dev, generator=torch.Generator(device=dev).manual_seed(4))
+    m = q.mse
+    pd = m.rotation.padded_dim
+    bnd, cen = m._host_tables()
+    pk, nm, z, rn = q.quantize(x)
+    term = z.float() @ q.qjl.S
+    per = 2 if bits - 1 == 3 else 8 // (bits - 1)
+    code_bytes = pd // per + 4
+    ms_kq = time_graph(torch, lambda: ops.prod_quantize(x, pd, bits - 1, m.rotation.signs, bnd,
+                                                        cen), steps, warmup)
+    ms_kd = time_graph(torch, lambda: ops.prod_dequantize(pk, nm, term, rn, dim, pd, bits - 1,
+                                                          m.rotation.signs, cen), steps, warmup)
+    ms_q = time_graph(torch, lambda: q.quantize(x), steps, warmup)
+    ms_d = time_graph(torch, lambda: q.dequantize(pk, nm, z, rn), steps, warmup)
+    bkq = n * (4 * dim + code_bytes + 4 * dim + 4)
+    bkd = n * (code_bytes + 4 * dim + 4 + 4 * dim)
+    return {"quantize_kernel_us": round(ms_kq * 1e3, 2),
+            "quantize_kernel_GB/s": round(bkq / (ms_kq * 1e-3) / 1e9, 1),
+            "dequantize_kernel_us": round(ms_kd * 1e3, 2),
+            "dequantize_kernel_GB/s": round(bkd / (ms_kd * 1e-3) / 1e9, 1),
+            "quantize_api_us": round(ms_q * 1e3, 2), "dequantize_api_us": round(ms_d * 1e3, 2),
+            "config": f"TurboQuantProd({dim}, {bits}) on {n} fp32 vectors (HIP kernels + "
+                      "fp32 BLAS GEMMs for QJL; output allocation inside the timed calls)"}
+
+
 def bench_dequant(torch, w, steps, warmup):
     """tq_dequant_paged (the read-back of cached context for a prefill chunk)
     over one configs[2] sequence: 32768 tokens x 8 heads of K and V back to
@@ -568,10 +604,14 @@ def main():
     step = step_static if args.static else step_balanced
     op_name = ("turboquant_v5::decode_v5_from_cache_paged_splitkv_ws (static splits)"
                if args.static else "turboquant_v5::decode_paged_balanced_ws (balanced plan)")
-    wr = dq = pf = pk = cpu = mse = None
+    wr = dq = pf = pk = cpu = mse = prod = None
     if not quick:
         mse = bench_mse(torch, args.steps, args.warmup)
         log(f"algorithm MSE quantize {mse['quantize_us']} us, dequantize {mse['dequantize_us']} us")
+        prod = bench_prod(torch, args.steps // 4, args.warmup // 4)
+        log(f"algorithm Prod kernels {prod['quantize_kernel_us']} / "
+            f"{prod['dequantize_kernel_us']} us, API {prod['quantize_api_us']} / "
+            f"{prod['dequantize_api_us']} us")
         wr = bench_write(torch, args.steps, args.warmup)
         log(f"write kernel {wr['us']} us -> {wr['GB/s']} GB/s")
         dq = bench_dequant(torch, w, args.steps, args.warmup)
@@ -718,6 +758,7 @@ def main():
         "write_kernel": wr,
         "dequant_kernel": dq,
         "algorithm_mse": mse,
+        "algorithm_prod": prod,
         "prefill_chunk": pf,
         "prefill_kernel": pk,
         "stream_ref": stream_ref,

@@ -289,6 +289,33 @@ int tq_mse_dequantize(const uint8_t* packed, const float* norms, int64_t num_vec
                       const float* centroids, float* out, tq_stream_t stream);
 
 /*
+ * The algorithm library's TurboQuantProd (reference
+ * turboquant/quantizer.py:121-158, with turboquant/qjl.py:28-63): the MSE
+ * quantizer at mse_bit_width = bit_width - 1 (1..3 here), then QJL on the unit
+ * residual.  The two d x d QJL products (sign(S r) and S^T z) are plain GEMMs
+ * left to the caller's BLAS; these two calls are the rest of the algorithm.
+ *
+ * tq_prod_quantize: tq_mse_quantize's outputs, plus the MSE read-back
+ *   x_hat = tq_mse_dequantize(packed, norms) (same fp32 bits), the residual
+ *   norms fp32 [num_vectors] = max(||x - x_hat||, 1e-8) and residual_unit
+ *   fp32 [num_vectors, dim] = (x - x_hat) / residual_norm (correctly rounded).
+ *   centroids: HOST fp32 array of 2^mse_bit_width values.  residual_unit
+ *   16-byte aligned.
+ * tq_prod_dequantize: out fp32 [num_vectors, dim] = tq_mse_dequantize(packed,
+ *   norms) + qjl_term * (fp32(sqrt(pi/2) / dim) * residual_norms), rounded in
+ *   that order (the reference's torch expression), with qjl_term fp32
+ *   [num_vectors, dim] = z S, z the +-1 QJL signs.
+ */
+int tq_prod_quantize(const float* x, int64_t num_vectors, int32_t dim, int32_t padded_dim,
+                     int32_t mse_bit_width, const float* signs, const float* boundaries,
+                     const float* centroids, uint8_t* packed, float* norms,
+                     float* residual_unit, float* residual_norms, tq_stream_t stream);
+int tq_prod_dequantize(const uint8_t* packed, const float* norms, const float* qjl_term,
+                       const float* residual_norms, int64_t num_vectors, int32_t dim,
+                       int32_t padded_dim, int32_t mse_bit_width, const float* signs,
+                       const float* centroids, float* out, tq_stream_t stream);
+
+/*
  * Diagnostic, no counterpart in the reference: tq_decode_partials at head
  * size 128 with 8 kv heads per workgroup (the configs[2] geometry) with parts
  * compiled out.  mode 1: the attention math (the same page walk, LDS copy

@@ -100,3 +100,85 @@ def test_mse_hip_nonfinite_rows_and_empty_batch():
     pe, ne = qg.quantize(torch.empty(0, 128, device="cuda:0"))
     assert pe.shape == (0, 64) and ne.shape == (0,)
     assert qg.dequantize(pe, ne).shape == (0, 128)
+
+
+PROD_CASES = [(64, 2), (96, 3), (128, 2), (128, 3), (128, 4), (200, 4), (256, 3), (1000, 2)]
+
+
+@pytest.mark.parametrize("dim,bits", PROD_CASES)
+def test_prod_hip_kernels_against_the_torch_path(dim, bits):
+    """TurboQuantProd through tq_prod_quantize / tq_prod_dequantize against
+    the same quantizer's torch ops.  Codes and norms as the MSE test; the
+    kernel's residual norm and unit residual against torch's x - x_hat, norm
+    and division on the kernel's own codes (the read-back is bit-identical,
+    only the norm's summation order differs); QJL signs against the CPU path
+    where the codes agree; the dequantize epilogue against torch's
+    x_mse + (z S) * (sqrt(pi/2) / d * gamma) on the same GEMM output, bit
+    for bit."""
+    print(f"case: algorithm Prod HIP dim={dim} bits={bits}", flush=True)
+    from turboquant_amd import ops
+    g = torch.Generator().manual_seed(dim * 7 + bits)
+    x = torch.randn(1500, dim, generator=g) * 2.0
+    x[9] = 0.0
+    qc = A.TurboQuantProd(dim, bits, device="cpu", seed=11)
+    qg = A.TurboQuantProd(dim, bits, device="cuda:0", seed=11)
+    pd = qg.mse.rotation.padded_dim
+    xg = x.cuda()
+    bnd, cen = qg.mse._host_tables()
+    pk, nm, ru, rn = ops.prod_quantize(xg, pd, bits - 1, qg.mse.rotation.signs, bnd, cen)
+    pm, nmm = qg.mse.quantize(xg)
+    assert torch.equal(pk, pm) and torch.equal(nm, nmm)  # the MSE kernel's outputs
+    r = xg - qg.mse.dequantize(pk, nm)
+    rn_t = torch.linalg.vector_norm(r, dim=-1).clamp_min(1e-8)
+    assert torch.allclose(rn, rn_t, rtol=2e-6, atol=0), (rn - rn_t).abs().max().item()
+    ru_t = r / rn_t.unsqueeze(-1)
+    err = (ru - ru_t).abs().max().item()
+    print(f"  unit residual max |diff| {err:.3e}", flush=True)
+    assert err <= 2e-6
+    # unit length, but for x = 0, whose residual (the centroids read back at the
+    # clamped norm 1e-8) is shorter than the 1e-8 clamp of its own norm
+    lens = ru.norm(dim=-1)
+    lens[9] = 1.0
+    assert rn[9].item() == 1e-8 or abs(rn[9].item() - 1e-8) < 1e-15
+    assert torch.allclose(lens, torch.ones_like(rn), atol=1e-5)
+    # the public API against the CPU path
+    pg, ng, zg, rg = qg.quantize(xg)
+    pc, nc, zc, rc = qc.quantize(x)
+    cg = A.unpack_bits(pg.cpu(), bits - 1, pd)
+    cc = A.unpack_bits(pc, bits - 1, pd)
+    same = (cg == cc).all(-1)
+    assert same.float().mean().item() >= 0.99
+    sign_agree = (zg.cpu()[same] == zc[same]).float().mean().item()
+    print(f"  QJL sign agreement {sign_agree:.6f} on {int(same.sum())} rows", flush=True)
+    assert zg.dtype == torch.int8 and set(zg.unique().tolist()) <= {-1, 1}
+    assert sign_agree >= 0.999
+    assert torch.allclose(rg.cpu()[same], rc[same], rtol=1e-5, atol=0)
+    # dequantize: the fused epilogue equals torch's expression on the same GEMM
+    term = zg.float() @ qg.qjl.S
+    want = qg.mse.dequantize(pg, ng) + term * (qg.qjl.dequant_scale * rg.unsqueeze(-1))
+    got = ops.prod_dequantize(pg, ng, term, rg, dim, pd, bits - 1, qg.mse.rotation.signs, cen)
+    assert torch.equal(got, want), (got - want).abs().max().item()
+    xh = qg.dequantize(pg, ng, zg, rg)
+    assert torch.equal(xh, want)
+    # and against the CPU dequantize of the CPU's own outputs, within GEMM rounding
+    xc = qc.dequantize(pc, nc, zc, rc)
+    assert torch.allclose(xh.cpu()[same], xc[same], rtol=1e-4, atol=1e-4)
+
+
+def test_prod_hip_unbiased_inner_products():
+    """The reference's unbiasedness check (tests/test_algorithm.py:120-138):
+    over many random pairs the mean error of <x_hat, y> is near 0 and far
+    below the MSE-only estimator's bias, on the HIP path."""
+    print("case: algorithm Prod HIP unbiasedness", flush=True)
+    g = torch.Generator().manual_seed(3)
+    d = 128
+    x = torch.randn(4000, d, generator=g)
+    x = x / x.norm(dim=-1, keepdim=True)
+    y = torch.randn(4000, d, generator=g)
+    y = y / y.norm(dim=-1, keepdim=True)
+    q = A.TurboQuantProd(d, 2, device="cuda:0")
+    xh = q.dequantize(*q.quantize(x.cuda())).cpu()
+    err = ((xh * y).sum(-1) - (x * y).sum(-1))
+    # |mean| within 4 standard errors; the variance bound is pi / (2 d) per pair
+    se = math.sqrt(math.pi / (2 * d) / x.shape[0])
+    assert abs(err.mean().item()) < 4 * se + 1e-3

@@ -350,6 +350,29 @@ def test_mse_entry_points_refuse_bad_arguments():
     assert lib.tq_mse_quantize(null, 0, 128, 128, 4, null, tab, null, null, null) == 0
 
 
+def test_prod_entry_points_refuse_bad_arguments():
+    """tq_prod_quantize / tq_prod_dequantize argument checks (no GPU call):
+    the residual outputs and the QJL term are required, and the MSE checks
+    apply to the MSE stage's bit width."""
+    from turboquant_amd import _lib
+    lib = _lib.load()
+    null = None
+    tab = (ctypes.c_float * 16)()
+    assert lib.tq_prod_quantize(null, 4, 128, 128, 3, null, tab, tab, null, null, null, null,
+                                null) == -22
+    assert b"null pointer" in lib.tq_last_error()
+    assert lib.tq_prod_dequantize(null, null, null, null, 4, 128, 128, 3, null, tab, null,
+                                  null) == -22
+    assert b"null pointer" in lib.tq_last_error()
+    one = ctypes.c_void_p(16)  # never dereferenced: the checks fail first
+    assert lib.tq_prod_quantize(one, 4, 128, 128, 5, one, tab, tab, one, one, one, one,
+                                null) == -22
+    assert b"bit_width" in lib.tq_last_error()
+    assert lib.tq_prod_dequantize(one, one, one, one, 4, 60, 128, 3, one, tab, one,
+                                  null) == -22
+    assert b"padded_dim" in lib.tq_last_error()
+
+
 def test_ops_refuse_tensors_on_two_devices():
     """The ops check that every tensor is on one GPU before any launch (CPU
     tensors are refused the same way)."""

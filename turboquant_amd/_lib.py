@@ -51,10 +51,12 @@ SIGNATURES = {
     "tq_prefill_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
     "tq_mse_quantize": (_I32, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
     "tq_mse_dequantize": (_I32, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P]),
+    "tq_prod_quantize": (_I32, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "tq_prod_dequantize": (_I32, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P]),
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_abi_version": (_I32, []),
 }
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 

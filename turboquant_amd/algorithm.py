@@ -236,7 +236,16 @@ class TurboQuantProd:
 
     @torch.no_grad()
     def quantize(self, x: torch.Tensor):
-        """-> (mse_packed, mse_norms, qjl_signs int8 {-1, +1}, residual_norms)."""
+        """-> (mse_packed, mse_norms, qjl_signs int8 {-1, +1}, residual_norms).
+        fp32 vectors on a GPU take one HIP kernel (tq_prod_quantize: the MSE
+        stage, its read-back and the unit residual) and the QJL GEMM."""
+        if x.dtype == torch.float32 and self.mse._hip(x):
+            from . import ops
+            bnd, cen = self.mse._host_tables()
+            packed, norms, ru, rn = ops.prod_quantize(x, self.mse.rotation.padded_dim,
+                                                      self.mse.bit_width,
+                                                      self.mse.rotation.signs, bnd, cen)
+            return packed, norms, self.qjl.quantize(ru), rn
         packed, norms = self.mse.quantize(x)
         r = x - self.mse.dequantize(packed, norms)
         rn = torch.linalg.vector_norm(r, dim=-1).clamp_min(1e-8)
@@ -244,5 +253,11 @@ class TurboQuantProd:
 
     @torch.no_grad()
     def dequantize(self, mse_packed, mse_norms, qjl_signs, residual_norms) -> torch.Tensor:
+        if self.mse._hip(mse_packed) and mse_norms.dtype == torch.float32:
+            from . import ops
+            return ops.prod_dequantize(mse_packed, mse_norms, qjl_signs.float() @ self.qjl.S,
+                                       residual_norms, self.dim, self.mse.rotation.padded_dim,
+                                       self.mse.bit_width, self.mse.rotation.signs,
+                                       self.mse._host_tables()[1])
         return (self.mse.dequantize(mse_packed, mse_norms)
                 + self.qjl.dequantize_inner_product(qjl_signs, residual_norms))

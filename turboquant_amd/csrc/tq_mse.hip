@@ -43,10 +43,16 @@ struct MseParams {
   float* norms;        // quantize out / dequantize in: [n]
   float* out;          // dequantize out: [n, dim]
   const float* signs;  // [pd]
+  float* resid;        // prod quantize out: unit residual [n, dim] (null: MSE only)
+  float* rnorm;        // prod quantize out: residual norms [n]
+  const float* add;    // prod dequantize in: S^T z rows [n, dim] (null: MSE only)
+  const float* gamma;  // prod dequantize in: residual norms [n]
+  float add_scale;     // sqrt(pi / 2) / dim
   int64_t n;
   int dim, nbytes;
   float inv_sqrt_pd;
   float table[16];     // boundaries (quantize, levels - 1 used) or centroids
+  float cen[16];       // centroids for the prod quantize's read-back
   int levels;
 };
 
@@ -121,7 +127,13 @@ __device__ __forceinline__ float apply_sign(float v, float s) {
 // (whole 16-byte pieces per load, and its E / per code bytes contiguous for
 // the stores); measured faster here than the dequantize kernel's chunk
 // layout (127 against 161 us on 1M x 128 at 4 bits).
-template <int PD, int BITS>
+//
+// With RES (TurboQuantProd's first stage, reference quantizer.py:137-143) the
+// kernel also reads its codes back as the dequantize kernel does (centroids,
+// the same ascending-stride FWHT, scale, sign, norm: the same fp32 bits),
+// forms the residual r = x - x_hat over the first dim dims, its norm
+// rn = max(||r||, 1e-8) and r / rn correctly rounded, and stores those two.
+template <int PD, int BITS, bool RES>
 __global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) {
 #pragma clang fp contract(off)
   using MG = MseGeom<PD>;
@@ -129,7 +141,9 @@ __global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) 
   constexpr int PER = BITS == 3 ? 2 : 8 / BITS;  // codes per byte
   constexpr int NB = E / PER;                    // packed bytes per lane
   __shared__ float bnd[16];
+  __shared__ float cen[16];
   if (threadIdx.x < 16) bnd[threadIdx.x] = p.table[threadIdx.x];
+  if (RES && threadIdx.x >= 16 && threadIdx.x < 32) cen[threadIdx.x - 16] = p.cen[threadIdx.x - 16];
   __syncthreads();
   const int lane = threadIdx.x & 63, sub = lane % P;
   const int64_t row = (int64_t)blockIdx.x * MG::VPB + threadIdx.x / P;
@@ -150,6 +164,11 @@ __global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) 
     const float* src = p.x + (live ? row : 0) * p.dim;
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = (live && d0 + i < p.dim) ? src[d0 + i] : 0.0f;
+  }
+  float xo[RES ? E : 1];
+  if constexpr (RES) {
+#pragma unroll
+    for (int i = 0; i < E; i++) xo[i] = v[i];
   }
   // ||x||: the lane's squares in dim order, then across the vector's lanes
   float ss = 0.0f;
@@ -188,6 +207,42 @@ __global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) 
     if (y != y) c = NBND;  // NaN: torch.bucketize's top index
     const int byte = i / PER, slot = i % PER;
     word[byte / 4] |= (uint32_t)c << (8 * (byte % 4) + BITS * slot);
+    if constexpr (RES) v[i] = cen[c];
+  }
+  if constexpr (RES) {
+    fwht_contig<E, P>(v, sub);
+    float rs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const float xh = apply_sign(v[i] * p.inv_sqrt_pd, sgn[i]) * nrm;
+      v[i] = d0 + i < p.dim ? xo[i] - xh : 0.0f;
+      rs = __builtin_fmaf(v[i], v[i], rs);
+    }
+#pragma unroll
+    for (int m = 1; m < P; m <<= 1) rs += lane_xor(rs, m);
+    const float rq = sqrtf(rs);
+    const float rn = rq < 1e-8f ? 1e-8f : rq;
+    const float ry = 1.0f / rn;
+#pragma unroll
+    for (int i = 0; i < E; i++) {  // r / rn correctly rounded, as x / n above
+      const float q = v[i] * ry;
+      const float r = __builtin_fmaf(-q, rn, v[i]);
+      v[i] = __builtin_fmaf(r, ry, q);
+    }
+    if (live) {
+      if (sub == 0) p.rnorm[row] = rn;
+      float* rrow = p.resid + row * p.dim;
+      if (p.dim == PD) {
+#pragma unroll
+        for (int i = 0; i < E / 4; i++)
+          reinterpret_cast<float4*>(rrow + d0)[i] =
+              float4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+      } else {
+#pragma unroll
+        for (int i = 0; i < E; i++)
+          if (d0 + i < p.dim) rrow[d0 + i] = v[i];
+      }
+    }
   }
   if (!live) return;
   if (sub == 0) p.norms[row] = nrm;
@@ -202,7 +257,10 @@ __global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) 
   }
 }
 
-template <int PD, int BITS>
+// With ADD (TurboQuantProd's dequantize, reference quantizer.py:145-158 and
+// qjl.py:46-63) each output gains the QJL term a_d * (add_scale * gamma) in
+// torch's order: the row's weight first, then the product, then the sum.
+template <int PD, int BITS, bool ADD>
 __global__ __launch_bounds__(kMseThreads) void mse_dequantize_kernel(MseParams p) {
 #pragma clang fp contract(off)
   using MG = MseGeom<PD>;
@@ -237,8 +295,13 @@ __global__ __launch_bounds__(kMseThreads) void mse_dequantize_kernel(MseParams p
   fwht_group<E, P>(v, sub);
   if (!live) return;
   float* orow = p.out + row * p.dim;
+  const float* arow = ADD ? p.add + row * p.dim : nullptr;
+  const float wq = ADD ? p.add_scale * p.gamma[row] : 0.0f;
   auto val = [&](int i) {
-    return apply_sign(v[i] * p.inv_sqrt_pd, p.signs[8 * (sub + P * (i / 8)) + i % 8]) * nrm;
+    const int d = 8 * (sub + P * (i / 8)) + i % 8;
+    const float xm = apply_sign(v[i] * p.inv_sqrt_pd, p.signs[d]) * nrm;
+    if constexpr (ADD) return xm + arow[d] * wq;
+    else return xm;
   };
   if (p.dim == PD) {
 #pragma unroll
@@ -260,12 +323,16 @@ template <int PD>
 hipError_t launch_mse(bool quant, int bits, const MseParams& p, hipStream_t st) {
   const dim3 grid((unsigned)((p.n + MseGeom<PD>::VPB - 1) / MseGeom<PD>::VPB));
   const dim3 block(kMseThreads);
-#define TQ_MSE_CASE(B)                                                              \
-  case B:                                                                           \
-    if (quant)                                                                      \
-      hipLaunchKernelGGL((mse_quantize_kernel<PD, B>), grid, block, 0, st, p);      \
-    else                                                                            \
-      hipLaunchKernelGGL((mse_dequantize_kernel<PD, B>), grid, block, 0, st, p);    \
+#define TQ_MSE_CASE(B)                                                                   \
+  case B:                                                                                \
+    if (quant && p.resid)                                                                \
+      hipLaunchKernelGGL((mse_quantize_kernel<PD, B, true>), grid, block, 0, st, p);     \
+    else if (quant)                                                                      \
+      hipLaunchKernelGGL((mse_quantize_kernel<PD, B, false>), grid, block, 0, st, p);    \
+    else if (p.add)                                                                      \
+      hipLaunchKernelGGL((mse_dequantize_kernel<PD, B, true>), grid, block, 0, st, p);   \
+    else                                                                                 \
+      hipLaunchKernelGGL((mse_dequantize_kernel<PD, B, false>), grid, block, 0, st, p);  \
     break;
   switch (bits) {
     TQ_MSE_CASE(1)
@@ -279,10 +346,20 @@ hipError_t launch_mse(bool quant, int bits, const MseParams& p, hipStream_t st) 
   return hipGetLastError();
 }
 
+// The extra operands of the prod variants (all null for the MSE entry points)
+struct ProdArgs {
+  const float* centroids = nullptr;  // quantize: read-back table
+  float* resid = nullptr;
+  float* rnorm = nullptr;
+  const float* add = nullptr;  // dequantize
+  const float* gamma = nullptr;
+  float add_scale = 0.0f;
+};
+
 int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* out,
              int64_t n, int32_t dim, int32_t padded_dim, int32_t bit_width, const float* signs,
-             const float* table, tq_stream_t stream) {
-  const char* what = quant ? "mse_quantize" : "mse_dequantize";
+             const float* table, tq_stream_t stream, const char* what,
+             const ProdArgs& pa = ProdArgs()) {
   if (bit_width < 1 || bit_width > 4) {
     set_error("%s: bit_width %d unsupported (1..4)", what, bit_width);
     return kEinval;
@@ -302,9 +379,15 @@ int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* o
     set_error("%s: null pointer", what);
     return kEinval;
   }
+  const bool prod_q = pa.resid || pa.rnorm || pa.centroids;
+  const bool prod_d = pa.add || pa.gamma;
+  if ((prod_q && !(pa.resid && pa.rnorm && pa.centroids)) || (prod_d && !(pa.add && pa.gamma))) {
+    set_error("%s: null pointer", what);
+    return kEinval;
+  }
   // full-width rows are read / written as float4, packed rows as dwords
   const uintptr_t al = (uintptr_t)(quant ? (const void*)x : (const void*)out) |
-                       (uintptr_t)packed;
+                       (uintptr_t)packed | (uintptr_t)pa.resid;
   if ((al & 15) != 0) {
     set_error("%s: x / out and packed must be 16-byte aligned", what);
     return kEinval;
@@ -316,6 +399,11 @@ int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* o
   p.norms = norms;
   p.out = out;
   p.signs = signs;
+  p.resid = pa.resid;
+  p.rnorm = pa.rnorm;
+  p.add = pa.add;
+  p.gamma = pa.gamma;
+  p.add_scale = pa.add_scale;
   p.n = n;
   p.dim = dim;
   p.nbytes = padded_dim / per;
@@ -323,6 +411,7 @@ int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* o
   p.levels = 1 << bit_width;
   for (int i = 0; i < 16; i++) p.table[i] = 0.0f;
   for (int i = 0; i < (quant ? p.levels - 1 : p.levels); i++) p.table[i] = table[i];
+  for (int i = 0; i < 16; i++) p.cen[i] = (pa.centroids && i < p.levels) ? pa.centroids[i] : 0.0f;
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   switch (padded_dim) {
@@ -344,7 +433,7 @@ extern "C" int tq_mse_quantize(const float* x, int64_t num_vectors, int32_t dim,
                                const float* boundaries, uint8_t* packed, float* norms,
                                tq_stream_t stream) {
   return tq::mse_call(true, x, packed, norms, nullptr, num_vectors, dim, padded_dim, bit_width,
-                      signs, boundaries, stream);
+                      signs, boundaries, stream, "mse_quantize");
 }
 
 extern "C" int tq_mse_dequantize(const uint8_t* packed, const float* norms, int64_t num_vectors,
@@ -352,5 +441,41 @@ extern "C" int tq_mse_dequantize(const uint8_t* packed, const float* norms, int6
                                  const float* signs, const float* centroids, float* out,
                                  tq_stream_t stream) {
   return tq::mse_call(false, nullptr, const_cast<uint8_t*>(packed), const_cast<float*>(norms),
-                      out, num_vectors, dim, padded_dim, bit_width, signs, centroids, stream);
+                      out, num_vectors, dim, padded_dim, bit_width, signs, centroids, stream,
+                      "mse_dequantize");
+}
+
+extern "C" int tq_prod_quantize(const float* x, int64_t num_vectors, int32_t dim,
+                                int32_t padded_dim, int32_t mse_bit_width, const float* signs,
+                                const float* boundaries, const float* centroids, uint8_t* packed,
+                                float* norms, float* residual_unit, float* residual_norms,
+                                tq_stream_t stream) {
+  tq::ProdArgs pa;
+  pa.centroids = centroids;
+  pa.resid = residual_unit;
+  pa.rnorm = residual_norms;
+  if (!centroids || !residual_unit || !residual_norms) {
+    tq::set_error("prod_quantize: null pointer");
+    return tq::kEinval;
+  }
+  return tq::mse_call(true, x, packed, norms, nullptr, num_vectors, dim, padded_dim,
+                      mse_bit_width, signs, boundaries, stream, "prod_quantize", pa);
+}
+
+extern "C" int tq_prod_dequantize(const uint8_t* packed, const float* norms,
+                                  const float* qjl_term, const float* residual_norms,
+                                  int64_t num_vectors, int32_t dim, int32_t padded_dim,
+                                  int32_t mse_bit_width, const float* signs,
+                                  const float* centroids, float* out, tq_stream_t stream) {
+  tq::ProdArgs pa;
+  pa.add = qjl_term;
+  pa.gamma = residual_norms;
+  pa.add_scale = (float)(std::sqrt(M_PI / 2.0) / dim);
+  if (!qjl_term || !residual_norms) {
+    tq::set_error("prod_dequantize: null pointer");
+    return tq::kEinval;
+  }
+  return tq::mse_call(false, nullptr, const_cast<uint8_t*>(packed), const_cast<float*>(norms),
+                      out, num_vectors, dim, padded_dim, mse_bit_width, signs, centroids, stream,
+                      "prod_dequantize", pa);
 }

@@ -355,6 +355,69 @@ def mse_dequantize(packed: torch.Tensor, norms: torch.Tensor, dim: int, padded_d
     return out
 
 
+def prod_quantize(x: torch.Tensor, padded_dim: int, mse_bit_width: int, signs: torch.Tensor,
+                  boundaries, centroids):
+    """TurboQuantProd's MSE stage and residual on the GPU (tq_prod_quantize):
+    x fp32 [..., dim] -> (packed, norms, residual_unit fp32 [..., dim],
+    residual_norms fp32 [...]); packed and norms are mse_quantize's."""
+    _require_gpu(x, signs)
+    if x.dtype != torch.float32:
+        raise RuntimeError("prod_quantize: x must be fp32")
+    if signs.dtype != torch.float32 or signs.numel() < padded_dim:
+        raise RuntimeError("prod_quantize: signs must be fp32 [padded_dim]")
+    x = x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    dim = x.shape[-1]
+    lead = x.shape[:-1]
+    n = x.numel() // dim if dim else 0
+    per = 2 if mse_bit_width == 3 else 8 // mse_bit_width
+    packed = torch.empty((*lead, padded_dim // per), dtype=torch.uint8, device=x.device)
+    norms = torch.empty(lead, dtype=torch.float32, device=x.device)
+    resid = torch.empty((*lead, dim), dtype=torch.float32, device=x.device)
+    rnorm = torch.empty(lead, dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        rc = lib.tq_prod_quantize(x.data_ptr(), n, dim, int(padded_dim), int(mse_bit_width),
+                                  signs.data_ptr(), _host_f32(boundaries), _host_f32(centroids),
+                                  packed.data_ptr(), norms.data_ptr(), resid.data_ptr(),
+                                  rnorm.data_ptr(), _stream_ptr(x.device))
+    _lib.check(rc, "prod_quantize")
+    return packed, norms, resid, rnorm
+
+
+def prod_dequantize(packed: torch.Tensor, norms: torch.Tensor, qjl_term: torch.Tensor,
+                    residual_norms: torch.Tensor, dim: int, padded_dim: int, mse_bit_width: int,
+                    signs: torch.Tensor, centroids) -> torch.Tensor:
+    """TurboQuantProd.dequantize on the GPU (tq_prod_dequantize): the MSE
+    read-back plus qjl_term * (sqrt(pi/2) / dim * residual_norms), qjl_term
+    being z S (fp32 [..., dim])."""
+    _require_gpu(packed, norms, qjl_term, residual_norms, signs)
+    per = 2 if mse_bit_width == 3 else 8 // mse_bit_width
+    if packed.dtype != torch.uint8 or packed.shape[-1] != padded_dim // per:
+        raise RuntimeError("prod_dequantize: packed must be uint8 [..., padded_dim / per]")
+    lead = tuple(packed.shape[:-1])
+    if tuple(norms.shape) != lead or tuple(residual_norms.shape) != lead:
+        raise RuntimeError("prod_dequantize: norms must match packed's leading dims")
+    if tuple(qjl_term.shape) != (*lead, dim):
+        raise RuntimeError("prod_dequantize: qjl_term must be [..., dim]")
+    packed = packed.contiguous()
+    if packed.data_ptr() % 16:
+        packed = packed.clone()
+    nf = norms.to(torch.float32).contiguous()
+    rn = residual_norms.to(torch.float32).contiguous()
+    qt = qjl_term.to(torch.float32).contiguous()
+    out = torch.empty((*lead, dim), dtype=torch.float32, device=packed.device)
+    lib = _lib.load()
+    with torch.cuda.device(packed.device):
+        rc = lib.tq_prod_dequantize(packed.data_ptr(), nf.data_ptr(), qt.data_ptr(),
+                                    rn.data_ptr(), nf.numel(), int(dim), int(padded_dim),
+                                    int(mse_bit_width), signs.data_ptr(), _host_f32(centroids),
+                                    out.data_ptr(), _stream_ptr(packed.device))
+    _lib.check(rc, "prod_dequantize")
+    return out
+
+
 # --------------------------------------------------------------------------
 # torch.library registration under the reference's namespaces and schemas
 # --------------------------------------------------------------------------
