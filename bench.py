@@ -467,11 +467,14 @@ def bench_mse(torch, steps, warmup, n=1 << 20, dim=128, bits=4):
 
 def bench_prod(torch, steps, warmup, n=1 << 20, dim=128, bits=4):
     """TurboQuantProd on the GPU: n fp32 vectors of dim 128 at 4 bits (MSE
-    stage at 3).  Kernel rows: tq_prod_quantize reads 4 dim and writes the
-    codes, norm, 4 dim of unit residual and its norm per vector;
-    tq_prod_dequantize reads the codes, norm, 4 dim of QJL term and the
-    residual norm and writes 4 dim.  The API rows add the two d x d fp32
-    QJL GEMMs (library BLAS) and the sign."""
+    stage at 3), through the public API, which at this size is one kernel
+    each way with the QJL products on the matrix cores
+    (tq_prod_quantize_qjl / tq_prod_dequantize_qjl).  Algorithmic bytes per
+    vector: quantize reads 4 dim and writes the codes, norm, dim int8 signs
+    and residual norm; dequantize the reverse.  MFMA work per vector: 3 (or
+    2) fp16 d x d products.  Also timed: the same with the QJL products as
+    fp32 BLAS GEMMs (tq_prod_quantize / tq_prod_dequantize around them), the
+    path above padded size 128."""
     from turboquant_amd import algorithm as A
     from turboquant_amd import ops
     dev = torch.device("cuda:0")
@@ -481,24 +484,31 @@ def bench_prod(torch, steps, warmup, n=1 << 20, dim=128, bits=4):
     pd = m.rotation.padded_dim
     bnd, cen = m._host_tables()
     pk, nm, z, rn = q.quantize(x)
-    term = z.float() @ q.qjl.S
     per = 2 if bits - 1 == 3 else 8 // (bits - 1)
     code_bytes = pd // per + 4
-    ms_kq = time_graph(torch, lambda: ops.prod_quantize(x, pd, bits - 1, m.rotation.signs, bnd,
-                                                        cen), steps, warmup)
-    ms_kd = time_graph(torch, lambda: ops.prod_dequantize(pk, nm, term, rn, dim, pd, bits - 1,
-                                                          m.rotation.signs, cen), steps, warmup)
     ms_q = time_graph(torch, lambda: q.quantize(x), steps, warmup)
     ms_d = time_graph(torch, lambda: q.dequantize(pk, nm, z, rn), steps, warmup)
-    bkq = n * (4 * dim + code_bytes + 4 * dim + 4)
-    bkd = n * (code_bytes + 4 * dim + 4 + 4 * dim)
-    return {"quantize_kernel_us": round(ms_kq * 1e3, 2),
-            "quantize_kernel_GB/s": round(bkq / (ms_kq * 1e-3) / 1e9, 1),
-            "dequantize_kernel_us": round(ms_kd * 1e3, 2),
-            "dequantize_kernel_GB/s": round(bkd / (ms_kd * 1e-3) / 1e9, 1),
-            "quantize_api_us": round(ms_q * 1e3, 2), "dequantize_api_us": round(ms_d * 1e3, 2),
-            "config": f"TurboQuantProd({dim}, {bits}) on {n} fp32 vectors (HIP kernels + "
-                      "fp32 BLAS GEMMs for QJL; output allocation inside the timed calls)"}
+
+    def blas_q():
+        p2, n2, ru, r2 = ops.prod_quantize(x, pd, bits - 1, m.rotation.signs, bnd, cen)
+        return q.qjl.quantize(ru)
+
+    def blas_d():
+        return ops.prod_dequantize(pk, nm, z.float() @ q.qjl.S, rn, dim, pd, bits - 1,
+                                   m.rotation.signs, cen)
+    ms_bq = time_graph(torch, blas_q, max(1, steps // 4), max(1, warmup // 4))
+    ms_bd = time_graph(torch, blas_d, max(1, steps // 4), max(1, warmup // 4))
+    bq = n * (4 * dim + code_bytes + dim + 4)
+    return {"quantize_us": round(ms_q * 1e3, 2),
+            "quantize_GB/s": round(bq / (ms_q * 1e-3) / 1e9, 1),
+            "dequantize_us": round(ms_d * 1e3, 2),
+            "dequantize_GB/s": round(bq / (ms_d * 1e-3) / 1e9, 1), "alg_bytes": bq,
+            "mfma_TFLOP/s": [round(n * 6 * pd * pd / (ms_q * 1e-3) / 1e12, 1),
+                             round(n * 4 * pd * pd / (ms_d * 1e-3) / 1e12, 1)],
+            "blas_path_us": [round(ms_bq * 1e3, 2), round(ms_bd * 1e3, 2)],
+            "config": f"TurboQuantProd({dim}, {bits}) on {n} fp32 vectors: fused HIP kernels "
+                      "(QJL on MFMA); blas_path_us = the kernels around fp32 BLAS GEMMs; "
+                      "output allocation inside the timed calls"}
 
 
 def bench_dequant(torch, w, steps, warmup):
@@ -608,10 +618,9 @@ def main():
     if not quick:
         mse = bench_mse(torch, args.steps, args.warmup)
         log(f"algorithm MSE quantize {mse['quantize_us']} us, dequantize {mse['dequantize_us']} us")
-        prod = bench_prod(torch, args.steps // 4, args.warmup // 4)
-        log(f"algorithm Prod kernels {prod['quantize_kernel_us']} / "
-            f"{prod['dequantize_kernel_us']} us, API {prod['quantize_api_us']} / "
-            f"{prod['dequantize_api_us']} us")
+        prod = bench_prod(torch, args.steps // 2, args.warmup // 2)
+        log(f"algorithm Prod quantize {prod['quantize_us']} us, dequantize "
+            f"{prod['dequantize_us']} us (BLAS path {prod['blas_path_us']})")
         wr = bench_write(torch, args.steps, args.warmup)
         log(f"write kernel {wr['us']} us -> {wr['GB/s']} GB/s")
         dq = bench_dequant(torch, w, args.steps, args.warmup)

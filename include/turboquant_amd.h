@@ -316,6 +316,34 @@ int tq_prod_dequantize(const uint8_t* packed, const float* norms, const float* q
                        const float* centroids, float* out, tq_stream_t stream);
 
 /*
+ * TurboQuantProd with the QJL projections on the GPU's matrix cores, for
+ * padded_dim 64 or 128 (dim <= 128): the whole of quantizer.py:137-158 and
+ * qjl.py:36-63 in one kernel each.  s_hi / s_lo (quantize) are the QJL
+ * matrix S [dim, dim] as fp16 halves with S = hi + lo to 22 bits, zero-padded
+ * to [padded_dim, padded_dim], row-major; st_hi / st_lo (dequantize) the same
+ * of S^T.  16-byte aligned device arrays.
+ *
+ * tq_prod_quantize_qjl: tq_prod_quantize's packed, norms and residual_norms,
+ *   and qjl_signs int8 [num_vectors, dim] = +1 where (S r)_j >= 0, else -1,
+ *   r the unit residual (the reference's sign() with 0 -> +1).  The product
+ *   is formed from the fp16 halves of S and r with fp32 accumulation, so a
+ *   sign may differ from an fp32 GEMM's where |(S r)_j| is within about
+ *   2^-22 |S_j| of 0.
+ * tq_prod_dequantize_qjl: tq_prod_dequantize with qjl_term = z S formed
+ *   in-kernel from qjl_signs (exact +-1 times the two halves of S).
+ */
+int tq_prod_quantize_qjl(const float* x, int64_t num_vectors, int32_t dim, int32_t padded_dim,
+                         int32_t mse_bit_width, const float* signs, const float* boundaries,
+                         const float* centroids, const void* s_hi, const void* s_lo,
+                         uint8_t* packed, float* norms, int8_t* qjl_signs,
+                         float* residual_norms, tq_stream_t stream);
+int tq_prod_dequantize_qjl(const uint8_t* packed, const float* norms, const int8_t* qjl_signs,
+                           const float* residual_norms, int64_t num_vectors, int32_t dim,
+                           int32_t padded_dim, int32_t mse_bit_width, const float* signs,
+                           const float* centroids, const void* st_hi, const void* st_lo,
+                           float* out, tq_stream_t stream);
+
+/*
  * Diagnostic, no counterpart in the reference: tq_decode_partials at head
  * size 128 with 8 kv heads per workgroup (the configs[2] geometry) with parts
  * compiled out.  mode 1: the attention math (the same page walk, LDS copy

@@ -371,6 +371,18 @@ def test_prod_entry_points_refuse_bad_arguments():
     assert lib.tq_prod_dequantize(one, one, one, one, 4, 60, 128, 3, one, tab, one,
                                   null) == -22
     assert b"padded_dim" in lib.tq_last_error()
+    # the fused QJL kernels: padded sizes 64 and 128 only, all operands required
+    assert lib.tq_prod_quantize_qjl(one, 4, 200, 256, 3, one, tab, tab, one, one, one, one, one,
+                                    one, null) == -22
+    assert b"padded_dim" in lib.tq_last_error()
+    assert lib.tq_prod_quantize_qjl(one, 4, 128, 128, 3, one, tab, tab, null, one, one, one, one,
+                                    one, null) == -22
+    assert b"null pointer" in lib.tq_last_error()
+    assert lib.tq_prod_dequantize_qjl(one, one, one, one, 4, 128, 128, 3, one, tab, one, null,
+                                      one, null) == -22
+    assert b"null pointer" in lib.tq_last_error()
+    assert lib.tq_prod_dequantize_qjl(one, one, one, one, 0, 128, 128, 3, one, tab, one, one,
+                                      one, null) == 0
 
 
 def test_ops_refuse_tensors_on_two_devices():

@@ -53,10 +53,14 @@ SIGNATURES = {
     "tq_mse_dequantize": (_I32, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P]),
     "tq_prod_quantize": (_I32, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tq_prod_dequantize": (_I32, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P]),
+    "tq_prod_quantize_qjl": (_I32, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P,
+                                    _P, _P]),
+    "tq_prod_dequantize_qjl": (_I32, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P,
+                                      _P, _P]),
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_abi_version": (_I32, []),
 }
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 

@@ -164,10 +164,30 @@ class QJL:
         g.manual_seed(seed)
         self.S = torch.randn(dim, dim, generator=g).to(device)
 
+    def halves(self, padded_dim: int):
+        """(S_hi, S_lo, S^T_hi, S^T_lo): fp16 halves with S = hi + lo (to 22
+        bits), zero-padded to [padded_dim, padded_dim], for the fused kernels
+        (made once per padded size and device)."""
+        cache = self.__dict__.setdefault("_halves", {})
+        key = (padded_dim, str(self.S.device))
+        if key not in cache:
+            out = []
+            for m in (self.S, self.S.t()):
+                hi = m.half()
+                lo = (m - hi.float()).half()
+                for h in (hi, lo):
+                    pad = torch.zeros((padded_dim, padded_dim), dtype=torch.float16,
+                                      device=self.S.device)
+                    pad[:self.dim, :self.dim] = h
+                    out.append(pad)
+            cache[key] = (out[0], out[1], out[2], out[3])
+        return cache[key]
+
     @torch.no_grad()
     def quantize(self, x: torch.Tensor) -> torch.Tensor:
         proj = x.float() @ self.S.t()
-        return torch.where(proj >= 0, 1, -1).to(torch.int8)
+        # sign() with 0 -> +1, without an int64 intermediate
+        return (proj >= 0).to(torch.int8).mul_(2).sub_(1)
 
     @torch.no_grad()
     def dequantize_inner_product(self, signs: torch.Tensor,
@@ -237,11 +257,18 @@ class TurboQuantProd:
     @torch.no_grad()
     def quantize(self, x: torch.Tensor):
         """-> (mse_packed, mse_norms, qjl_signs int8 {-1, +1}, residual_norms).
-        fp32 vectors on a GPU take one HIP kernel (tq_prod_quantize: the MSE
-        stage, its read-back and the unit residual) and the QJL GEMM."""
+        fp32 vectors on a GPU take one HIP kernel: up to padded size 128 the
+        whole algorithm with the QJL product on the matrix cores
+        (tq_prod_quantize_qjl), above it the MSE stage, its read-back and the
+        unit residual (tq_prod_quantize) followed by the QJL GEMM."""
         if x.dtype == torch.float32 and self.mse._hip(x):
             from . import ops
             bnd, cen = self.mse._host_tables()
+            pd = self.mse.rotation.padded_dim
+            if pd <= 128:  # QJL product fused on the matrix cores
+                sh, sl, _, _ = self.qjl.halves(pd)
+                return ops.prod_quantize_qjl(x, pd, self.mse.bit_width, self.mse.rotation.signs,
+                                             bnd, cen, sh, sl)
             packed, norms, ru, rn = ops.prod_quantize(x, self.mse.rotation.padded_dim,
                                                       self.mse.bit_width,
                                                       self.mse.rotation.signs, bnd, cen)
@@ -255,6 +282,13 @@ class TurboQuantProd:
     def dequantize(self, mse_packed, mse_norms, qjl_signs, residual_norms) -> torch.Tensor:
         if self.mse._hip(mse_packed) and mse_norms.dtype == torch.float32:
             from . import ops
+            pd = self.mse.rotation.padded_dim
+            if pd <= 128 and qjl_signs.dtype == torch.int8:
+                _, _, th, tl = self.qjl.halves(pd)
+                return ops.prod_dequantize_qjl(mse_packed, mse_norms, qjl_signs, residual_norms,
+                                               self.dim, pd, self.mse.bit_width,
+                                               self.mse.rotation.signs,
+                                               self.mse._host_tables()[1], th, tl)
             return ops.prod_dequantize(mse_packed, mse_norms, qjl_signs.float() @ self.qjl.S,
                                        residual_norms, self.dim, self.mse.rotation.padded_dim,
                                        self.mse.bit_width, self.mse.rotation.signs,

@@ -28,6 +28,7 @@
 // norm's sqrt and its correctly rounded reciprocal) is shared by the P lanes
 // and each lane's codes pack in its own registers.  HBM-bound in bytes:
 // 4 dim + pd*b/8 + 4 per vector.
+#include <atomic>
 #include <cmath>
 
 #include "tq_common.h"
@@ -129,27 +130,18 @@ __device__ __forceinline__ float apply_sign(float v, float s) {
 // layout (127 against 161 us on 1M x 128 at 4 bits).
 //
 // With RES (TurboQuantProd's first stage, reference quantizer.py:137-143) the
-// kernel also reads its codes back as the dequantize kernel does (centroids,
+// row also reads its codes back as the dequantize kernel does (centroids,
 // the same ascending-stride FWHT, scale, sign, norm: the same fp32 bits),
 // forms the residual r = x - x_hat over the first dim dims, its norm
-// rn = max(||r||, 1e-8) and r / rn correctly rounded, and stores those two.
-template <int PD, int BITS, bool RES>
-__global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) {
-#pragma clang fp contract(off)
-  using MG = MseGeom<PD>;
-  constexpr int P = MG::P, E = MG::E;
-  constexpr int PER = BITS == 3 ? 2 : 8 / BITS;  // codes per byte
-  constexpr int NB = E / PER;                    // packed bytes per lane
-  __shared__ float bnd[16];
-  __shared__ float cen[16];
-  if (threadIdx.x < 16) bnd[threadIdx.x] = p.table[threadIdx.x];
-  if (RES && threadIdx.x >= 16 && threadIdx.x < 32) cen[threadIdx.x - 16] = p.cen[threadIdx.x - 16];
-  __syncthreads();
-  const int lane = threadIdx.x & 63, sub = lane % P;
-  const int64_t row = (int64_t)blockIdx.x * MG::VPB + threadIdx.x / P;
+// rn = max(||r||, 1e-8) (stored) and r / rn correctly rounded, left in v
+// (0 beyond dim).  Every lane of the workgroup runs this, live or not (the
+// lane exchanges need the whole vector group); only live rows store.
+template <int PD>
+__device__ __forceinline__ void load_row(const MseParams& p, int64_t row, int sub,
+                                         float (&v)[MseGeom<PD>::E]) {
+  constexpr int E = MseGeom<PD>::E;
   const bool live = row < p.n;
   const int d0 = sub * E;
-  float v[E];
   if (live && p.dim == PD) {
     const float4* src = reinterpret_cast<const float4*>(p.x + row * PD + d0);
 #pragma unroll
@@ -165,6 +157,20 @@ __global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) 
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = (live && d0 + i < p.dim) ? src[d0 + i] : 0.0f;
   }
+}
+
+// v holds the row as load_row leaves it
+template <int PD, int BITS, bool RES>
+__device__ __forceinline__ void quantize_row(const MseParams& p, const float* bnd,
+                                             const float* cen, int64_t row, int sub,
+                                             float (&v)[MseGeom<PD>::E]) {
+#pragma clang fp contract(off)
+  using MG = MseGeom<PD>;
+  constexpr int P = MG::P, E = MG::E;
+  constexpr int PER = BITS == 3 ? 2 : 8 / BITS;  // codes per byte
+  constexpr int NB = E / PER;                    // packed bytes per lane
+  const bool live = row < p.n;
+  const int d0 = sub * E;
   float xo[RES ? E : 1];
   if constexpr (RES) {
 #pragma unroll
@@ -229,20 +235,7 @@ __global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) 
       const float r = __builtin_fmaf(-q, rn, v[i]);
       v[i] = __builtin_fmaf(r, ry, q);
     }
-    if (live) {
-      if (sub == 0) p.rnorm[row] = rn;
-      float* rrow = p.resid + row * p.dim;
-      if (p.dim == PD) {
-#pragma unroll
-        for (int i = 0; i < E / 4; i++)
-          reinterpret_cast<float4*>(rrow + d0)[i] =
-              float4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
-      } else {
-#pragma unroll
-        for (int i = 0; i < E; i++)
-          if (d0 + i < p.dim) rrow[d0 + i] = v[i];
-      }
-    }
+    if (live && sub == 0) p.rnorm[row] = rn;
   }
   if (!live) return;
   if (sub == 0) p.norms[row] = nrm;
@@ -257,35 +250,85 @@ __global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) 
   }
 }
 
-// With ADD (TurboQuantProd's dequantize, reference quantizer.py:145-158 and
-// qjl.py:46-63) each output gains the QJL term a_d * (add_scale * gamma) in
-// torch's order: the row's weight first, then the product, then the sum.
+template <int PD, int BITS, bool RES>
+__global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) {
+  using MG = MseGeom<PD>;
+  constexpr int P = MG::P, E = MG::E;
+  __shared__ float bnd[16];
+  __shared__ float cen[16];
+  if (threadIdx.x < 16) bnd[threadIdx.x] = p.table[threadIdx.x];
+  if (RES && threadIdx.x >= 16 && threadIdx.x < 32) cen[threadIdx.x - 16] = p.cen[threadIdx.x - 16];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, sub = lane % P;
+  const int64_t row = (int64_t)blockIdx.x * MG::VPB + threadIdx.x / P;
+  float v[E];
+  load_row<PD>(p, row, sub, v);
+  quantize_row<PD, BITS, RES>(p, bnd, cen, row, sub, v);
+  if constexpr (RES) {
+    if (row >= p.n) return;
+    const int d0 = sub * E;
+    float* rrow = p.resid + row * p.dim;
+    if (p.dim == PD) {
+#pragma unroll
+      for (int i = 0; i < E / 4; i++)
+        reinterpret_cast<float4*>(rrow + d0)[i] =
+            float4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; i++)
+        if (d0 + i < p.dim) rrow[d0 + i] = v[i];
+    }
+  }
+}
+
+// Dequantize of one row in the chunk layout (lane p: chunks of 8 dims at
+// 8 (p + P i)).  With ADD (TurboQuantProd's dequantize, reference
+// quantizer.py:145-158 and qjl.py:46-63) each output gains the QJL term
+// arow[d] * (add_scale * gamma) in torch's order: the row's weight first,
+// then the product, then the sum; arow may point to global memory or LDS.
+// a row's code words (chunk layout) and norm
+template <int PD, int BITS>
+struct RowCodes {
+  uint32_t word[MseGeom<PD>::E / 8];
+  float nrm;
+};
+
+template <int PD, int BITS>
+__device__ __forceinline__ RowCodes<PD, BITS> load_codes(const MseParams& p, int64_t row,
+                                                         int sub) {
+  using MG = MseGeom<PD>;
+  constexpr int P = MG::P, NC = MG::E / 8;
+  constexpr int PER = BITS == 3 ? 2 : 8 / BITS;
+  constexpr int CB = 8 / PER;
+  RowCodes<PD, BITS> rc;
+#pragma unroll
+  for (int i = 0; i < NC; i++) rc.word[i] = 0u;
+  rc.nrm = 0.0f;
+  if (row < p.n) {
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+      const uint8_t* src = p.packed + row * p.nbytes + (sub + P * i) * CB;
+      if constexpr (CB == 1) rc.word[i] = *src;
+      else if constexpr (CB == 2) rc.word[i] = *reinterpret_cast<const uint16_t*>(src);
+      else rc.word[i] = *reinterpret_cast<const uint32_t*>(src);
+    }
+    rc.nrm = p.norms[row];
+  }
+  return rc;
+}
+
 template <int PD, int BITS, bool ADD>
-__global__ __launch_bounds__(kMseThreads) void mse_dequantize_kernel(MseParams p) {
+__device__ __forceinline__ void dequantize_row(const MseParams& p, const float* cen, int64_t row,
+                                               int sub, const float* arow,
+                                               const RowCodes<PD, BITS>& rc) {
 #pragma clang fp contract(off)
   using MG = MseGeom<PD>;
   constexpr int P = MG::P, E = MG::E, NC = E / 8;
   constexpr int PER = BITS == 3 ? 2 : 8 / BITS;
-  constexpr int CB = 8 / PER;
   constexpr uint32_t kMask = (1u << BITS) - 1u;
-  __shared__ float cen[16];
-  if (threadIdx.x < 16) cen[threadIdx.x] = p.table[threadIdx.x];
-  __syncthreads();
-  const int lane = threadIdx.x & 63, sub = lane % P;
-  const int64_t row = (int64_t)blockIdx.x * MG::VPB + threadIdx.x / P;
   const bool live = row < p.n;
-  uint32_t word[NC] = {};
-  float nrm = 0.0f;
-  if (live) {
-#pragma unroll
-    for (int i = 0; i < NC; i++) {
-      const uint8_t* src = p.packed + row * p.nbytes + (sub + P * i) * CB;
-      if constexpr (CB == 1) word[i] = *src;
-      else if constexpr (CB == 2) word[i] = *reinterpret_cast<const uint16_t*>(src);
-      else word[i] = *reinterpret_cast<const uint32_t*>(src);
-    }
-    nrm = p.norms[row];
-  }
+  const uint32_t* word = rc.word;
+  const float nrm = rc.nrm;
   float v[E];
 #pragma unroll
   for (int i = 0; i < E; i++) {
@@ -295,7 +338,6 @@ __global__ __launch_bounds__(kMseThreads) void mse_dequantize_kernel(MseParams p
   fwht_group<E, P>(v, sub);
   if (!live) return;
   float* orow = p.out + row * p.dim;
-  const float* arow = ADD ? p.add + row * p.dim : nullptr;
   const float wq = ADD ? p.add_scale * p.gamma[row] : 0.0f;
   auto val = [&](int i) {
     const int d = 8 * (sub + P * (i / 8)) + i % 8;
@@ -316,6 +358,233 @@ __global__ __launch_bounds__(kMseThreads) void mse_dequantize_kernel(MseParams p
       const int d = 8 * (sub + P * (i / 8)) + i % 8;
       if (d < p.dim) orow[d] = val(i);
     }
+  }
+}
+
+template <int PD, int BITS, bool ADD>
+__global__ __launch_bounds__(kMseThreads) void mse_dequantize_kernel(MseParams p) {
+  using MG = MseGeom<PD>;
+  constexpr int P = MG::P;
+  __shared__ float cen[16];
+  if (threadIdx.x < 16) cen[threadIdx.x] = p.table[threadIdx.x];
+  __syncthreads();
+  const int sub = (threadIdx.x & 63) % P;
+  const int64_t row = (int64_t)blockIdx.x * MG::VPB + threadIdx.x / P;
+  dequantize_row<PD, BITS, ADD>(p, cen, row, sub,
+                                ADD && row < p.n ? p.add + row * p.dim : nullptr,
+                                load_codes<PD, BITS>(p, row, sub));
+}
+
+// --------------------------------------------------------------------------
+// TurboQuantProd with the QJL projections on the matrix cores (padded size 64
+// or 128, so dim <= 128).  The d x d Gaussian matrix S enters as fp16 hi + lo
+// halves (S = hi + lo to 22 bits, zero-padded to PD x PD); every product
+// S r runs as v_mfma_f32_16x16x32_f16 with fp32 accumulation:
+//   quantize:   sign(S r) = sign(hi rh + hi rl + lo rh), r = rh + rl the unit
+//               residual split the same way (the dropped lo rl term and the
+//               splits' rounding are ~2^-22 of |S_j| |r|, so a sign differs
+//               from an fp32 GEMM's only where that GEMM's own rounding could
+//               flip it);
+//   dequantize: z S = z hi + z lo (z = +-1 exact in fp16).
+// Persistent workgroups: each wave loads its 16-row blocks of S (or S^T) into
+// registers once and then serves batches of 32 vectors.  C^T = S R^T per
+// batch: A = S rows (lane: row l % 16, dims 8 (l / 16) ..), B = the batch's
+// vectors from LDS (lane: vector l % 16, the same dims), D = lane: vector
+// l % 16, outputs 4 (l / 16) + e.
+// --------------------------------------------------------------------------
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct QjlParams {
+  const _Float16* s_hi;  // [PD][PD] row-major: quantize S, dequantize S^T
+  const _Float16* s_lo;
+  int8_t* z;             // quantize out: +-1 [n][dim]
+  const int8_t* zin;     // dequantize in: +-1 [n][dim]
+  int64_t nbatch;        // ceil(n / 32)
+};
+
+template <int PD>
+struct QjlGeom {
+  static constexpr int NRB = PD / 64;  // 16-row blocks of S per wave (4 waves)
+  static constexpr int NKS = PD / 32;  // k-steps of 32 dims
+  static constexpr int RS = PD + 8;    // LDS row stride in halves (16-byte pad)
+};
+
+template <int PD>
+__device__ __forceinline__ void load_s_frags(const QjlParams& q, int w, int lane,
+                                             half8_t (&ah)[QjlGeom<PD>::NRB][QjlGeom<PD>::NKS],
+                                             half8_t (&al)[QjlGeom<PD>::NRB][QjlGeom<PD>::NKS]) {
+  using QG = QjlGeom<PD>;
+#pragma unroll
+  for (int rb = 0; rb < QG::NRB; rb++)
+#pragma unroll
+    for (int ks = 0; ks < QG::NKS; ks++) {
+      const int64_t off =
+          (int64_t)(16 * (QG::NRB * w + rb) + (lane & 15)) * PD + 32 * ks + 8 * (lane >> 4);
+      ah[rb][ks] = *reinterpret_cast<const half8_t*>(q.s_hi + off);
+      al[rb][ks] = *reinterpret_cast<const half8_t*>(q.s_lo + off);
+    }
+}
+
+template <int PD, int BITS>
+__global__ __launch_bounds__(kMseThreads) void prod_qjl_quantize_kernel(MseParams p, QjlParams q) {
+  using MG = MseGeom<PD>;
+  using QG = QjlGeom<PD>;
+  constexpr int P = MG::P, E = MG::E, RS = QG::RS;
+  static_assert(MG::VPB == 32 && (PD == 64 || PD == 128), "32 vectors of <= 128 dims per batch");
+  __shared__ float bnd[16];
+  __shared__ float cen[16];
+  __shared__ __attribute__((aligned(16))) _Float16 rh[32 * RS];
+  __shared__ __attribute__((aligned(16))) _Float16 rl[32 * RS];
+  if (threadIdx.x < 16) bnd[threadIdx.x] = p.table[threadIdx.x];
+  if (threadIdx.x >= 16 && threadIdx.x < 32) cen[threadIdx.x - 16] = p.cen[threadIdx.x - 16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, sub = lane % P, vl = threadIdx.x / P;
+  half8_t ah[QG::NRB][QG::NKS], al[QG::NRB][QG::NKS];
+  load_s_frags<PD>(q, w, lane, ah, al);
+  float xn[E];  // the next batch's rows, loaded while this batch computes
+  load_row<PD>(p, (int64_t)blockIdx.x * 32 + vl, sub, xn);
+  __syncthreads();
+  for (int64_t bt = blockIdx.x; bt < q.nbatch; bt += gridDim.x) {
+    float v[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) v[i] = xn[i];
+    if (bt + gridDim.x < q.nbatch) load_row<PD>(p, (bt + gridDim.x) * 32 + vl, sub, xn);
+    quantize_row<PD, BITS, true>(p, bnd, cen, bt * 32 + vl, sub, v);
+    // the unit residual as fp16 hi + lo (v - hi is exact in fp32)
+#pragma unroll
+    for (int c = 0; c < E / 8; c++) {
+      half8_t h, l;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        h[e] = (_Float16)v[8 * c + e];
+        l[e] = (_Float16)(v[8 * c + e] - (float)h[e]);
+      }
+      *reinterpret_cast<half8_t*>(rh + vl * RS + sub * E + 8 * c) = h;
+      *reinterpret_cast<half8_t*>(rl + vl * RS + sub * E + 8 * c) = l;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++) {
+      f32x4 acc[QG::NRB];
+#pragma unroll
+      for (int rb = 0; rb < QG::NRB; rb++) acc[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < QG::NKS; ks++) {
+        const int o = (16 * cb + (lane & 15)) * RS + 32 * ks + 8 * (lane >> 4);
+        const half8_t bh = *reinterpret_cast<const half8_t*>(rh + o);
+        const half8_t bl = *reinterpret_cast<const half8_t*>(rl + o);
+#pragma unroll
+        for (int rb = 0; rb < QG::NRB; rb++) {
+          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[rb][ks], bh, acc[rb], 0, 0, 0);
+          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[rb][ks], bl, acc[rb], 0, 0, 0);
+          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[rb][ks], bh, acc[rb], 0, 0, 0);
+        }
+      }
+      const int64_t vec = bt * 32 + 16 * cb + (lane & 15);
+      if (vec < p.n) {
+        int8_t* zrow = q.z + vec * p.dim;
+#pragma unroll
+        for (int rb = 0; rb < QG::NRB; rb++) {
+          const int j = 16 * (QG::NRB * w + rb) + 4 * (lane >> 4);
+          uint32_t pk = 0;
+#pragma unroll
+          for (int e = 0; e < 4; e++)  // +1 for >= 0 (sign() with 0 -> +1), else -1
+            pk |= (acc[rb][e] >= 0.0f ? 0x01u : 0xffu) << (8 * e);
+          if ((p.dim & 3) == 0) {
+            if (j < p.dim) *reinterpret_cast<uint32_t*>(zrow + j) = pk;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              if (j + e < p.dim) zrow[j + e] = (int8_t)(pk >> (8 * e));
+          }
+        }
+      }
+    }
+    __syncthreads();  // the next batch rewrites the tile
+  }
+}
+
+template <int PD, int BITS>
+__global__ __launch_bounds__(kMseThreads) void prod_qjl_dequantize_kernel(MseParams p,
+                                                                          QjlParams q) {
+  using MG = MseGeom<PD>;
+  using QG = QjlGeom<PD>;
+  constexpr int P = MG::P, TS = PD + 4;  // fp32 term tile row stride
+  static_assert(MG::VPB == 32 && (PD == 64 || PD == 128), "32 vectors of <= 128 dims per batch");
+  __shared__ float cen[16];
+  __shared__ __attribute__((aligned(16))) float term[32 * TS];
+  if (threadIdx.x < 16) cen[threadIdx.x] = p.table[threadIdx.x];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, sub = lane % P, vl = threadIdx.x / P;
+  half8_t ah[QG::NRB][QG::NKS], al[QG::NRB][QG::NKS];
+  load_s_frags<PD>(q, w, lane, ah, al);  // S^T rows
+  // the QJL signs of a batch as B fragments: lane (vector l % 16 of column
+  // block cb, dims 32 ks + 8 (l / 16) ..) holds 8 signs, 0 past dim or n
+  auto load_z = [&](int64_t bt, uint2 (&zb)[2][QG::NKS]) {
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++) {
+      const int64_t vec = bt * 32 + 16 * cb + (lane & 15);
+      const bool vlive = vec < p.n;
+#pragma unroll
+      for (int ks = 0; ks < QG::NKS; ks++) {
+        const int k0 = 32 * ks + 8 * (lane >> 4);
+        const int8_t* zp = q.zin + (vlive ? vec : 0) * p.dim + k0;
+        if (vlive && (p.dim & 7) == 0 && k0 < p.dim) {
+          zb[cb][ks] = *reinterpret_cast<const uint2*>(zp);
+        } else {
+          uint32_t lo = 0, hi = 0;
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            const uint32_t byte = (vlive && k0 + e < p.dim) ? (uint8_t)zp[e] : 0u;
+            if (e < 4) lo |= byte << (8 * e);
+            else hi |= byte << (8 * (e - 4));
+          }
+          zb[cb][ks] = uint2{lo, hi};
+        }
+      }
+    }
+  };
+  uint2 zn[2][QG::NKS];
+  load_z(blockIdx.x, zn);
+  RowCodes<PD, BITS> cn = load_codes<PD, BITS>(p, (int64_t)blockIdx.x * 32 + vl, sub);
+  __syncthreads();
+  for (int64_t bt = blockIdx.x; bt < q.nbatch; bt += gridDim.x) {
+    uint2 zc[2][QG::NKS];
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+      for (int ks = 0; ks < QG::NKS; ks++) zc[cb][ks] = zn[cb][ks];
+    const RowCodes<PD, BITS> cc = cn;
+    if (bt + gridDim.x < q.nbatch) {  // the next batch's inputs, in flight meanwhile
+      load_z(bt + gridDim.x, zn);
+      cn = load_codes<PD, BITS>(p, (bt + gridDim.x) * 32 + vl, sub);
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++) {
+      f32x4 acc[QG::NRB];
+#pragma unroll
+      for (int rb = 0; rb < QG::NRB; rb++) acc[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < QG::NKS; ks++) {
+        half8_t b;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          b[e] = (_Float16)(int8_t)((e < 4 ? zc[cb][ks].x : zc[cb][ks].y) >> (8 * (e & 3)));
+#pragma unroll
+        for (int rb = 0; rb < QG::NRB; rb++) {
+          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[rb][ks], b, acc[rb], 0, 0, 0);
+          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[rb][ks], b, acc[rb], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int rb = 0; rb < QG::NRB; rb++) {
+        const int j = 16 * (QG::NRB * w + rb) + 4 * (lane >> 4);
+        *reinterpret_cast<f32x4*>(term + (16 * cb + (lane & 15)) * TS + j) = acc[rb];
+      }
+    }
+    __syncthreads();
+    const int64_t row = bt * 32 + vl;
+    dequantize_row<PD, BITS, true>(p, cen, row, sub, term + vl * TS, cc);
+    __syncthreads();  // the next batch rewrites the tile
   }
 }
 
@@ -425,6 +694,123 @@ int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* o
   return (int)e;
 }
 
+// CUs of the current device, queried once per device (0 if unknown).
+int mse_device_cus() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cache[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0 && hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+    cache[dev].store(c, std::memory_order_relaxed);
+  return c;
+}
+
+// TurboQuantProd with the QJL projections fused (padded size 64 or 128).
+int prod_qjl_call(bool quant, const float* x, uint8_t* packed, float* norms, float* out,
+                  int64_t n, int32_t dim, int32_t padded_dim, int32_t bits, const float* signs,
+                  const float* table, const float* centroids, const _Float16* s_hi,
+                  const _Float16* s_lo, int8_t* z, const int8_t* zin, float* rnorm,
+                  const float* gamma, tq_stream_t stream) {
+  const char* what = quant ? "prod_quantize_qjl" : "prod_dequantize_qjl";
+  if (padded_dim != 64 && padded_dim != 128) {
+    set_error("%s: padded_dim %d unsupported (64 or 128; larger sizes take the BLAS path)", what,
+              padded_dim);
+    return kEinval;
+  }
+  if (bits < 1 || bits > 4) {
+    set_error("%s: bit_width %d unsupported (1..4)", what, bits);
+    return kEinval;
+  }
+  if (dim < 1 || dim > padded_dim || 2 * dim <= padded_dim) {
+    set_error("%s: padded_dim %d must be the power of two next to dim %d", what, padded_dim, dim);
+    return kEinval;
+  }
+  if (n < 0 || n > ((int64_t)1 << 40)) {
+    set_error("%s: vector count %lld out of range", what, (long long)n);
+    return kEinval;
+  }
+  if (!packed || !norms || !signs || !table || !s_hi || !s_lo ||
+      (quant ? (!x || !centroids || !z || !rnorm) : (!out || !zin || !gamma))) {
+    set_error("%s: null pointer", what);
+    return kEinval;
+  }
+  if (n == 0) return 0;
+  const uintptr_t al = (uintptr_t)(quant ? (const void*)x : (const void*)out) |
+                       (uintptr_t)packed | (uintptr_t)s_hi | (uintptr_t)s_lo;
+  if ((al & 15) != 0) {
+    set_error("%s: x / out, packed and the S halves must be 16-byte aligned", what);
+    return kEinval;
+  }
+  const int per = bits == 3 ? 2 : 8 / bits;
+  MseParams p;
+  p.x = x;
+  p.packed = packed;
+  p.norms = norms;
+  p.out = out;
+  p.signs = signs;
+  p.resid = nullptr;
+  p.rnorm = rnorm;
+  p.add = nullptr;
+  p.gamma = gamma;
+  p.add_scale = (float)(std::sqrt(M_PI / 2.0) / dim);
+  p.n = n;
+  p.dim = dim;
+  p.nbytes = padded_dim / per;
+  p.inv_sqrt_pd = (float)(1.0 / std::sqrt((double)padded_dim));
+  p.levels = 1 << bits;
+  for (int i = 0; i < 16; i++) {
+    p.table[i] = i < (quant ? p.levels - 1 : p.levels) ? table[i] : 0.0f;
+    p.cen[i] = (centroids && i < p.levels) ? centroids[i] : 0.0f;
+  }
+  QjlParams q;
+  q.s_hi = s_hi;
+  q.s_lo = s_lo;
+  q.z = z;
+  q.zin = zin;
+  q.nbatch = (n + 31) / 32;
+  // persistent: the resident workgroups of the whole chip, each loading its
+  // S blocks once (occupancy queried per kernel, once)
+  const int cus = mse_device_cus();
+  const dim3 block(kMseThreads);
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  auto grid_for = [&](const void* fn, std::atomic<int>& per_cu) {
+    int b = per_cu.load(std::memory_order_relaxed);
+    if (b == 0) {
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fn, kMseThreads, 0) != hipSuccess ||
+          b < 1)
+        b = 1;
+      per_cu.store(b, std::memory_order_relaxed);
+    }
+    const int64_t cap = (int64_t)(cus > 0 ? cus : 256) * b;
+    return dim3((unsigned)(q.nbatch < cap ? q.nbatch : cap));
+  };
+#define TQ_QJL_CASE(PD, B)                                                                      \
+  if (padded_dim == PD && bits == B) {                                                         \
+    static std::atomic<int> occ_q{0}, occ_d{0};                                                \
+    if (quant)                                                                                 \
+      hipLaunchKernelGGL((prod_qjl_quantize_kernel<PD, B>),                                    \
+                         grid_for((const void*)prod_qjl_quantize_kernel<PD, B>, occ_q), block, \
+                         0, st, p, q);                                                         \
+    else                                                                                       \
+      hipLaunchKernelGGL((prod_qjl_dequantize_kernel<PD, B>),                                  \
+                         grid_for((const void*)prod_qjl_dequantize_kernel<PD, B>, occ_d),      \
+                         block, 0, st, p, q);                                                  \
+  }
+  TQ_QJL_CASE(64, 1)
+  TQ_QJL_CASE(64, 2)
+  TQ_QJL_CASE(64, 3)
+  TQ_QJL_CASE(64, 4)
+  TQ_QJL_CASE(128, 1)
+  TQ_QJL_CASE(128, 2)
+  TQ_QJL_CASE(128, 3)
+  TQ_QJL_CASE(128, 4)
+#undef TQ_QJL_CASE
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+  return (int)e;
+}
+
 }  // namespace
 }  // namespace tq
 
@@ -478,4 +864,29 @@ extern "C" int tq_prod_dequantize(const uint8_t* packed, const float* norms,
   return tq::mse_call(false, nullptr, const_cast<uint8_t*>(packed), const_cast<float*>(norms),
                       out, num_vectors, dim, padded_dim, mse_bit_width, signs, centroids, stream,
                       "prod_dequantize", pa);
+}
+
+extern "C" int tq_prod_quantize_qjl(const float* x, int64_t num_vectors, int32_t dim,
+                                    int32_t padded_dim, int32_t mse_bit_width, const float* signs,
+                                    const float* boundaries, const float* centroids,
+                                    const void* s_hi, const void* s_lo, uint8_t* packed,
+                                    float* norms, int8_t* qjl_signs, float* residual_norms,
+                                    tq_stream_t stream) {
+  return tq::prod_qjl_call(true, x, packed, norms, nullptr, num_vectors, dim, padded_dim,
+                           mse_bit_width, signs, boundaries, centroids,
+                           static_cast<const _Float16*>(s_hi), static_cast<const _Float16*>(s_lo),
+                           qjl_signs, nullptr, residual_norms, nullptr, stream);
+}
+
+extern "C" int tq_prod_dequantize_qjl(const uint8_t* packed, const float* norms,
+                                      const int8_t* qjl_signs, const float* residual_norms,
+                                      int64_t num_vectors, int32_t dim, int32_t padded_dim,
+                                      int32_t mse_bit_width, const float* signs,
+                                      const float* centroids, const void* st_hi,
+                                      const void* st_lo, float* out, tq_stream_t stream) {
+  return tq::prod_qjl_call(false, nullptr, const_cast<uint8_t*>(packed),
+                           const_cast<float*>(norms), out, num_vectors, dim, padded_dim,
+                           mse_bit_width, signs, centroids, nullptr,
+                           static_cast<const _Float16*>(st_hi), static_cast<const _Float16*>(st_lo),
+                           nullptr, qjl_signs, nullptr, residual_norms, stream);
 }

@@ -418,6 +418,83 @@ def prod_dequantize(packed: torch.Tensor, norms: torch.Tensor, qjl_term: torch.T
     return out
 
 
+def prod_quantize_qjl(x: torch.Tensor, padded_dim: int, mse_bit_width: int,
+                      signs: torch.Tensor, boundaries, centroids, s_hi: torch.Tensor,
+                      s_lo: torch.Tensor):
+    """TurboQuantProd.quantize with the QJL product fused (tq_prod_quantize_qjl,
+    padded_dim 64 or 128): x fp32 [..., dim] -> (packed, norms, qjl_signs int8
+    [..., dim], residual_norms).  s_hi / s_lo: fp16 [padded_dim, padded_dim]
+    halves of the QJL matrix."""
+    _require_gpu(x, signs, s_hi, s_lo)
+    if x.dtype != torch.float32:
+        raise RuntimeError("prod_quantize_qjl: x must be fp32")
+    for t in (s_hi, s_lo):
+        if t.dtype != torch.float16 or tuple(t.shape) != (padded_dim, padded_dim) \
+                or not t.is_contiguous() or t.data_ptr() % 16:
+            raise RuntimeError("prod_quantize_qjl: S halves must be contiguous aligned fp16 "
+                               "[padded_dim, padded_dim]")
+    x = x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    dim = x.shape[-1]
+    lead = x.shape[:-1]
+    n = x.numel() // dim if dim else 0
+    per = 2 if mse_bit_width == 3 else 8 // mse_bit_width
+    packed = torch.empty((*lead, padded_dim // per), dtype=torch.uint8, device=x.device)
+    norms = torch.empty(lead, dtype=torch.float32, device=x.device)
+    z = torch.empty((*lead, dim), dtype=torch.int8, device=x.device)
+    rnorm = torch.empty(lead, dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        rc = lib.tq_prod_quantize_qjl(x.data_ptr(), n, dim, int(padded_dim), int(mse_bit_width),
+                                      signs.data_ptr(), _host_f32(boundaries),
+                                      _host_f32(centroids), s_hi.data_ptr(), s_lo.data_ptr(),
+                                      packed.data_ptr(), norms.data_ptr(), z.data_ptr(),
+                                      rnorm.data_ptr(), _stream_ptr(x.device))
+    _lib.check(rc, "prod_quantize_qjl")
+    return packed, norms, z, rnorm
+
+
+def prod_dequantize_qjl(packed: torch.Tensor, norms: torch.Tensor, qjl_signs: torch.Tensor,
+                        residual_norms: torch.Tensor, dim: int, padded_dim: int,
+                        mse_bit_width: int, signs: torch.Tensor, centroids,
+                        st_hi: torch.Tensor, st_lo: torch.Tensor) -> torch.Tensor:
+    """TurboQuantProd.dequantize with z S formed in-kernel
+    (tq_prod_dequantize_qjl, padded_dim 64 or 128).  st_hi / st_lo: fp16
+    halves of S^T."""
+    _require_gpu(packed, norms, qjl_signs, residual_norms, signs, st_hi, st_lo)
+    per = 2 if mse_bit_width == 3 else 8 // mse_bit_width
+    if packed.dtype != torch.uint8 or packed.shape[-1] != padded_dim // per:
+        raise RuntimeError("prod_dequantize_qjl: packed must be uint8 [..., padded_dim / per]")
+    lead = tuple(packed.shape[:-1])
+    if tuple(norms.shape) != lead or tuple(residual_norms.shape) != lead:
+        raise RuntimeError("prod_dequantize_qjl: norms must match packed's leading dims")
+    if qjl_signs.dtype != torch.int8 or tuple(qjl_signs.shape) != (*lead, dim):
+        raise RuntimeError("prod_dequantize_qjl: qjl_signs must be int8 [..., dim]")
+    for t in (st_hi, st_lo):
+        if t.dtype != torch.float16 or tuple(t.shape) != (padded_dim, padded_dim) \
+                or not t.is_contiguous() or t.data_ptr() % 16:
+            raise RuntimeError("prod_dequantize_qjl: S^T halves must be contiguous aligned "
+                               "fp16 [padded_dim, padded_dim]")
+    packed = packed.contiguous()
+    if packed.data_ptr() % 16:
+        packed = packed.clone()
+    nf = norms.to(torch.float32).contiguous()
+    rn = residual_norms.to(torch.float32).contiguous()
+    z = qjl_signs.contiguous()
+    out = torch.empty((*lead, dim), dtype=torch.float32, device=packed.device)
+    lib = _lib.load()
+    with torch.cuda.device(packed.device):
+        rc = lib.tq_prod_dequantize_qjl(packed.data_ptr(), nf.data_ptr(), z.data_ptr(),
+                                        rn.data_ptr(), nf.numel(), int(dim), int(padded_dim),
+                                        int(mse_bit_width), signs.data_ptr(),
+                                        _host_f32(centroids), st_hi.data_ptr(),
+                                        st_lo.data_ptr(), out.data_ptr(),
+                                        _stream_ptr(packed.device))
+    _lib.check(rc, "prod_dequantize_qjl")
+    return out
+
+
 # --------------------------------------------------------------------------
 # torch.library registration under the reference's namespaces and schemas
 # --------------------------------------------------------------------------
