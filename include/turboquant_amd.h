@@ -344,6 +344,32 @@ int tq_prod_dequantize_qjl(const uint8_t* packed, const float* norms, const int8
                            float* out, tq_stream_t stream);
 
 /*
+ * Layer glue of the end-to-end harness, no counterpart in the
+ * reference: in a vLLM deployment vLLM's own fused layer kernels do this.
+ * fp16 tensors, rows contiguous, fp32 arithmetic inside.
+ *
+ * tq_e2e_add_rms_norm: x[r] += y[r] (fp16 add; skipped when y is NULL), then
+ *   h[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w (skipped when h is NULL);
+ *   hidden a multiple of 8 up to 8192, 16-byte aligned rows.
+ * tq_e2e_qk_norm_rope: for the q and k heads of each fused QKV row (q heads,
+ *   then kv heads, then the v part, row stride qkv_row_stride elements):
+ *   RMSNorm over the head's dims with q_w or k_w, rounded to fp16, then
+ *   rotate-half RoPE with row positions[t] of the fp16 cos / signed-sin
+ *   tables [*, head_dim]: out[i] = n[i] cos[i] + n[(i + D/2) mod D] sin[i].
+ *   q_out [tokens, q_heads, D], k_out [tokens, kv_heads, D].  D even, <= 256.
+ * tq_e2e_silu_mul: out[t, i] = silu(gate_up[t, i]) * gate_up[t, inter + i].
+ */
+int tq_e2e_add_rms_norm(void* x, const void* y, const void* w, void* h, int64_t rows,
+                        int32_t hidden, float eps, tq_stream_t stream);
+int tq_e2e_qk_norm_rope(const void* qkv, int64_t qkv_row_stride, const void* q_w,
+                        const void* k_w, const void* cos_table, const void* sin_table,
+                        const int64_t* positions, int64_t tokens, int32_t q_heads,
+                        int32_t kv_heads, int32_t head_dim, float eps, void* q_out,
+                        void* k_out, tq_stream_t stream);
+int tq_e2e_silu_mul(const void* gate_up, void* out, int64_t rows, int32_t inter,
+                    tq_stream_t stream);
+
+/*
  * Diagnostic, no counterpart in the reference: tq_decode_partials at head
  * size 128 with 8 kv heads per workgroup (the configs[2] geometry) with parts
  * compiled out.  mode 1: the attention math (the same page walk, LDS copy

@@ -401,3 +401,30 @@ def test_ops_refuse_tensors_on_two_devices():
     ops._require_gpu(FakeCuda(0), FakeCuda(0))
     with pytest.raises(RuntimeError, match="one GPU"):
         ops._require_gpu(FakeCuda(0), FakeCuda(1))
+
+
+def test_e2e_glue_entry_points_refuse_bad_arguments():
+    """tq_e2e_* argument checks (no GPU call)."""
+    from turboquant_amd import _lib
+    lib = _lib.load()
+    one = ctypes.c_void_p(16)
+    assert lib.tq_e2e_add_rms_norm(one, one, one, one, 4, 4100, 1e-6, None) == -22
+    assert b"hidden" in lib.tq_last_error()
+    assert lib.tq_e2e_add_rms_norm(one, one, one, one, 4, 16384, 1e-6, None) == -22
+    assert lib.tq_e2e_add_rms_norm(one, None, one, None, 4, 4096, 1e-6, None) == -22
+    assert lib.tq_e2e_add_rms_norm(one, one, None, one, 4, 4096, 1e-6, None) == -22
+    assert b"null pointer" in lib.tq_last_error()
+    assert lib.tq_e2e_add_rms_norm(ctypes.c_void_p(18), one, None, None, 4, 4096, 1e-6,
+                                   None) == -22
+    assert b"aligned" in lib.tq_last_error()
+    assert lib.tq_e2e_add_rms_norm(None, None, None, None, 0, 4096, 1e-6, None) == 0
+    assert lib.tq_e2e_qk_norm_rope(one, 6144, one, one, one, one, one, 4, 32, 8, 97, 1e-6,
+                                   one, one, None) == -22
+    assert b"head_dim" in lib.tq_last_error()
+    assert lib.tq_e2e_qk_norm_rope(one, 1000, one, one, one, one, one, 4, 32, 8, 128, 1e-6,
+                                   one, one, None) == -22
+    assert lib.tq_e2e_qk_norm_rope(one, 6144, one, one, None, one, one, 4, 32, 8, 128, 1e-6,
+                                   one, one, None) == -22
+    assert lib.tq_e2e_silu_mul(one, one, 4, 12, None) == -22
+    assert lib.tq_e2e_silu_mul(one, None, 4, 16, None) == -22
+    assert lib.tq_e2e_silu_mul(None, None, 0, 16, None) == 0

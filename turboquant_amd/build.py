@@ -15,7 +15,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libtq_hip.so")
-SOURCES = ["tq_write.hip", "tq_decode.hip", "tq_dequant.hip", "tq_prefill.hip", "tq_mse.hip"]
+SOURCES = ["tq_write.hip", "tq_decode.hip", "tq_dequant.hip", "tq_prefill.hip", "tq_mse.hip",
+           "tq_e2e.hip"]
 ARCH = os.environ.get("TQ_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

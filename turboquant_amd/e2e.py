@@ -103,8 +103,57 @@ def build_weights(shape: ModelShape, seed: int, device) -> dict:
 
 
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    """RMSNorm over the last dim (fp32 accumulation inside the fused kernel)."""
+    """RMSNorm over the last dim in torch (the definition the fused glue
+    kernels below are tested against)."""
     return F.rms_norm(x, (x.shape[-1],), w, eps)
+
+
+# ---------------------------------------------------------------- layer glue
+# The model's elementwise work between the GEMMs runs as three fused HIP
+# kernels (tq_e2e.hip): residual add + RMSNorm, per-head q/k RMSNorm + RoPE
+# straight from the QKV GEMM's output, and SiLU(g) * u.
+
+def add_rms_norm(x: torch.Tensor, y: torch.Tensor | None, w: torch.Tensor | None,
+                 h: torch.Tensor | None, eps: float) -> None:
+    """x += y (when y is given), then h = RMSNorm(x) * w (when h is given);
+    x, y, h fp16 [T, H] contiguous, updated in place."""
+    from . import _lib
+    assert x.is_contiguous() and x.dtype == torch.float16
+    rc = _lib.load().tq_e2e_add_rms_norm(
+        x.data_ptr(), y.data_ptr() if y is not None else None,
+        w.data_ptr() if w is not None else None, h.data_ptr() if h is not None else None,
+        x.shape[0], x.shape[1], float(eps), ops._stream_ptr(x.device))
+    _lib.check(rc, "e2e_add_rms_norm")
+
+
+def qk_norm_rope(qkv: torch.Tensor, shape: "ModelShape", q_w: torch.Tensor, k_w: torch.Tensor,
+                 cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor):
+    """q [T, Hq, D] and k [T, Hkv, D] of a fused QKV GEMM output [T, *]:
+    per-head RMSNorm, then rotate-half RoPE at positions pos (int64 [T])."""
+    from . import _lib
+    s = shape
+    t = qkv.shape[0]
+    q = torch.empty((t, s.heads, s.head_dim), dtype=torch.float16, device=qkv.device)
+    k = torch.empty((t, s.kv_heads, s.head_dim), dtype=torch.float16, device=qkv.device)
+    assert qkv.stride(1) == 1 and pos.dtype == torch.int64 and pos.is_contiguous()
+    rc = _lib.load().tq_e2e_qk_norm_rope(
+        qkv.data_ptr(), qkv.stride(0), q_w.data_ptr(), k_w.data_ptr(), cos.data_ptr(),
+        sin.data_ptr(), pos.data_ptr(), t, s.heads, s.kv_heads, s.head_dim, float(s.eps),
+        q.data_ptr(), k.data_ptr(), ops._stream_ptr(qkv.device))
+    _lib.check(rc, "e2e_qk_norm_rope")
+    return q, k
+
+
+def silu_mul(gu: torch.Tensor) -> torch.Tensor:
+    """SiLU(gu[:, :I]) * gu[:, I:] of the gate/up GEMM output [T, 2I]."""
+    from . import _lib
+    assert gu.is_contiguous()
+    t, i2 = gu.shape
+    out = torch.empty((t, i2 // 2), dtype=gu.dtype, device=gu.device)
+    rc = _lib.load().tq_e2e_silu_mul(gu.data_ptr(), out.data_ptr(), t, i2 // 2,
+                                     ops._stream_ptr(gu.device))
+    _lib.check(rc, "e2e_silu_mul")
+    return out
 
 
 def rope_tables(n: int, d: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -182,31 +231,37 @@ class Runner:
         self.probe = None
 
     # ------------------------------------------------------------ layers
-    def _attn_qkv(self, lw, x, cs):
-        """q, k, v of the tokens x; cs = (cos, sin) rows of their positions."""
+    def _qkv(self, lw, h, pos):
+        """q, k (normed, rotated), v of the normed tokens h at positions pos."""
         s = self.shape
-        t = x.shape[0]
-        h = rms_norm(x, lw["ln1"], s.eps)
+        t = h.shape[0]
         qkv = F.linear(h, lw["qkv"])
-        q, k, v = qkv.split([s.heads * s.head_dim, s.kv_heads * s.head_dim,
-                             s.kv_heads * s.head_dim], dim=-1)
-        q = rms_norm(q.reshape(t, s.heads, s.head_dim), lw["q_norm"], s.eps)
-        k = rms_norm(k.reshape(t, s.kv_heads, s.head_dim), lw["k_norm"], s.eps)
-        q = rope(q, *cs)
-        k = rope(k, *cs)
-        return q, k, v.reshape(t, s.kv_heads, s.head_dim)
+        q, k = qk_norm_rope(qkv, s, lw["q_norm"], lw["k_norm"], self.cos, self.sin, pos)
+        v = qkv[:, (s.heads + s.kv_heads) * s.head_dim:].view(t, s.kv_heads, s.head_dim)
+        return q, k, v
 
-    def _rope_rows(self, pos):
-        return self.cos.index_select(0, pos), self.sin.index_select(0, pos)
+    def _layers(self, x, pos, attend):
+        """Every layer over the residual stream x [T, hidden] (fp16,
+        contiguous, updated in place): x += o_proj(attend(li, lw, q, k, v));
+        x += MLP(x).  attend returns the attention output [T, Hq * D]."""
+        s = self.shape
+        layers = self.weights["layers"]
+        h = torch.empty_like(x)
+        add_rms_norm(x, None, layers[0]["ln1"], h, s.eps)
+        for li, lw in enumerate(layers):
+            q, k, v = self._qkv(lw, h, pos)
+            o = attend(li, lw, q, k, v)
+            add_rms_norm(x, F.linear(o, lw["o"]), lw["ln2"], h, s.eps)
+            y = F.linear(silu_mul(F.linear(h, lw["gate_up"])), lw["down"])
+            if li + 1 < len(layers):
+                add_rms_norm(x, y, layers[li + 1]["ln1"], h, s.eps)
+            else:
+                add_rms_norm(x, y, None, None, s.eps)
+        return x
 
-    def _mlp(self, lw, x):
-        h = rms_norm(x, lw["ln2"], self.shape.eps)
-        gu = F.linear(h, lw["gate_up"])
-        g, u = gu.chunk(2, dim=-1)
-        return x + F.linear(F.silu(g) * u, lw["down"])
-
-    def _logits(self, x_last):
-        h = rms_norm(x_last, self.weights["norm"], self.shape.eps)
+    def _logits(self, x_rows):
+        h = torch.empty_like(x_rows)
+        add_rms_norm(x_rows, None, self.weights["norm"], h, self.shape.eps)
         return F.linear(h, self.weights["lm_head"])
 
     # ------------------------------------------------------------ prefill
@@ -223,18 +278,16 @@ class Runner:
         meta = Meta(L, L, pages[None, :], torch.tensor([L], dtype=torch.int32, device=dev),
                     torch.tensor([0, L], dtype=torch.int32, device=dev), slots)
         x = F.embedding(tokens, self.weights["embed"])
-        cs = self._rope_rows(pos)
-        for li, lw in enumerate(self.weights["layers"]):
-            q, k, v = self._attn_qkv(lw, x, cs)
+
+        def attend(li, lw, q, k, v):
             impl = self.impls[li]
             impl.do_kv_cache_update(None, k, v, self.caches[li], slots)
             if self.kv16 is not None:
                 self.kv16[li][0, b, :, :L] = k.transpose(0, 1)
                 self.kv16[li][1, b, :, :L] = v.transpose(0, 1)
-            o = impl.forward(None, q.reshape(L, -1), k.reshape(L, -1), v.reshape(L, -1),
-                             self.caches[li], meta)
-            x = x + F.linear(o, lw["o"])
-            x = self._mlp(lw, x)
+            return impl.forward(None, q.reshape(L, -1), k.reshape(L, -1), v.reshape(L, -1),
+                                self.caches[li], meta)
+        x = self._layers(x, pos, attend)
         first = greedy(self._logits(x[-1:]))
         self.pos[b] = L
         self.tok[b] = first[0]
@@ -253,18 +306,16 @@ class Runner:
         self.seq_lens.copy_((pos + 1).to(torch.int32))
         meta = Meta(1, self.batch, bt, self.seq_lens, self.qsl, self.slots)
         x = F.embedding(self.tok, self.weights["embed"])
-        cs = self._rope_rows(pos)
-        for li, lw in enumerate(self.weights["layers"]):
-            q, k, v = self._attn_qkv(lw, x, cs)
+
+        def attend(li, lw, q, k, v):
             impl = self.impls[li]
             impl.do_kv_cache_update(None, k, v, self.caches[li], self.slots)
-            q2 = q.reshape(self.batch, -1)
-            o = impl.forward(None, q2, k.reshape(self.batch, -1), v.reshape(self.batch, -1),
-                             self.caches[li], meta)
+            o = impl.forward(None, q.reshape(self.batch, -1), k.reshape(self.batch, -1),
+                             v.reshape(self.batch, -1), self.caches[li], meta)
             if self.probe is not None:
                 self.probe.append((li, q.clone(), k.clone(), v.clone(), o.clone()))
-            x = x + F.linear(o, lw["o"])
-            x = self._mlp(lw, x)
+            return o
+        x = self._layers(x, pos, attend)
         nxt = greedy(self._logits(x))
         self.tok.copy_(nxt)
         self.out_buf.index_copy_(0, self.step_idx, nxt[None, :])
@@ -375,12 +426,11 @@ class Runner:
         for step in range(steps):
             p = p0 + step
             x = F.embedding(tok, self.weights["embed"])
-            cs = self._rope_rows(pos)
             if kv == "dequant":
                 page = bt.gather(1, (pos // BLOCK)[:, None]).squeeze(1).to(torch.int64)
                 slots = (page * BLOCK + pos % BLOCK).to(torch.int32)
-            for li, lw in enumerate(self.weights["layers"]):
-                q, k, v = self._attn_qkv(lw, x, cs)
+
+            def attend(li, lw, q, k, v):
                 if kv == "fp16":
                     kvl = self.kv16[li]
                     kvl[0, :, :, p] = k
@@ -396,8 +446,8 @@ class Runner:
                     vv = kd[1, :, :p + 1].transpose(1, 2)
                 o = F.scaled_dot_product_attention(q[:, :, None, :], kk, vv, scale=scale,
                                                    enable_gqa=True)
-                x = x + F.linear(o.reshape(self.batch, -1), lw["o"])
-                x = self._mlp(lw, x)
+                return o.reshape(self.batch, -1)
+            x = self._layers(x, pos, attend)
             logits = self._logits(x)
             top = greedy(logits)
             out[step] = top
