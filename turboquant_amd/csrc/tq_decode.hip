@@ -1085,7 +1085,12 @@ void decode_partials_kernel(DecodeParams p) {
   // the 8 consecutive elements e = 512 j + 8 l .. + 7 (head e / PD, dim
   // e % PD).  Elements past the wave's heads read as zeros (empty range).
   // Larger head groups (ratio * PD > 512 * NQL) form q' through LDS below.
-  constexpr int NQL = 2;
+  // Four loads at head size 256 with at most two kv heads per workgroup
+  // (ratio 8 there: 2048 elements), whose 8 KB hi / lo scratch per wave still
+  // fits the table region; two elsewhere.  QLO: byte offset of the lo parts
+  // in a wave's scratch (the hi parts come first).
+  constexpr int NQL = PD == 256 && G <= 2 ? 4 : 2;
+  constexpr int QLO = NQL * 1024;
   const bool qreg = ratio * PD <= 512 * NQL;  // uniform
   float qx[NQL][8];
   // sign bits of dims (8 lane) % PD .. + 7 (bit k: dim + k), for the inverse
@@ -1297,11 +1302,11 @@ void decode_partials_kernel(DecodeParams p) {
       // in registers: butterflies h = 1, 2, 4 inside a lane, h >= 8 between
       // lanes l and l ^ (h / 8) (DPP, one fma with a lane sign each)
       // the second 512 elements only exist when ratio * PD > 512
-      const bool q2 = ratio * PD > 512;  // uniform
+      const int nql = (ratio * PD + 511) / 512;  // loads holding real elements (uniform)
       if (p.signs) {
 #pragma unroll
         for (int j = 0; j < NQL; j++) {
-          if (j > 0 && !q2) break;
+          if (j >= nql) break;
 #pragma unroll
           for (int h = 1; h < 8; h <<= 1)
 #pragma unroll
@@ -1324,10 +1329,10 @@ void decode_partials_kernel(DecodeParams p) {
       // q4 * PD/4 + 8c + 0..7.  Inline assembly: the scratch shares the ring
       // with the copy in flight, and the compiler would otherwise wait for it.
 #if defined(__HIP_DEVICE_COMPILE__)
-      const uint32_t qsb = lds_addr(sm.klut) + (uint32_t)w * 4096u;
+      const uint32_t qsb = lds_addr(sm.klut) + (uint32_t)w * (2u * QLO);
 #pragma unroll
       for (int j = 0; j < NQL; j++) {
-        if (j > 0 && !q2) break;  // those scratch elements are never read
+        if (j >= nql) break;  // those scratch elements are never read
         u32x4 vh, vl;
 #pragma unroll
         for (int wd = 0; wd < 4; wd++) {
@@ -1340,9 +1345,9 @@ void decode_partials_kernel(DecodeParams p) {
                    ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
         }
         const uint32_t a = qsb + (uint32_t)(512 * j + 8 * lane) * 2u;
-        asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:2048"
+        asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:%3"
                      :
-                     : "v"(a), "v"(vh), "v"(vl)
+                     : "v"(a), "v"(vh), "v"(vl), "i"(QLO)
                      : "memory");
       }
 #pragma unroll
@@ -1353,15 +1358,15 @@ void decode_partials_kernel(DecodeParams p) {
           // (columns of heads >= ratio read elements never written: zeroed)
           asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
                        : "=v"(vh)
-                       : "v"(qsb + e * 2u + (n < 8 ? 0u : 2048u))
+                       : "v"(qsb + e * 2u + (n < 8 ? 0u : (uint32_t)QLO))
                        : "memory");
           if (hq >= ratio) vh = u32x4{0u, 0u, 0u, 0u};
           qb[c] = __builtin_bit_cast(half8_t, vh);
         } else {
-          asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:2048\n\t"
+          asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:%3\n\t"
                        "s_waitcnt lgkmcnt(0)"
                        : "=&v"(vh), "=&v"(vl)
-                       : "v"(qsb + e * 2u)
+                       : "v"(qsb + e * 2u), "i"(QLO)
                        : "memory");
           if (hq >= ratio) vh = vl = u32x4{0u, 0u, 0u, 0u};
           qb[c] = __builtin_bit_cast(half8_t, vh);
@@ -1548,7 +1553,8 @@ void decode_partials_kernel(DecodeParams p) {
   // The staging holds G * ratio * PD floats: within the table region when
   // ratio * PD <= 1024 (the assert), and within table + ring otherwise (the
   // launcher picks G so that the q scratch of that size fits, the same bound).
-  static_assert(G * 4096 <= RG::LUTB, "the q' scratch of the waves exceeds the table region");
+  static_assert(G * 2 * (PD == 256 && G <= 2 ? 4 : 2) * 1024 <= RG::LUTB,
+                "the q' scratch of the waves exceeds the table region");
   __builtin_amdgcn_s_barrier();
   float* const stage = reinterpret_cast<float*>(&sm) + (size_t)w * ratio * PD;
   const int64_t orow0 = row * p.Hq + kvh * ratio;  // first row of this wave
