@@ -370,6 +370,15 @@ int tq_e2e_silu_mul(const void* gate_up, void* out, int64_t rows, int32_t inter,
                     tq_stream_t stream);
 
 /*
+ * Diagnostic, no counterpart in the reference: with force_search != 0 the
+ * quantize kernels (tq_mse_quantize, tq_prod_quantize*) take their codes by a
+ * binary search over the boundaries instead of the one-lookup bin table they
+ * use for symmetric codebooks, so that tests can check the two give the
+ * same codes on the same inputs.  Process-wide; returns 0.
+ */
+int tq_diag_mse_bucketize(int32_t force_search);
+
+/*
  * Diagnostic, no counterpart in the reference: tq_decode_partials at head
  * size 128 with 8 kv heads per workgroup (the configs[2] geometry) with parts
  * compiled out.  mode 1: the attention math (the same page walk, LDS copy

@@ -208,3 +208,61 @@ def test_prod_hip_unbiased_inner_products():
     # |mean| within 4 standard errors; the variance bound is pi / (2 d) per pair
     se = math.sqrt(math.pi / (2 * d) / x.shape[0])
     assert abs(err.mean().item()) < 4 * se + 1e-3
+
+
+@pytest.mark.parametrize("pd,bits", [(64, 1), (64, 4), (128, 2), (128, 3), (128, 4), (256, 4),
+                                     (1024, 3)])
+def test_bin_table_codes_equal_the_search(pd, bits):
+    """The quantize kernels' one-lookup bucketize (bin table of the symmetric
+    codebook) against their binary search on the same inputs: identical
+    codes, norms and residuals.  The inputs put many rotated coordinates
+    within a few ulps of a boundary, exactly on 0, and at +-inf / NaN rows."""
+    print(f"case: algorithm bin-table bucketize pd={pd} bits={bits}", flush=True)
+    from turboquant_amd import _lib, ops
+    lib = _lib.load()
+    q = A.TurboQuantMSE(pd, bits, device="cuda:0")
+    s = q.rotation.signs.double().cpu()
+    b = q.codebook.boundaries.double().cpu()
+    g = torch.Generator().manual_seed(pd + bits)
+    n = 3000
+    # rotated targets near the boundaries (and exact zeros), mapped back to
+    # x = s * FWHT(y) / sqrt(pd) in float64, so the kernel's y lands within
+    # rounding of them
+    pick = torch.randint(0, len(b), (n, pd), generator=g)
+    y = b[pick] * (1 + 1e-7 * torch.randn(n, pd, generator=g, dtype=torch.float64))
+    y[torch.rand(n, pd, generator=g) < 0.05] = 0.0
+    h = y.clone()
+    step = 1
+    while step < pd:  # unnormalised FWHT
+        h = h.view(n, -1, 2, step)
+        h = torch.stack((h[:, :, 0] + h[:, :, 1], h[:, :, 0] - h[:, :, 1]), dim=2)
+        step *= 2
+    x = (h.reshape(n, pd) * s / math.sqrt(pd)).float()
+    x[0] = 0.0
+    x[1, 3] = float("inf")
+    x[2, 5] = float("nan")
+    xg = x.cuda()
+    bnd, cen = q._host_tables()
+    try:
+        pb, nb = ops.mse_quantize(xg, pd, bits, q.rotation.signs, bnd)
+        lib.tq_diag_mse_bucketize(1)
+        ps, ns = ops.mse_quantize(xg, pd, bits, q.rotation.signs, bnd)
+    finally:
+        lib.tq_diag_mse_bucketize(0)
+    assert torch.equal(nb.isnan(), ns.isnan())
+    assert torch.equal(nb[~nb.isnan()], ns[~ns.isnan()])
+    diff = (A.unpack_bits(pb.cpu(), bits, pd) != A.unpack_bits(ps.cpu(), bits, pd)).sum().item()
+    print(f"  codes differing: {diff}", flush=True)
+    assert torch.equal(pb, ps)
+    if bits >= 2 and pd <= 128:  # the fused Prod kernel's MSE stage the same way
+        pq = A.TurboQuantProd(pd, bits + 1, device="cuda:0")
+        bq, cq = pq.mse._host_tables()
+        sh, sl, _, _ = pq.qjl.halves(pd)
+        try:
+            r1 = ops.prod_quantize_qjl(xg, pd, bits, pq.mse.rotation.signs, bq, cq, sh, sl)
+            lib.tq_diag_mse_bucketize(1)
+            r2 = ops.prod_quantize_qjl(xg, pd, bits, pq.mse.rotation.signs, bq, cq, sh, sl)
+        finally:
+            lib.tq_diag_mse_bucketize(0)
+        assert torch.equal(r1[0], r2[0])
+        assert torch.equal(r1[2], r2[2])

@@ -57,6 +57,7 @@ SIGNATURES = {
                                     _P, _P]),
     "tq_prod_dequantize_qjl": (_I32, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P,
                                       _P, _P]),
+    "tq_diag_mse_bucketize": (_I32, [_I32]),
     "tq_e2e_add_rms_norm": (_I32, [_P, _P, _P, _P, _I64, _I32, _F32, _P]),
     "tq_e2e_qk_norm_rope": (_I32, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _F32,
                                    _P, _P, _P]),
@@ -64,7 +65,7 @@ SIGNATURES = {
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_abi_version": (_I32, []),
 }
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib = None
 

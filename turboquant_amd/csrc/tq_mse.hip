@@ -30,6 +30,7 @@
 // 4 dim + pd*b/8 + 4 per vector.
 #include <atomic>
 #include <cmath>
+#include <cstring>
 
 #include "tq_common.h"
 
@@ -55,6 +56,10 @@ struct MseParams {
   float table[16];     // boundaries (quantize, levels - 1 used) or centroids
   float cen[16];       // centroids for the prod quantize's read-back
   int levels;
+  // quantize: the bin table of a symmetric codebook (see bin_code), when
+  // use_bins; else the binary search over `table`
+  int use_bins, bin_base;
+  uint32_t bin_b[64], bin_n[64];
 };
 
 template <int PD>
@@ -124,6 +129,40 @@ __device__ __forceinline__ float apply_sign(float v, float s) {
   return __uint_as_float(__float_as_uint(v) ^ (__float_as_uint(s) & 0x80000000u));
 }
 
+// code = #{j : b_j < y} (torch.bucketize; NaN takes the top code) by a
+// binary search over the sorted boundaries in LDS: BITS dependent LDS reads.
+template <int BITS>
+__device__ __forceinline__ int search_code(float y, const float* bnd) {
+  int c = 0;
+#pragma unroll
+  for (int s = BITS - 1; s >= 0; s--) {
+    const int cand = c + (1 << s);
+    c = bnd[cand - 1] < y ? cand : c;
+  }
+  return y != y ? (1 << BITS) - 1 : c;
+}
+
+// The same code from one LDS lookup, for a codebook symmetric about a middle
+// boundary 0 (b[M-1+k] == -b[M-1-k], M = 2^(BITS-1)).  With a = |y| as
+// integer bits (positive floats order as their bits), bin = clamp((a >> 20)
+// - base, 0, 63) is a 1/8-binade bin; the host builds the table so that each
+// bin holds at most one positive boundary B (bits; all ones if none) and
+// below = M + #{positive boundaries under the bin}, bins 0..7 lying under the
+// smallest positive boundary and bin 63 over the largest.  For y > 0 (and
+// NaN, which lands in bin 63): code = below + (a > B).  For y <= 0, code =
+// (M - 1) - #{P <= |y|} = (2M - 1) - (below + (a >= B)), and a >= B is
+// a + 1 > B.
+template <int BITS>
+__device__ __forceinline__ int bin_code(float y, const uint2* bins, int base) {
+  constexpr uint32_t kTop = (1u << BITS) - 1u;
+  const uint32_t a = __float_as_uint(y) & 0x7fffffffu;
+  const bool pos = !(y <= 0.0f);
+  const int bin = min(max((int)(a >> 20) - base, 0), 63);
+  const uint2 e = bins[bin];
+  const uint32_t t = e.y + ((pos ? a : a + 1u) > e.x ? 1u : 0u);
+  return (int)(pos ? t : kTop - t);
+}
+
 // Quantize: lane p of a vector holds its E consecutive dims p E .. p E + E - 1
 // (whole 16-byte pieces per load, and its E / per code bytes contiguous for
 // the stores); measured faster here than the dequantize kernel's chunk
@@ -162,8 +201,8 @@ __device__ __forceinline__ void load_row(const MseParams& p, int64_t row, int su
 // v holds the row as load_row leaves it
 template <int PD, int BITS, bool RES>
 __device__ __forceinline__ void quantize_row(const MseParams& p, const float* bnd,
-                                             const float* cen, int64_t row, int sub,
-                                             float (&v)[MseGeom<PD>::E]) {
+                                             const uint2* bins, const float* cen, int64_t row,
+                                             int sub, float (&v)[MseGeom<PD>::E]) {
 #pragma clang fp contract(off)
   using MG = MseGeom<PD>;
   constexpr int P = MG::P, E = MG::E;
@@ -198,23 +237,21 @@ __device__ __forceinline__ void quantize_row(const MseParams& p, const float* bn
     v[i] = apply_sign(__builtin_fmaf(r, yr, q), sgn[i]);
   }
   fwht_contig<E, P>(v, sub);
-  // code = #{j : b_j < y}: a binary search over the sorted boundaries in LDS
+  // code = #{j : b_j < y}
   uint32_t word[(NB + 3) / 4] = {};
-  constexpr int NBND = (1 << BITS) - 1;
+  auto encode = [&](auto code_of) {
 #pragma unroll
-  for (int i = 0; i < E; i++) {
-    const float y = v[i] * p.inv_sqrt_pd;
-    int c = 0;
-#pragma unroll
-    for (int s = BITS - 1; s >= 0; s--) {
-      const int cand = c + (1 << s);
-      c = bnd[cand - 1] < y ? cand : c;
+    for (int i = 0; i < E; i++) {
+      const int c = code_of(v[i] * p.inv_sqrt_pd);
+      const int byte = i / PER, slot = i % PER;
+      word[byte / 4] |= (uint32_t)c << (8 * (byte % 4) + BITS * slot);
+      if constexpr (RES) v[i] = cen[c];
     }
-    if (y != y) c = NBND;  // NaN: torch.bucketize's top index
-    const int byte = i / PER, slot = i % PER;
-    word[byte / 4] |= (uint32_t)c << (8 * (byte % 4) + BITS * slot);
-    if constexpr (RES) v[i] = cen[c];
-  }
+  };
+  if (p.use_bins)
+    encode([&](float y) { return bin_code<BITS>(y, bins, p.bin_base); });
+  else
+    encode([&](float y) { return search_code<BITS>(y, bnd); });
   if constexpr (RES) {
     fwht_contig<E, P>(v, sub);
     float rs = 0.0f;
@@ -256,14 +293,17 @@ __global__ __launch_bounds__(kMseThreads) void mse_quantize_kernel(MseParams p) 
   constexpr int P = MG::P, E = MG::E;
   __shared__ float bnd[16];
   __shared__ float cen[16];
+  __shared__ uint2 bins[64];
   if (threadIdx.x < 16) bnd[threadIdx.x] = p.table[threadIdx.x];
   if (RES && threadIdx.x >= 16 && threadIdx.x < 32) cen[threadIdx.x - 16] = p.cen[threadIdx.x - 16];
+  if (threadIdx.x >= 64 && threadIdx.x < 128)
+    bins[threadIdx.x - 64] = uint2{p.bin_b[threadIdx.x - 64], p.bin_n[threadIdx.x - 64]};
   __syncthreads();
   const int lane = threadIdx.x & 63, sub = lane % P;
   const int64_t row = (int64_t)blockIdx.x * MG::VPB + threadIdx.x / P;
   float v[E];
   load_row<PD>(p, row, sub, v);
-  quantize_row<PD, BITS, RES>(p, bnd, cen, row, sub, v);
+  quantize_row<PD, BITS, RES>(p, bnd, bins, cen, row, sub, v);
   if constexpr (RES) {
     if (row >= p.n) return;
     const int d0 = sub * E;
@@ -434,10 +474,13 @@ __global__ __launch_bounds__(kMseThreads) void prod_qjl_quantize_kernel(MseParam
   static_assert(MG::VPB == 32 && (PD == 64 || PD == 128), "32 vectors of <= 128 dims per batch");
   __shared__ float bnd[16];
   __shared__ float cen[16];
+  __shared__ uint2 bins[64];
   __shared__ __attribute__((aligned(16))) _Float16 rh[32 * RS];
   __shared__ __attribute__((aligned(16))) _Float16 rl[32 * RS];
   if (threadIdx.x < 16) bnd[threadIdx.x] = p.table[threadIdx.x];
   if (threadIdx.x >= 16 && threadIdx.x < 32) cen[threadIdx.x - 16] = p.cen[threadIdx.x - 16];
+  if (threadIdx.x >= 64 && threadIdx.x < 128)
+    bins[threadIdx.x - 64] = uint2{p.bin_b[threadIdx.x - 64], p.bin_n[threadIdx.x - 64]};
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, sub = lane % P, vl = threadIdx.x / P;
   half8_t ah[QG::NRB][QG::NKS], al[QG::NRB][QG::NKS];
   load_s_frags<PD>(q, w, lane, ah, al);
@@ -449,7 +492,7 @@ __global__ __launch_bounds__(kMseThreads) void prod_qjl_quantize_kernel(MseParam
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = xn[i];
     if (bt + gridDim.x < q.nbatch) load_row<PD>(p, (bt + gridDim.x) * 32 + vl, sub, xn);
-    quantize_row<PD, BITS, true>(p, bnd, cen, bt * 32 + vl, sub, v);
+    quantize_row<PD, BITS, true>(p, bnd, bins, cen, bt * 32 + vl, sub, v);
     // the unit residual as fp16 hi + lo (v - hi is exact in fp32)
 #pragma unroll
     for (int c = 0; c < E / 8; c++) {
@@ -615,6 +658,59 @@ hipError_t launch_mse(bool quant, int bits, const MseParams& p, hipStream_t st) 
   return hipGetLastError();
 }
 
+// The bin table of bin_code for the 2^bits - 1 sorted boundaries b, when the
+// codebook is symmetric about a middle 0 and every 1/8-binade bin holds at
+// most one positive boundary (the Lloyd-Max codebooks of 1..4 bits do);
+// returns false (binary search) otherwise.
+std::atomic<int> g_force_search{0};  // tq_diag_mse_bucketize
+
+bool build_bins(const float* b, int bits, MseParams& p) {
+  if (g_force_search.load(std::memory_order_relaxed)) return false;
+  const int M = 1 << (bits - 1);
+  auto fbits = [](float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+  };
+  if (fbits(b[M - 1]) & 0x7fffffffu) return false;  // middle boundary +-0
+  for (int k = 1; k < M; k++)
+    if (!(b[M - 1 + k] > 0.0f) || fbits(b[M - 1 + k]) != (fbits(b[M - 1 - k]) ^ 0x80000000u))
+      return false;
+  if (M == 1) {
+    p.bin_base = 0;
+    for (int i = 0; i < 64; i++) {
+      p.bin_b[i] = 0xffffffffu;
+      p.bin_n[i] = 1;
+    }
+    p.use_bins = 1;
+    return true;
+  }
+  const int base = (int)(fbits(b[M]) >> 20) - 8;
+  if (base < 0) return false;
+  for (int i = 0; i < 64; i++) {
+    const uint64_t lo = (uint64_t)(base + i) << 20, hi = (uint64_t)(base + i + 1) << 20;
+    int below = 0, inside = 0;
+    uint32_t bb = 0xffffffffu;
+    for (int k = 1; k < M; k++) {
+      const uint64_t u = fbits(b[M - 1 + k]);
+      if (u < lo) {
+        below++;
+      } else if (u < hi) {
+        inside++;
+        bb = (uint32_t)u;
+      }
+    }
+    if (inside > 1 || (i == 0 && below > 0) || (i == 63 && below + inside != M - 1))
+      return false;
+    if (i == 63 && inside) return false;  // the top bin holds every larger |y|
+    p.bin_b[i] = bb;
+    p.bin_n[i] = (uint32_t)(M + below);
+  }
+  p.bin_base = base;
+  p.use_bins = 1;
+  return true;
+}
+
 // The extra operands of the prod variants (all null for the MSE entry points)
 struct ProdArgs {
   const float* centroids = nullptr;  // quantize: read-back table
@@ -681,6 +777,9 @@ int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* o
   for (int i = 0; i < 16; i++) p.table[i] = 0.0f;
   for (int i = 0; i < (quant ? p.levels - 1 : p.levels); i++) p.table[i] = table[i];
   for (int i = 0; i < 16; i++) p.cen[i] = (pa.centroids && i < p.levels) ? pa.centroids[i] : 0.0f;
+  p.use_bins = 0;
+  p.bin_base = 0;
+  if (quant) build_bins(table, bit_width, p);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   switch (padded_dim) {
@@ -763,6 +862,9 @@ int prod_qjl_call(bool quant, const float* x, uint8_t* packed, float* norms, flo
     p.table[i] = i < (quant ? p.levels - 1 : p.levels) ? table[i] : 0.0f;
     p.cen[i] = (centroids && i < p.levels) ? centroids[i] : 0.0f;
   }
+  p.use_bins = 0;
+  p.bin_base = 0;
+  if (quant) build_bins(table, bits, p);
   QjlParams q;
   q.s_hi = s_hi;
   q.s_lo = s_lo;
@@ -889,4 +991,9 @@ extern "C" int tq_prod_dequantize_qjl(const uint8_t* packed, const float* norms,
                            mse_bit_width, signs, centroids, nullptr,
                            static_cast<const _Float16*>(st_hi), static_cast<const _Float16*>(st_lo),
                            nullptr, qjl_signs, nullptr, residual_norms, stream);
+}
+
+extern "C" int tq_diag_mse_bucketize(int32_t force_search) {
+  tq::g_force_search.store(force_search ? 1 : 0, std::memory_order_relaxed);
+  return 0;
 }

@@ -658,7 +658,7 @@ void set_error(const char* fmt, ...) {
 }  // namespace tq
 
 extern "C" const char* tq_last_error(void) { return tq::g_err; }
-extern "C" int32_t tq_abi_version(void) { return 7; }
+extern "C" int32_t tq_abi_version(void) { return 8; }
 
 extern "C" int tq_quantize_write_kv_cache(void* k_slab, void* v_slab, const void* key,
                                           const void* value, int32_t in_dtype,
