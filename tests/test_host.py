@@ -428,3 +428,18 @@ def test_e2e_glue_entry_points_refuse_bad_arguments():
     assert lib.tq_e2e_silu_mul(one, one, 4, 12, None) == -22
     assert lib.tq_e2e_silu_mul(one, None, 4, 16, None) == -22
     assert lib.tq_e2e_silu_mul(None, None, 0, 16, None) == 0
+
+
+def test_bench_refuses_more_than_one_gpu_and_imports_no_tests():
+    """bench.py --gpus N > 1 exits non-zero with a message saying the build
+    is one-GPU (no GPU call happens before that check), and the measurement
+    harness imports nothing from tests/."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0
+    assert "--gpus 2 is not supported" in (r.stdout + r.stderr)
+    src = open(os.path.join(root, "bench.py")).read()
+    assert "from tests" not in src and "import tests" not in src
