@@ -51,6 +51,10 @@ CASES64 = [
     (129, 400, 16, 4),
     (1000, 1000, 16, 4),
     (4100, 4500, 16, 4),
+    # 256-row blocks of four waves x two row blocks (heads x blocks >= CUs):
+    # GQA 8 with a ragged last block, and GQA 1
+    (2500, 3001, 32, 4),
+    (4097, 4097, 16, 16),
     # short chunk over a long context: keys split over workgroups, then merged
     (256, 8000, 16, 4),
 ]

@@ -396,6 +396,251 @@ void prefill_kernel(PrefillParams p) {
   }
 }
 
+// The same attention with RB row blocks of 32 query rows per wave: each K
+// fragment and each V^T fragment read from LDS feeds RB MFMAs instead of
+// one, so a tile's LDS reads per MFMA drop by RB.  Non-split only.  Row block
+// rb of wave w holds rows q0 + 32 (RB w + rb) + n.  Used at head size 64
+// (RB 2, 64-key tiles: 217 VGPRs, two waves per SIMD), where the registers
+// of two row blocks fit; at head size 128 they do not (one wave per SIMD,
+// measured slower).
+template <int kD, int NW, int kBN, int RB, int WPE>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void prefill_rb_kernel(PrefillParams p) {
+  constexpr int kKRow = kD * 2;
+  constexpr int kCH = kD / 8;
+  constexpr int kRPC = 1024 / kKRow;
+  constexpr int kBM = 32 * NW * RB;
+  constexpr int kNU = kBN / 32, kNS = kBN / 16;
+  constexpr int kQS = kD >= 128 ? 0 : 1;
+  __shared__ __attribute__((aligned(16))) uint8_t kbuf0[kBN * kKRow];
+  __shared__ __attribute__((aligned(16))) uint8_t kbuf1[kBN * kKRow];
+  __shared__ __attribute__((aligned(16))) uint8_t vbuf0[kBN * kKRow];
+  __shared__ __attribute__((aligned(16))) uint8_t vbuf1[kBN * kKRow];
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int hh = lane >> 5, n = lane & 31;
+  const int qb = p.nqb - 1 - (int)blockIdx.y;
+  const int head = blockIdx.x, g = head / p.ratio;
+  const int q0 = qb * kBM;
+  const int off = p.lk - p.lq;
+  const int wrow0 = q0 + 32 * RB * w;  // the wave's first row
+  const int kend = min(p.lk, off + min(q0 + kBM, p.lq));
+  const int ntiles = (kend + kBN - 1) / kBN;
+
+  half8_t qB[RB][kD / 16];
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++) {
+    const int qrow = wrow0 + 32 * rb + n;
+    const _Float16* qp = p.q + (int64_t)qrow * p.q_st + (int64_t)head * p.q_sh + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < kD / 16; s++) {
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (qrow < p.lq) x = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+      qB[rb][s] = __builtin_bit_cast(half8_t, x);
+    }
+  }
+
+  constexpr int kKC = (kBN / kRPC) / NW;
+  const int kst_b = (int)(p.k_st * 2), vst_b = (int)(p.v_st * 2);
+  uint32_t koff[kKC], voff[kKC];
+#pragma unroll
+  for (int i = 0; i < kKC; i++) {
+    const int j = w + NW * i, row = kRPC * j + lane / kCH;
+    koff[i] = (uint32_t)(row * kst_b + (((lane % kCH) ^ (row % kCH)) * 16));
+    voff[i] = (uint32_t)(row * vst_b + (((lane % kCH) ^ (4 * ((row & 3) >> kQS))) * 16));
+  }
+  auto tile_rsrc = [&](const _Float16* base, int64_t st, int kb) {
+    const int rows = min(kBN, p.lk - kb);
+    const uint64_t a = (uint64_t)(uintptr_t)(base + (int64_t)kb * st);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    const int nrec = __builtin_amdgcn_readfirstlane(rows * (int)(st * 2));
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)(((uint64_t)hi << 32) | lo),
+                                             (short)0, nrec, 0x00020000);
+  };
+  const _Float16* const kbase = p.k + (int64_t)g * p.k_sh;
+  const _Float16* const vbase = p.v + (int64_t)g * p.v_sh;
+  auto issue = [&](int kt, uint8_t* kb, uint8_t* vb) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase, p.k_st, kt * kBN);
+    const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase, p.v_st, kt * kBN);
+#pragma unroll
+    for (int i = 0; i < kKC; i++) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (void*)(kb + 1024 * (w + NW * i)), 16,
+                                               koff[i], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (void*)(vb + 1024 * (w + NW * i)), 16,
+                                               voff[i], 0, 0, 0);
+    }
+#else
+    (void)kt;
+    (void)kb;
+    (void)vb;
+    (void)tile_rsrc;
+    (void)kbase;
+    (void)vbase;
+#endif
+  };
+  const int vgq = lane >> 4, vsl = lane & 15, vt4 = vsl >> 2;
+  const uint32_t vread_base =
+      (uint32_t)((4 * hh + vt4) * kKRow +
+                 ((2 * (vgq & 1) + ((vsl & 3) >> 1)) ^ (4 * (vt4 >> kQS))) * 16 + 8 * (vsl & 1));
+
+  f32x16 oacc[RB][kD / 32];
+  float m[RB], mc[RB], lsum[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++) {
+#pragma unroll
+    for (int d = 0; d < kD / 32; d++)
+#pragma unroll
+      for (int j = 0; j < 16; j++) oacc[rb][d][j] = 0.0f;
+    m[rb] = -INFINITY;
+    mc[rb] = -INFINITY;
+    lsum[rb] = 0.0f;
+  }
+
+  auto tile = [&](int kt, const uint8_t* kbuf, const uint8_t* vt) {
+    const int kb = kt * kBN;
+    if (kb > off + wrow0 + 32 * RB - 1) return;  // beyond every row of the wave
+    constexpr int kKP = 4;
+    constexpr int kNI = kNU * (kD / 16);
+    f32x16 sacc[RB][kNU];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int u = 0; u < kNU; u++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) sacc[rb][u][j] = 0.0f;
+    auto kfrag = [&](int i) {
+      const int u = i % kNU, s = i / kNU, row = 32 * u + n;
+      return *reinterpret_cast<const u32x4*>(kbuf + row * kKRow +
+                                             (((2 * s + hh) ^ (row % kCH)) * 16));
+    };
+    u32x4 fr[kKP];
+#pragma unroll
+    for (int j = 0; j < kKP; j++) fr[j] = kfrag(j);
+#pragma unroll
+    for (int i = 0; i < kNI; i++) {
+      const u32x4 a = fr[i % kKP];
+      if (i + kKP < kNI) fr[i % kKP] = kfrag(i + kKP);
+#pragma unroll
+      for (int rb = 0; rb < RB; rb++)
+        sacc[rb][i % kNU] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(half8_t, a), qB[rb][i / kNU], sacc[rb][i % kNU], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, kKP, 0);
+#pragma unroll
+    for (int i = 0; i < kNI; i++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);  // the RB MFMAs of read i
+      if (i + kKP < kNI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    half8_t pB[RB][kNS];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+      const int rfirst = wrow0 + 32 * rb;
+      if (kb + kBN - 1 > off + rfirst || kb + kBN > p.lk) {
+        const int lim = min(off + rfirst + n, p.lk - 1) - kb - 4 * hh;
+#pragma unroll
+        for (int u = 0; u < kNU; u++)
+#pragma unroll
+          for (int j = 0; j < 16; j++) {
+            const int kk = 32 * u + 8 * (j >> 2) + (j & 3);
+            sacc[rb][u][j] += __int_as_float(((lim - kk) >> 31) & (int)0xff800000u);
+          }
+      }
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < kNU; u++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) tmax = fmaxf(tmax, sacc[rb][u][j]);
+      tmax = max32(tmax);
+      const float m_new = fmaxf(m[rb], tmax);
+      if (__builtin_amdgcn_ballot_w64(m_new * p.c > mc[rb] + 8.0f) != 0) {
+        const float alpha =
+            m[rb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc[rb] - m_new * p.c);
+#pragma unroll
+        for (int d = 0; d < kD / 32; d++) oacc[rb][d] *= alpha;
+        lsum[rb] *= alpha;
+        m[rb] = m_new;
+        mc[rb] = m_new * p.c;
+      }
+      const float mce = mc[rb] == -INFINITY ? 0.0f : mc[rb];
+#pragma unroll
+      for (int u = 0; u < kNU; u++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          float pr[8];
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[rb][u][8 * t + i], p.c, -mce));
+            if constexpr (kD != 64) lsum[rb] += pr[i];
+          }
+          u32x4 pk;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const half2_t h = __builtin_convertvector(f32x2{pr[2 * i], pr[2 * i + 1]}, half2_t);
+            if constexpr (kD == 64)
+              lsum[rb] = __builtin_amdgcn_fdot2(h, half2_t{(_Float16)1.0f, (_Float16)1.0f},
+                                                lsum[rb], false);
+            pk[i] = __builtin_bit_cast(uint32_t, h);
+          }
+          pB[rb][2 * u + t] = __builtin_bit_cast(half8_t, pk);
+        }
+    }
+#pragma unroll
+    for (int st = 0; st < kNS; st++) {
+#pragma unroll
+      for (int d = 0; d < kD / 32; d++) {
+        typedef __attribute__((address_space(3))) uint8_t lds_u8;
+        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+        lds_u8* const pd = (lds_u8*)vt + (vread_base ^ (uint32_t)(64 * d)) + 16 * st * kKRow;
+        const u32x2 a0 =
+            __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)pd));
+        const u32x2 a1 = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(pd + 8 * kKRow)));
+        const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+          oacc[rb][d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              __builtin_bit_cast(half8_t, a), pB[rb][st], oacc[rb][d], 0, 0, 0);
+      }
+    }
+  };
+
+  if (ntiles > 0) issue(0, kbuf0, vbuf0);
+  for (int kt = 0; kt < ntiles; kt += 2) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+    if (kt + 1 < ntiles) issue(kt + 1, kbuf1, vbuf1);
+    tile(kt, kbuf0, vbuf0);
+    if (kt + 1 >= ntiles) break;
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+    if (kt + 2 < ntiles) issue(kt + 2, kbuf0, vbuf0);
+    tile(kt + 1, kbuf1, vbuf1);
+  }
+
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++) {
+    const int qrow = wrow0 + 32 * rb + n;
+    const float ls = sum32(lsum[rb]);
+    if (qrow < p.lq) {
+      const float inv = ls > 0.0f ? 1.0f / ls : 0.0f;
+      _Float16* op = p.o + (int64_t)qrow * p.o_st + (int64_t)head * p.o_sh + 4 * hh;
+#pragma unroll
+      for (int d = 0; d < kD / 32; d++)
+#pragma unroll
+        for (int jq = 0; jq < 4; jq++) {
+          const uint32_t lo =
+              pack_h2(oacc[rb][d][4 * jq] * inv, oacc[rb][d][4 * jq + 1] * inv);
+          const uint32_t hi =
+              pack_h2(oacc[rb][d][4 * jq + 2] * inv, oacc[rb][d][4 * jq + 3] * inv);
+          *reinterpret_cast<u32x2*>(op + 32 * d + 8 * jq) = u32x2{lo, hi};
+        }
+    }
+  }
+}
+
 // Merge of the splits of split-KV mode: one wave per (query row, q head),
 // o = sum_z w_z (O_z / l_z) / sum_z w_z, w_z = 2^(mc_z - M) l_z, fp16 out.
 template <int kD>
@@ -426,8 +671,10 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p, int
   for (int i = 0; i < V; i++) op[i] = (_Float16)(acc[i] * inv);
 }
 
-// the workgroup shapes, at head size 64 or 128: eight waves, 128-key tiles;
-// four waves, 64-key tiles; four waves split over the keys (then merged).
+// the workgroup shapes, at head size 64 or 128: 256 query rows (eight waves
+// with 128-key tiles at head size 128; four waves of two row blocks with
+// 64-key tiles at head size 64); four waves, 64-key tiles; four waves split
+// over the keys (then merged).
 // Head size 256: four waves, 64-key tiles (128 KB of LDS for the K and V
 // double buffers), one wave per SIMD, split or not.
 template <int D>
@@ -446,6 +693,10 @@ hipError_t launch_prefill(int nw, int heads, hipStream_t st, const PrefillParams
       hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)((waves + 3) / 4)), dim3(256),
                          0, st, p, heads);
     }
+  } else if (nw == 8 && D == 64) {
+    // head size 64: four waves of 64 rows (two row blocks each), 64-key tiles
+    hipLaunchKernelGGL((prefill_rb_kernel<D, 4, 64, 2, 2>), dim3(heads, p.nqb), dim3(256), 0, st,
+                       p);
   } else if (nw == 8) {
     hipLaunchKernelGGL((prefill_kernel<D, 8, 128, false>), dim3(heads, p.nqb), dim3(512), 0, st,
                        p);
