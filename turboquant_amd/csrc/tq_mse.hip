@@ -69,8 +69,21 @@ struct MseGeom {
   static constexpr int VPB = kMseThreads / P;        // vectors per workgroup
 };
 
-// value of lane l ^ m (m < 64) through ds_bpermute
-__device__ __forceinline__ float lane_xor(float v, int m) { return __shfl_xor(v, m); }
+// value of lane l ^ m: DPP moves for m = 1, 2, 4, 8 (quad permutes; row
+// half-mirror then quad reversal; row rotate by 8), ds_bpermute otherwise
+__device__ __forceinline__ float lane_xor(float v, int m) {
+  const int x = __float_as_int(v);
+  switch (m) {
+    case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false));
+    case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false));
+    case 4: {
+      const int t = __builtin_amdgcn_mov_dpp(x, 0x141, 0xf, 0xf, false);
+      return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x1B, 0xf, 0xf, false));
+    }
+    case 8: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, false));
+    default: return __shfl_xor(v, m);
+  }
+}
 
 // Walsh-Hadamard transform (unnormalised, ascending stride) of the PD dims
 // the P lanes of a vector hold: v[8 i + c] = dim 8 (p + P i) + c.
@@ -229,7 +242,15 @@ __device__ __forceinline__ void quantize_row(const MseParams& p, const float* bn
   // theorem, IBM J. Res. Dev. 34(1), 1990), for every finite x here (|x / n|
   // <= 1, no overflow; x = 0 gives +-0 as x / n does)
   const float yr = 1.0f / nrm;
-  const float* sgn = p.signs + d0;
+  float sgn[E];  // the lane's signs, float4 loads (signs is 16-byte aligned)
+#pragma unroll
+  for (int i = 0; i < E / 4; i++) {
+    const float4 f = reinterpret_cast<const float4*>(p.signs + d0)[i];
+    sgn[4 * i] = f.x;
+    sgn[4 * i + 1] = f.y;
+    sgn[4 * i + 2] = f.z;
+    sgn[4 * i + 3] = f.w;
+  }
 #pragma unroll
   for (int i = 0; i < E; i++) {
     const float q = v[i] * yr;
@@ -379,9 +400,24 @@ __device__ __forceinline__ void dequantize_row(const MseParams& p, const float* 
   if (!live) return;
   float* orow = p.out + row * p.dim;
   const float wq = ADD ? p.add_scale * p.gamma[row] : 0.0f;
+  // the signs of the lane's chunks, two float4 loads per chunk
+  float sg[E];
+#pragma unroll
+  for (int i = 0; i < NC; i++) {
+    const float4* sp = reinterpret_cast<const float4*>(p.signs + 8 * (sub + P * i));
+    const float4 a = sp[0], b = sp[1];
+    sg[8 * i] = a.x;
+    sg[8 * i + 1] = a.y;
+    sg[8 * i + 2] = a.z;
+    sg[8 * i + 3] = a.w;
+    sg[8 * i + 4] = b.x;
+    sg[8 * i + 5] = b.y;
+    sg[8 * i + 6] = b.z;
+    sg[8 * i + 7] = b.w;
+  }
   auto val = [&](int i) {
     const int d = 8 * (sub + P * (i / 8)) + i % 8;
-    const float xm = apply_sign(v[i] * p.inv_sqrt_pd, p.signs[d]) * nrm;
+    const float xm = apply_sign(v[i] * p.inv_sqrt_pd, sg[i]) * nrm;
     if constexpr (ADD) return xm + arow[d] * wq;
     else return xm;
   };
@@ -752,9 +788,9 @@ int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* o
   }
   // full-width rows are read / written as float4, packed rows as dwords
   const uintptr_t al = (uintptr_t)(quant ? (const void*)x : (const void*)out) |
-                       (uintptr_t)packed | (uintptr_t)pa.resid;
+                       (uintptr_t)packed | (uintptr_t)pa.resid | (uintptr_t)signs;
   if ((al & 15) != 0) {
-    set_error("%s: x / out and packed must be 16-byte aligned", what);
+    set_error("%s: x / out, packed and signs must be 16-byte aligned", what);
     return kEinval;
   }
   const int per = bit_width == 3 ? 2 : 8 / bit_width;
@@ -836,9 +872,9 @@ int prod_qjl_call(bool quant, const float* x, uint8_t* packed, float* norms, flo
   }
   if (n == 0) return 0;
   const uintptr_t al = (uintptr_t)(quant ? (const void*)x : (const void*)out) |
-                       (uintptr_t)packed | (uintptr_t)s_hi | (uintptr_t)s_lo;
+                       (uintptr_t)packed | (uintptr_t)s_hi | (uintptr_t)s_lo | (uintptr_t)signs;
   if ((al & 15) != 0) {
-    set_error("%s: x / out, packed and the S halves must be 16-byte aligned", what);
+    set_error("%s: x / out, packed, signs and the S halves must be 16-byte aligned", what);
     return kEinval;
   }
   const int per = bits == 3 ? 2 : 8 / bits;

@@ -298,6 +298,13 @@ def _host_f32(values) -> "ctypes.Array":
     return (ctypes.c_float * max(1, len(vals)))(*vals)
 
 
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    """t contiguous at a 16-byte aligned address (the kernels read it in
+    16-byte pieces); a copy when it is not."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def mse_quantize(x: torch.Tensor, padded_dim: int, bit_width: int, signs: torch.Tensor,
                  boundaries) -> tuple[torch.Tensor, torch.Tensor]:
     """TurboQuantMSE.quantize on the GPU (tq_mse_quantize): x fp32
@@ -318,6 +325,7 @@ def mse_quantize(x: torch.Tensor, padded_dim: int, bit_width: int, signs: torch.
     per = 2 if bit_width == 3 else 8 // bit_width
     packed = torch.empty((*lead, padded_dim // per), dtype=torch.uint8, device=x.device)
     norms = torch.empty(lead, dtype=torch.float32, device=x.device)
+    signs = _aligned16(signs)
     lib = _lib.load()
     with torch.cuda.device(x.device):
         rc = lib.tq_mse_quantize(x.data_ptr(), n, dim, int(padded_dim), int(bit_width),
@@ -345,6 +353,7 @@ def mse_dequantize(packed: torch.Tensor, norms: torch.Tensor, dim: int, padded_d
     lead = packed.shape[:-1]
     n = nf.numel()
     out = torch.empty((*lead, dim), dtype=torch.float32, device=packed.device)
+    signs = _aligned16(signs)
     lib = _lib.load()
     with torch.cuda.device(packed.device):
         rc = lib.tq_mse_dequantize(packed.data_ptr(), nf.data_ptr(), n, int(dim),
@@ -376,6 +385,7 @@ def prod_quantize(x: torch.Tensor, padded_dim: int, mse_bit_width: int, signs: t
     norms = torch.empty(lead, dtype=torch.float32, device=x.device)
     resid = torch.empty((*lead, dim), dtype=torch.float32, device=x.device)
     rnorm = torch.empty(lead, dtype=torch.float32, device=x.device)
+    signs = _aligned16(signs)
     lib = _lib.load()
     with torch.cuda.device(x.device):
         rc = lib.tq_prod_quantize(x.data_ptr(), n, dim, int(padded_dim), int(mse_bit_width),
@@ -408,6 +418,7 @@ def prod_dequantize(packed: torch.Tensor, norms: torch.Tensor, qjl_term: torch.T
     rn = residual_norms.to(torch.float32).contiguous()
     qt = qjl_term.to(torch.float32).contiguous()
     out = torch.empty((*lead, dim), dtype=torch.float32, device=packed.device)
+    signs = _aligned16(signs)
     lib = _lib.load()
     with torch.cuda.device(packed.device):
         rc = lib.tq_prod_dequantize(packed.data_ptr(), nf.data_ptr(), qt.data_ptr(),
@@ -444,6 +455,7 @@ def prod_quantize_qjl(x: torch.Tensor, padded_dim: int, mse_bit_width: int,
     norms = torch.empty(lead, dtype=torch.float32, device=x.device)
     z = torch.empty((*lead, dim), dtype=torch.int8, device=x.device)
     rnorm = torch.empty(lead, dtype=torch.float32, device=x.device)
+    signs = _aligned16(signs)
     lib = _lib.load()
     with torch.cuda.device(x.device):
         rc = lib.tq_prod_quantize_qjl(x.data_ptr(), n, dim, int(padded_dim), int(mse_bit_width),
@@ -483,6 +495,7 @@ def prod_dequantize_qjl(packed: torch.Tensor, norms: torch.Tensor, qjl_signs: to
     rn = residual_norms.to(torch.float32).contiguous()
     z = qjl_signs.contiguous()
     out = torch.empty((*lead, dim), dtype=torch.float32, device=packed.device)
+    signs = _aligned16(signs)
     lib = _lib.load()
     with torch.cuda.device(packed.device):
         rc = lib.tq_prod_dequantize_qjl(packed.data_ptr(), nf.data_ptr(), z.data_ptr(),
