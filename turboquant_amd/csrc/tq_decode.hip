@@ -1693,17 +1693,27 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
   }
   // the split groups of a column: lanes c + CW g, g = 0 .. NG-1, met by lane
   // xors CW .. 32 (a common max first, then the rescaled sums)
+  // (lane xor 4 / 8 by DPP, 16 / 32 by permlane swaps: no LDS round trips)
+  auto xsum = [](float x, int d) {
+    if (d == 16) return xor16_sum(x);
+    if (d == 32) return xor32_sum(x);
+    return x + xor_lane(x, d);
+  };
   float mx = m;
 #pragma unroll
-  for (int d = CW; d < 64; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+  for (int d = CW; d < 64; d <<= 1) {
+    if (d == 16) mx = xor16_max(mx);
+    else if (d == 32) mx = xor32_max(mx);
+    else mx = fmaxf(mx, xor_lane(mx, d));
+  }
   const float sc = (m > -INFINITY) ? __expf(m - mx) : 0.0f;
   den *= sc;
   acc *= sc;
 #pragma unroll
   for (int d = CW; d < 64; d <<= 1) {
-    den += __shfl_xor(den, d);
+    den = xsum(den, d);
 #pragma unroll
-    for (int k = 0; k < 4; k++) acc[k] += __shfl_xor(acc[k], d);
+    for (int k = 0; k < 4; k++) acc[k] = xsum(acc[k], d);
   }
   if (g == 0) {
     const float inv = den > 0.f ? 1.0f / den : 0.0f;
