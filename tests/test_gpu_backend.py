@@ -184,3 +184,61 @@ def test_dequant_paged_matches_float64_dequantization():
                 g = got[:333, kvh].float().cpu().numpy()
                 assert np.abs(g - want).max() <= 2e-3 * max(1.0, np.abs(want).max()), hd
         assert (out_k[333:] == 7.0).all()  # rows past num_tokens untouched
+
+
+def test_backend_decode_batches_beyond_one_balanced_plan():
+    """A balanced plan takes at most 1024 sequences: a 1100-sequence decode
+    batch goes through the reference's static-split op (same kernels), and
+    the 1030 decode rows of a mixed batch through the balanced op in chunks
+    of at most 1024; both against the oracle."""
+    print("case: backend decode of 1100 sequences and a mixed batch of 1030 + 1", flush=True)
+    from turboquant_amd import decoder_dispatch as dd
+    from turboquant_amd.geometry import BALANCED_MAX_BATCH
+    from turboquant_amd.vllm_backend_fused import TurboQuantBackend, TurboQuantFusedImpl
+    dd.pick_decode_op.cache_clear()
+    assert BALANCED_MAX_BATCH == 1024
+    dev = G.DEV
+    hq, hkv, hd, bs = 8, 2, 128, 16
+    rng = np.random.default_rng(5)
+    lens = rng.integers(1, 70, size=1100).tolist()
+    c = W.decode_case(72, len(lens), lens, hq, hkv, hd)
+    shape = TurboQuantBackend.get_kv_cache_shape(c["num_blocks"], bs, hkv, hd, "fp8")
+    cache = torch.zeros(shape, dtype=torch.uint8, device=dev)
+    impl = TurboQuantFusedImpl(hq, hd, 1.0 / np.sqrt(hd), hkv, None, None, "fp8")
+    k = torch.from_numpy(c["k"]).to(dev)
+    v = torch.from_numpy(c["v"]).to(dev)
+    slots = torch.from_numpy(c["slots"]).to(dev)
+    impl.do_kv_cache_update(None, k.view(-1, hkv, hd), v.view(-1, hkv, hd), cache, slots)
+    b = len(lens)
+    bt = torch.from_numpy(c["block_table"]).to(dev)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    q = torch.from_numpy(c["q"]).to(dev).view(b, hq * hd)
+    ref = G.oracle_decode(c, cache.cpu().numpy(), c["q"], 128, 1.0 / np.sqrt(hd))
+    # pure decode batch of 1100
+    meta = Meta(1, b, bt, sl, torch.arange(b + 1, dtype=torch.int32, device=dev), slots[:b])
+    out = torch.empty((b, hq * hd), dtype=torch.float16, device=dev)
+    impl.forward(None, q, None, None, cache, meta, output=out)
+    torch.cuda.synchronize()
+    G.assert_close(out.float().cpu().numpy().reshape(b, hq, hd), ref, "decode of 1100")
+    # mixed batch: 1030 sequences decode one token each (ctx > 0),
+    # the last one brings a 2-token chunk (its output is not checked here)
+    dec = [i for i in range(b) if lens[i] >= 2][:1030]  # ctx = len - 1 > 0: decode rows
+    last = b - 1
+    while lens[last] < 3:
+        last -= 1
+    rows = dec + [last]
+    qsl = list(range(len(dec) + 1)) + [len(dec) + 2]
+    n = qsl[-1]
+    qm = torch.zeros((n, hq * hd), dtype=torch.float16, device=dev)
+    qm[:len(dec)] = q[dec]
+    km = torch.zeros((n, hkv * hd), dtype=torch.float16, device=dev)
+    vm = torch.zeros_like(km)
+    meta = Meta(2, n, bt[rows], sl[rows], torch.tensor(qsl, dtype=torch.int32, device=dev),
+                slots[:n])
+    out = torch.zeros((n, hq * hd), dtype=torch.float16, device=dev)
+    impl.forward(None, qm, km, vm, cache, meta, output=out)
+    torch.cuda.synchronize()
+    got = out[:len(dec)].float().cpu().numpy().reshape(len(dec), hq, hd)
+    assert len(dec) == 1030
+    G.assert_close(got, ref[dec], "mixed decode rows")
+    dd.pick_decode_op.cache_clear()

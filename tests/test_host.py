@@ -443,3 +443,13 @@ def test_bench_refuses_more_than_one_gpu_and_imports_no_tests():
     assert "--gpus 2 is not supported" in (r.stdout + r.stderr)
     src = open(os.path.join(root, "bench.py")).read()
     assert "from tests" not in src and "import tests" not in src
+
+
+def test_balanced_batch_limit_matches_the_kernel():
+    """The backend routes decode batches above BALANCED_MAX_BATCH to the
+    static-split op; the constant is the kernel's plan limit."""
+    from turboquant_amd.geometry import BALANCED_MAX_BATCH
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = open(os.path.join(root, "turboquant_amd", "csrc", "tq_decode.hip")).read()
+    m = re.search(r"constexpr int kPlanMaxBatch = (\d+);", src)
+    assert m and int(m.group(1)) == BALANCED_MAX_BATCH

@@ -132,3 +132,8 @@ def choose_splits(batch: int, max_len: int, num_kv_heads: int, num_qo_heads: int
     chunk = (chunk + CHUNK_ALIGN - 1) // CHUNK_ALIGN * CHUNK_ALIGN
     splits = math.ceil(max_len / chunk)
     return splits, chunk
+
+# Sequences one balanced decode plan takes (tq_decode.hip kPlanMaxBatch; the
+# plan stages per-sequence lengths in LDS).  Larger decode batches take the
+# static-split op.
+BALANCED_MAX_BATCH = 1024

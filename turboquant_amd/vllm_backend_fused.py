@@ -24,9 +24,10 @@ import traceback
 import torch
 import torch.nn.functional as F
 
-from .decoder_dispatch import KERNEL_NAME
-from .geometry import (QUANT_BYTES_PER_CHUNK, TILE_DIMS, choose_splits, entry_bytes,
-                       hadamard_signs, padded_dim)
+from .decoder_dispatch import KERNEL_NAME, STATIC_KERNEL_NAME
+from .decoder_dispatch import _op as _dispatch_op
+from .geometry import (BALANCED_MAX_BATCH, QUANT_BYTES_PER_CHUNK, TILE_DIMS, choose_splits,
+                       entry_bytes, hadamard_signs, padded_dim)
 
 try:  # pragma: no cover - exercised only where vLLM is installed
     from vllm.v1.attention.backends.flash_attn import (FlashAttentionBackend,
@@ -163,15 +164,17 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
         return choose_splits(batch_size, max_len, num_kv_heads)[0]
 
     def _get_v5_ws(self, batch_size: int, max_pages: int, block_size: int,
-                   device: torch.device):
+                   device: torch.device, op_name: str | None = None):
         """Workspace keyed by (batch_size, max_pages) as in the reference
         (vllm_backend_fused.py:158-215): allocated on the first call of a
-        shape bucket (vLLM warm-up), reused by graph replays.
+        shape bucket (vLLM warm-up), reused by graph replays.  op_name: the
+        op the workspace is for (default: the dispatched one).
         Returns (ws, max_len, num_splits)."""
-        key = (batch_size, max_pages, self._decode_op_name)
+        op_name = op_name or self._decode_op_name
+        key = (batch_size, max_pages, op_name)
         max_len = max_pages * block_size
         ws = self._v5_ws_cache.get(key)
-        if ws is None and self._decode_op_name == KERNEL_NAME:
+        if ws is None and op_name == KERNEL_NAME:
             # balanced plan: rows for the resident workgroup slots, the row
             # table written by the kernel
             from .ops import balanced_rows
@@ -396,6 +399,15 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
             o = self._attend(q, kk, vv, ctx, dst)
             if o.data_ptr() != dst.data_ptr():
                 dst.copy_(o)
+        for c0 in range(0, len(dec), BALANCED_MAX_BATCH):  # a plan takes <= 1024 rows
+            self._decode_rows(dec[c0:c0 + BALANCED_MAX_BATCH], qsl, query, kv_cache, bt,
+                              attn_metadata, output)
+        return output
+
+    def _decode_rows(self, dec, qsl, query, kv_cache, bt, attn_metadata, output):
+        """The decode rows `dec` (request indices, q_len 1) of a mixed batch
+        through the balanced decode op; at most BALANCED_MAX_BATCH of them."""
+        from . import ops
         if dec:
             dev = query.device
             rows = torch.tensor([qsl[i] for i in dec], dtype=torch.long, device=dev)
@@ -465,8 +477,17 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
             if self.head_size < self._pd:
                 q_fp16 = F.pad(q_fp16, (0, self._pd - self.head_size))
             batch_size = q_fp16.shape[0]
+            # the balanced plan takes up to BALANCED_MAX_BATCH sequences; a
+            # larger decode batch takes the reference's static-split op (same
+            # kernels, host-planned splits)
+            balanced = (self._decode_op_name == KERNEL_NAME
+                        and batch_size <= BALANCED_MAX_BATCH)
+            op_name = (self._decode_op_name if balanced or self._decode_op_name != KERNEL_NAME
+                       else STATIC_KERNEL_NAME)
+            decode_op = (self._decode_op if op_name == self._decode_op_name
+                         else _dispatch_op(STATIC_KERNEL_NAME))
             ws, max_len, num_splits = self._get_v5_ws(batch_size, max_pages, block_size,
-                                                      q.device)
+                                                      q.device, op_name)
             kv_indptr = ws.get("indptr")
             if kv_indptr is None:
                 kv_indptr = ws["indptr"] = torch.arange(
@@ -478,9 +499,9 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
             direct = (self.head_size == self._pd and out3.dtype == torch.float16
                       and out3.is_contiguous())
             o_ws = out3 if direct else ws["o"]
-            if self._decode_op_name == KERNEL_NAME:
+            if balanced:
                 # the op writes o_ws (declared in its schema) and returns nothing
-                self._decode_op(
+                decode_op(
                     q_fp16, kv_cache, kv_indices, kv_indptr, sl, self.num_kv_heads,
                     self.head_size, self._pd, self.scale, self._signs, o_ws,
                     ws["partition_o"], ws["partition_lse"], ws["split_indptr"])
@@ -488,7 +509,7 @@ class TurboQuantFusedImpl(FlashAttentionImpl):
             else:
                 num_pages = (seq_lens + block_size - 1) // block_size
                 kv_last_page_len = seq_lens - (num_pages - 1) * block_size
-                result = self._decode_op(
+                result = decode_op(
                     q_fp16, kv_cache, kv_indices, kv_indptr, kv_last_page_len, sl,
                     self.num_kv_heads, block_size, self.head_size, self._pd, self.scale,
                     self._signs, self._qbytes, self._nbytes, o_ws, max_len,
