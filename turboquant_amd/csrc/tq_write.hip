@@ -414,18 +414,15 @@ __global__ __launch_bounds__(256) void write_f16_kernel(
   const uint32_t rem = g - (kv ? per_kv : 0u);
   const uint32_t t = H == 1 ? rem : __umulhi(rem, hmul);  // rem / H, exact (hmul = ceil(2^32/H))
   const int h = (int)(rem - t * (uint32_t)H);
+  // lanes past the end read row 0 of K (no branch, no zero fill); they
+  // store nothing (slot -1)
   u32x4 raw[CPL];
-  int32_t slot = -1;
-  if (live) {
-    const _Float16* row = kv ? value + (int64_t)t * v_st + (int64_t)h * v_sh
-                             : key + (int64_t)t * k_st + (int64_t)h * k_sh;
+  const _Float16* row = !live ? key
+                        : kv  ? value + (int64_t)t * v_st + (int64_t)h * v_sh
+                              : key + (int64_t)t * k_st + (int64_t)h * k_sh;
 #pragma unroll
-    for (int i = 0; i < CPL; i++) raw[i] = *reinterpret_cast<const u32x4*>(row + 8 * (p + P * i));
-    slot = slots[t];
-  } else {
-#pragma unroll
-    for (int i = 0; i < CPL; i++) raw[i] = u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int i = 0; i < CPL; i++) raw[i] = *reinterpret_cast<const u32x4*>(row + 8 * (p + P * i));
+  const int32_t slot = live ? slots[t] : -1;
 
   // boundaries b_k * scale (k = 1..7) as integer bits (positive floats order
   // as their bits); bin table over the four binades from the smallest one
