@@ -37,4 +37,7 @@ __host__ __device__ constexpr float boundary_pos(int k) {  // k = 1..7 -> b[7+k]
 // Thread-local error message for the C ABI.
 void set_error(const char* fmt, ...);
 
+// Compute units of the current device, queried once per device (0 if unknown).
+int device_cus();
+
 }  // namespace tq

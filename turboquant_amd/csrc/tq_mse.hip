@@ -829,17 +829,6 @@ int mse_call(bool quant, const float* x, uint8_t* packed, float* norms, float* o
   return (int)e;
 }
 
-// CUs of the current device, queried once per device (0 if unknown).
-int mse_device_cus() {
-  constexpr int kMaxDev = 64;
-  static std::atomic<int> cache[kMaxDev];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
-  int c = cache[dev].load(std::memory_order_relaxed);
-  if (c == 0 && hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-    cache[dev].store(c, std::memory_order_relaxed);
-  return c;
-}
 
 // TurboQuantProd with the QJL projections fused (padded size 64 or 128).
 int prod_qjl_call(bool quant, const float* x, uint8_t* packed, float* norms, float* out,
@@ -909,7 +898,7 @@ int prod_qjl_call(bool quant, const float* x, uint8_t* packed, float* norms, flo
   q.nbatch = (n + 31) / 32;
   // persistent: the resident workgroups of the whole chip, each loading its
   // S blocks once (occupancy queried per kernel, once)
-  const int cus = mse_device_cus();
+  const int cus = device_cus();
   const dim3 block(kMseThreads);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   auto grid_for = [&](const void* fn, std::atomic<int>& per_cu) {

@@ -715,17 +715,6 @@ hipError_t launch_prefill(int nw, int heads, hipStream_t st, const PrefillParams
   return hipGetLastError();
 }
 
-// CUs of the current device, queried once per device (0 if unknown).
-int device_cus() {
-  constexpr int kMaxDev = 64;
-  static std::atomic<int> cache[kMaxDev];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
-  int c = cache[dev].load(std::memory_order_relaxed);
-  if (c == 0 && hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-    cache[dev].store(c, std::memory_order_relaxed);
-  return c;
-}
 
 // Launch plan of one call: the workgroup shape and, when the grid would
 // leave CUs idle (short chunks over long contexts), a split of the keys.

@@ -15,6 +15,8 @@
 
 #include <type_traits>
 
+#include <atomic>
+
 #include "tq_common.h"
 
 namespace tq {
@@ -650,6 +652,17 @@ void set_error(const char* fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
+}
+
+int device_cus() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cache[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0 && hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+    cache[dev].store(c, std::memory_order_relaxed);
+  return c;
 }
 
 }  // namespace tq
