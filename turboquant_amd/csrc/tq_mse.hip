@@ -22,9 +22,10 @@
 // chunks of 8 consecutive dims, chunk i of lane p being dims 8 (p + P i) ..
 // + 7 (the lanes of a vector then write neighbouring 32-byte pieces of its
 // row).  FWHT stages of stride 1, 2, 4 run inside a chunk, strides 8 ..
-// 4P across lanes as one fma each, z = sg * z + partner with sg = -1 on the
-// upper lane (the same rounding as a + b or a - b), and the larger strides
-// between a lane's chunks.  The per-vector work (the
+// 4P across lanes as one fma with a DPP operand each, z + sg * partner with
+// sg = -1 on the upper lane (a + b, or a - b negated: the same rounding; the
+// sign is folded into the 1/sqrt(pd) scale, see tau_scale), and the larger
+// strides between a lane's chunks.  The per-vector work (the
 // norm's sqrt and its correctly rounded reciprocal) is shared by the P lanes
 // and each lane's codes pack in its own registers.  HBM-bound in bytes:
 // 4 dim + pd*b/8 + 4 per vector.
@@ -85,6 +86,48 @@ __device__ __forceinline__ float lane_xor(float v, int m) {
   }
 }
 
+// x[k] += sg * (x[k] of lane l ^ M) for 8 registers, M in {1, 2, 8}: one
+// v_fmac_f32 with a DPP operand each (quad permute, or row rotate by 8),
+// one rounding.  The leading s_nop covers the wait states a DPP read needs
+// after a VALU write of its source; no instruction of the batch reads a
+// register another one writes.
+template <int M>
+__device__ __forceinline__ void fmac_xor8(float* x, float sg) {
+  static_assert(M == 1 || M == 2 || M == 8, "DPP distance");
+#if defined(__HIP_DEVICE_COMPILE__)
+#define TQ_F(I, CTL) "v_fmac_f32_dpp %" #I ", %" #I ", %8 " CTL " row_mask:0xf bank_mask:0xf\n\t"
+#define TQ_F8(CTL)                                                                          \
+  asm volatile("s_nop 1\n\t" TQ_F(0, CTL) TQ_F(1, CTL) TQ_F(2, CTL) TQ_F(3, CTL)           \
+                   TQ_F(4, CTL) TQ_F(5, CTL) TQ_F(6, CTL) TQ_F(7, CTL)                       \
+               : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),     \
+                 "+v"(x[6]), "+v"(x[7])                                                      \
+               : "v"(sg))
+  if constexpr (M == 1) TQ_F8("quad_perm:[1,0,3,2]");
+  else if constexpr (M == 2) TQ_F8("quad_perm:[2,3,0,1]");
+  else TQ_F8("row_ror:8");
+#undef TQ_F8
+#undef TQ_F
+#else
+  for (int k = 0; k < 8; k++) x[k] = __builtin_fmaf(lane_xor(x[k], M), sg, x[k]);
+#endif
+}
+
+// one cross-lane stage over E registers: v += sg * v of lane l ^ m
+template <int E>
+__device__ __forceinline__ void fmac_xor(float (&v)[E], int m, float sg) {
+  static_assert(E % 8 == 0, "registers in batches of 8");
+#pragma unroll
+  for (int b = 0; b < E; b += 8) {
+    if (m == 1) fmac_xor8<1>(v + b, sg);
+    else if (m == 2) fmac_xor8<2>(v + b, sg);
+    else if (m == 8) fmac_xor8<8>(v + b, sg);
+    else {
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[b + k] = __builtin_fmaf(lane_xor(v[b + k], m), sg, v[b + k]);
+    }
+  }
+}
+
 // Walsh-Hadamard transform (unnormalised, ascending stride) of the PD dims
 // the P lanes of a vector hold: v[8 i + c] = dim 8 (p + P i) + c.
 template <int E, int P>
@@ -100,9 +143,8 @@ __device__ __forceinline__ void fwht_group(float (&v)[E], int p) {
       }
 #pragma unroll
   for (int m = 1; m < P; m <<= 1) {
-    const float sg = (p & m) ? -1.0f : 1.0f;  // upper lane keeps partner - own
-#pragma unroll
-    for (int i = 0; i < E; i++) v[i] = __builtin_fmaf(sg, v[i], lane_xor(v[i], m));
+    const float sg = (p & m) ? -1.0f : 1.0f;  // own + sg * partner: one v_fmac with DPP
+    fmac_xor<E>(v, m, sg);
   }
 #pragma unroll
   for (int h = 8; h < E; h <<= 1)  // chunk index bits: stride 8 P h / 8
@@ -132,9 +174,19 @@ __device__ __forceinline__ void fwht_contig(float (&v)[E], int p) {
 #pragma unroll
   for (int m = 1; m < P; m <<= 1) {
     const float sg = (p & m) ? -1.0f : 1.0f;
-#pragma unroll
-    for (int i = 0; i < E; i++) v[i] = __builtin_fmaf(sg, v[i], lane_xor(v[i], m));
+    fmac_xor<E>(v, m, sg);
   }
+}
+
+// Both transforms leave lane p with tau_p times the reference's values, tau_p
+// = (-1)^popcount(p): a cross-lane stage keeps own + sg * partner, which on
+// the upper lane is own - partner = -(partner - own), the reference's value
+// negated (exactly); lanes paired in a stage share tau from the earlier
+// stages, and negation commutes with the in-lane stages.  The scale 1/sqrt(pd)
+// then takes tau: (tau v) * (tau s) == v * s bit for bit.
+template <int P>
+__device__ __forceinline__ float tau_scale(float inv_sqrt_pd, int p) {
+  return (__builtin_popcount(p & (P - 1)) & 1) ? -inv_sqrt_pd : inv_sqrt_pd;
 }
 
 // fp32 value with the sign of a +-1 sign value folded in (exact: s * v)
@@ -258,12 +310,13 @@ __device__ __forceinline__ void quantize_row(const MseParams& p, const float* bn
     v[i] = apply_sign(__builtin_fmaf(r, yr, q), sgn[i]);
   }
   fwht_contig<E, P>(v, sub);
+  const float ts = tau_scale<P>(p.inv_sqrt_pd, sub);  // v holds tau * FWHT
   // code = #{j : b_j < y}
   uint32_t word[(NB + 3) / 4] = {};
   auto encode = [&](auto code_of) {
 #pragma unroll
     for (int i = 0; i < E; i++) {
-      const int c = code_of(v[i] * p.inv_sqrt_pd);
+      const int c = code_of(v[i] * ts);
       const int byte = i / PER, slot = i % PER;
       word[byte / 4] |= (uint32_t)c << (8 * (byte % 4) + BITS * slot);
       if constexpr (RES) v[i] = cen[c];
@@ -278,7 +331,7 @@ __device__ __forceinline__ void quantize_row(const MseParams& p, const float* bn
     float rs = 0.0f;
 #pragma unroll
     for (int i = 0; i < E; i++) {
-      const float xh = apply_sign(v[i] * p.inv_sqrt_pd, sgn[i]) * nrm;
+      const float xh = apply_sign(v[i] * ts, sgn[i]) * nrm;
       v[i] = d0 + i < p.dim ? xo[i] - xh : 0.0f;
       rs = __builtin_fmaf(v[i], v[i], rs);
     }
@@ -397,6 +450,7 @@ __device__ __forceinline__ void dequantize_row(const MseParams& p, const float* 
     v[i] = cen[(word[i / 8] >> (8 * (k / PER) + BITS * (k % PER))) & kMask];
   }
   fwht_group<E, P>(v, sub);
+  const float ts = tau_scale<P>(p.inv_sqrt_pd, sub);  // v holds tau * FWHT
   if (!live) return;
   float* orow = p.out + row * p.dim;
   const float wq = ADD ? p.add_scale * p.gamma[row] : 0.0f;
@@ -417,7 +471,7 @@ __device__ __forceinline__ void dequantize_row(const MseParams& p, const float* 
   }
   auto val = [&](int i) {
     const int d = 8 * (sub + P * (i / 8)) + i % 8;
-    const float xm = apply_sign(v[i] * p.inv_sqrt_pd, sg[i]) * nrm;
+    const float xm = apply_sign(v[i] * ts, sg[i]) * nrm;
     if constexpr (ADD) return xm + arow[d] * wq;
     else return xm;
   };
