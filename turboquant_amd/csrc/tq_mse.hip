@@ -434,7 +434,8 @@ __device__ __forceinline__ RowCodes<PD, BITS> load_codes(const MseParams& p, int
 template <int PD, int BITS, bool ADD>
 __device__ __forceinline__ void dequantize_row(const MseParams& p, const float* cen, int64_t row,
                                                int sub, const float* arow,
-                                               const RowCodes<PD, BITS>& rc) {
+                                               const RowCodes<PD, BITS>& rc,
+                                               float* stage = nullptr) {
 #pragma clang fp contract(off)
   using MG = MseGeom<PD>;
   constexpr int P = MG::P, E = MG::E, NC = E / 8;
@@ -476,9 +477,11 @@ __device__ __forceinline__ void dequantize_row(const MseParams& p, const float* 
     else return xm;
   };
   if (p.dim == PD) {
+    // into the row's LDS stage (the caller writes it out coalesced), or HBM
+    float* const dst = stage ? stage : orow;
 #pragma unroll
     for (int i = 0; i < NC; i++) {
-      float4* o4 = reinterpret_cast<float4*>(orow + 8 * (sub + P * i));
+      float4* o4 = reinterpret_cast<float4*>(dst + 8 * (sub + P * i));
       o4[0] = float4{val(8 * i), val(8 * i + 1), val(8 * i + 2), val(8 * i + 3)};
       o4[1] = float4{val(8 * i + 4), val(8 * i + 5), val(8 * i + 6), val(8 * i + 7)};
     }
@@ -491,18 +494,40 @@ __device__ __forceinline__ void dequantize_row(const MseParams& p, const float* 
   }
 }
 
+// Full-width rows (dim == pd) go out through an LDS stage per wave: the
+// wave's 64 / P rows are consecutive in memory, so each store instruction
+// writes 1 KB of consecutive bytes (64 lanes x 16 B) instead of 16-byte
+// pieces at a 32-byte stride that leave every line half-written.
 template <int PD, int BITS, bool ADD>
 __global__ __launch_bounds__(kMseThreads) void mse_dequantize_kernel(MseParams p) {
   using MG = MseGeom<PD>;
-  constexpr int P = MG::P;
+  constexpr int P = MG::P, VW = 64 / P;  // vectors per wave
   __shared__ float cen[16];
+  __shared__ __attribute__((aligned(16))) float stg[kMseThreads / 64][VW * PD];
   if (threadIdx.x < 16) cen[threadIdx.x] = p.table[threadIdx.x];
   __syncthreads();
-  const int sub = (threadIdx.x & 63) % P;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int sub = lane % P, vw = lane / P;
   const int64_t row = (int64_t)blockIdx.x * MG::VPB + threadIdx.x / P;
+  const bool staged = p.dim == PD;  // uniform
   dequantize_row<PD, BITS, ADD>(p, cen, row, sub,
                                 ADD && row < p.n ? p.add + row * p.dim : nullptr,
-                                load_codes<PD, BITS>(p, row, sub));
+                                load_codes<PD, BITS>(p, row, sub),
+                                staged ? &stg[w][vw * PD] : nullptr);
+  if (!staged) return;
+  // LDS operations of one wave complete in order; the wave barrier keeps the
+  // compiler from moving the reads above the writes
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int64_t row0 = (int64_t)blockIdx.x * MG::VPB + (int64_t)w * VW;
+  const int64_t rows = p.n - row0 < VW ? p.n - row0 : VW;
+  if (rows <= 0) return;
+  const int total = (int)rows * PD;  // floats of the wave's live rows
+  float* const dst = p.out + row0 * PD;
+#pragma unroll
+  for (int k = 4 * lane; k < VW * PD; k += 256)
+    if (k < total) *reinterpret_cast<float4*>(dst + k) = *reinterpret_cast<const float4*>(&stg[w][k]);
 }
 
 // --------------------------------------------------------------------------
@@ -716,7 +741,28 @@ __global__ __launch_bounds__(kMseThreads) void prod_qjl_dequantize_kernel(MsePar
     }
     __syncthreads();
     const int64_t row = bt * 32 + vl;
-    dequantize_row<PD, BITS, true>(p, cen, row, sub, term + vl * TS, cc);
+    // full-width rows: each lane overwrites its own dims of the term row with
+    // the output, and the wave writes its 8 consecutive rows out coalesced
+    const bool staged = p.dim == PD;  // uniform
+    dequantize_row<PD, BITS, true>(p, cen, row, sub, term + vl * TS, cc,
+                                   staged ? term + vl * TS : nullptr);
+    if (staged) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      constexpr int VW = 64 / P;
+      const int64_t row0 = bt * 32 + (int64_t)w * VW;
+      const int64_t rows = p.n - row0 < VW ? p.n - row0 : VW;
+      if (rows > 0) {
+        const int total = (int)rows * PD;
+        float* const dst = p.out + row0 * PD;
+#pragma unroll
+        for (int k = 4 * lane; k < VW * PD; k += 256)
+          if (k < total)
+            *reinterpret_cast<float4*>(dst + k) = *reinterpret_cast<const float4*>(
+                term + (w * VW + k / PD) * TS + k % PD);
+      }
+    }
     __syncthreads();  // the next batch rewrites the tile
   }
 }
