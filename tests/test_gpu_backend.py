@@ -184,6 +184,14 @@ def test_dequant_paged_matches_float64_dequantization():
                 g = got[:333, kvh].float().cpu().numpy()
                 assert np.abs(g - want).max() <= 2e-3 * max(1.0, np.abs(want).max()), hd
         assert (out_k[333:] == 7.0).all()  # rows past num_tokens untouched
+        # rows with a wider stride (not packed): the same values, bit for bit
+        wide_k = torch.full((340, hkv + 1, hd), 7.0, dtype=torch.float16, device=G.DEV)
+        wide_v = torch.full_like(wide_k, 7.0)
+        ops.dequant_paged(cache, pages, 333, hkv, hd, pd, signs, wide_k[:, :hkv], wide_v[:, :hkv])
+        torch.cuda.synchronize()
+        assert torch.equal(wide_k[:333, :hkv], out_k[:333])
+        assert torch.equal(wide_v[:333, :hkv], out_v[:333])
+        assert (wide_k[:, hkv:] == 7.0).all() and (wide_k[333:] == 7.0).all()
 
 
 def test_backend_decode_batches_beyond_one_balanced_plan():

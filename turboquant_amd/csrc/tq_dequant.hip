@@ -102,9 +102,15 @@ __global__ __launch_bounds__(256) void dequant_kernel(
     }
   }
   __syncthreads();  // codebook ready
+  // packed full rows (row stride H * head_dim): a wave's 64 / L vectors are
+  // 4 KB of consecutive output, staged in LDS and written with whole-wave
+  // 1 KB stores instead of 16-byte pieces at a 64-byte stride
+  __shared__ __attribute__((aligned(16))) _Float16 stage[VPB / (64 / L)][64 * 32];
+  const bool packed = vec_store && out_stride_tok == (int64_t)H * head_dim;  // uniform
+  const int wv = threadIdx.x >> 6;
 #pragma unroll 1
   for (int j = 0; j < NV; j++) {
-    if (tv[j] < 0) continue;  // whole vector (L lanes of one DPP row) together
+    if (!packed && tv[j] < 0) continue;  // whole vector (L lanes of one DPP row) together
     float y[32];  // dims 32 * lane + i
     const float sc = nrm[j] * (1.0f / __builtin_sqrtf((float)PD));
 #pragma unroll
@@ -135,6 +141,38 @@ __global__ __launch_bounds__(256) void dequant_kernel(
       if constexpr (L >= 8) cross(std::integral_constant<int, 4>{});
 #pragma unroll
       for (int i = 0; i < 32; i++) y[i] = y[i] * sg[i];
+    }
+    if (packed) {
+      typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+      _Float16* st = &stage[wv][32 * (threadIdx.x & 63)];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        h8 o;
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = (_Float16)y[8 * c + i];
+        *reinterpret_cast<h8*>(st + 8 * c) = o;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // the wave's vectors: vec0 .. vec0 + 64 / L - 1, the live ones first
+      const int64_t vec0 = ((int64_t)blockIdx.x * NV + j) * VPB + (int64_t)wv * (64 / L);
+      const int64_t live = nvec - vec0 < 64 / L ? nvec - vec0 : 64 / L;
+      if (live > 0) {
+        const int bytes = (int)live * head_dim * 2;
+        uint8_t* const dst0 = reinterpret_cast<uint8_t*>(out + vec0 * head_dim);
+        const uint8_t* const src0 = reinterpret_cast<const uint8_t*>(&stage[wv][0]);
+        const int lb = 16 * (threadIdx.x & 63);
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          if (lb + 1024 * k < bytes)
+            *reinterpret_cast<u32x4*>(dst0 + lb + 1024 * k) =
+                *reinterpret_cast<const u32x4*>(src0 + lb + 1024 * k);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();  // the next vectors rewrite the stage
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      continue;
     }
     _Float16* dst = out + tv[j] * out_stride_tok + (int64_t)hv[j] * head_dim + 32 * lane;
     if (vec_store) {  // 8 dims per 16-byte store
