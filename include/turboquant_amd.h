@@ -321,7 +321,8 @@ int tq_prod_dequantize(const uint8_t* packed, const float* norms, const float* q
  * qjl.py:36-63 in one kernel each.  s_hi / s_lo (quantize) are the QJL
  * matrix S [dim, dim] as fp16 halves with S = hi + lo to 22 bits, zero-padded
  * to [padded_dim, padded_dim], row-major; st_hi / st_lo (dequantize) the same
- * of S^T.  16-byte aligned device arrays.
+ * of S^T.  16-byte aligned device arrays; qjl_signs 8-byte aligned (its
+ * rows are read and written in 4- and 8-byte pieces when dim allows).
  *
  * tq_prod_quantize_qjl: tq_prod_quantize's packed, norms and residual_norms,
  *   and qjl_signs int8 [num_vectors, dim] = +1 where (S r)_j >= 0, else -1,

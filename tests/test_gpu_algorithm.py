@@ -180,6 +180,14 @@ def test_prod_hip_kernels_against_the_torch_path(dim, bits):
         fused = ops.prod_dequantize_qjl(pg, ng, zg, rg, dim, pd, bits - 1,
                                         qg.mse.rotation.signs, cen, th, tl)
         assert torch.equal(xh, fused)
+        # the signs at an odd address (a view one byte into a buffer): the op
+        # copies them to an aligned tensor, same result
+        buf = torch.empty(zg.numel() + 1, dtype=torch.int8, device=zg.device)
+        zodd = buf[1:].view(zg.shape)
+        zodd.copy_(zg)
+        assert zodd.data_ptr() % 8 != 0
+        assert torch.equal(xh, ops.prod_dequantize_qjl(pg, ng, zodd, rg, dim, pd, bits - 1,
+                                                       qg.mse.rotation.signs, cen, th, tl))
         err = (xh - want).abs().max().item()
         print(f"  fused dequantize max |diff| from the fp32 GEMM expression {err:.2e}", flush=True)
         assert torch.allclose(xh, want, rtol=1e-5, atol=1e-5 * want.abs().max().item())

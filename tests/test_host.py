@@ -383,6 +383,15 @@ def test_prod_entry_points_refuse_bad_arguments():
     assert b"null pointer" in lib.tq_last_error()
     assert lib.tq_prod_dequantize_qjl(one, one, one, one, 0, 128, 128, 3, one, tab, one, one,
                                       one, null) == 0
+    # qjl_signs rows are read and written in 4- and 8-byte pieces: the base
+    # must be 8-byte aligned
+    odd = ctypes.c_void_p(20)
+    assert lib.tq_prod_quantize_qjl(one, 4, 128, 128, 3, one, tab, tab, one, one, one, one, odd,
+                                    one, null) == -22
+    assert b"8-byte aligned" in lib.tq_last_error()
+    assert lib.tq_prod_dequantize_qjl(one, one, odd, one, 4, 128, 128, 3, one, tab, one, one,
+                                      one, null) == -22
+    assert b"8-byte aligned" in lib.tq_last_error()
 
 
 def test_ops_refuse_tensors_on_two_devices():

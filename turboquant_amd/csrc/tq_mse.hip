@@ -966,6 +966,10 @@ int prod_qjl_call(bool quant, const float* x, uint8_t* packed, float* norms, flo
     set_error("%s: x / out, packed, signs and the S halves must be 16-byte aligned", what);
     return kEinval;
   }
+  if ((((uintptr_t)z | (uintptr_t)zin) & 7) != 0) {
+    set_error("%s: qjl_signs must be 8-byte aligned", what);
+    return kEinval;
+  }
   const int per = bits == 3 ? 2 : 8 / bits;
   MseParams p;
   p.x = x;

@@ -493,7 +493,7 @@ def prod_dequantize_qjl(packed: torch.Tensor, norms: torch.Tensor, qjl_signs: to
         packed = packed.clone()
     nf = norms.to(torch.float32).contiguous()
     rn = residual_norms.to(torch.float32).contiguous()
-    z = qjl_signs.contiguous()
+    z = _aligned16(qjl_signs)
     out = torch.empty((*lead, dim), dtype=torch.float32, device=packed.device)
     signs = _aligned16(signs)
     lib = _lib.load()
