@@ -356,15 +356,18 @@ int tq_prod_dequantize_qjl(const uint8_t* packed, const float* norms, const int8
  *   then kv heads, then the v part, row stride qkv_row_stride elements):
  *   RMSNorm over the head's dims with q_w or k_w, rounded to fp16, then
  *   rotate-half RoPE with row positions[t] of the fp16 cos / signed-sin
- *   tables [*, head_dim]: out[i] = n[i] cos[i] + n[(i + D/2) mod D] sin[i].
- *   q_out [tokens, q_heads, D], k_out [tokens, kv_heads, D].  D even, <= 256.
+ *   tables [table_rows, head_dim]: out[i] = n[i] cos[i] + n[(i + D/2) mod D]
+ *   sin[i].  q_out [tokens, q_heads, D], k_out [tokens, kv_heads, D].  D
+ *   even, <= 256.  A position outside [0, table_rows) gives NaN rows for its
+ *   token (the positions live on the device; nothing is read past the tables).
  * tq_e2e_silu_mul: out[t, i] = silu(gate_up[t, i]) * gate_up[t, inter + i].
  */
 int tq_e2e_add_rms_norm(void* x, const void* y, const void* w, void* h, int64_t rows,
                         int32_t hidden, float eps, tq_stream_t stream);
 int tq_e2e_qk_norm_rope(const void* qkv, int64_t qkv_row_stride, const void* q_w,
                         const void* k_w, const void* cos_table, const void* sin_table,
-                        const int64_t* positions, int64_t tokens, int32_t q_heads,
+                        int64_t table_rows, const int64_t* positions, int64_t tokens,
+                        int32_t q_heads,
                         int32_t kv_heads, int32_t head_dim, float eps, void* q_out,
                         void* k_out, tq_stream_t stream);
 int tq_e2e_silu_mul(const void* gate_up, void* out, int64_t rows, int32_t inter,

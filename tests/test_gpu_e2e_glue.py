@@ -70,6 +70,17 @@ def test_qk_norm_rope(tokens, hq, hkv, d):
     assert err_q < 8e-3 and err_k < 8e-3
     assert torch.allclose(q.float(), want_q, rtol=4e-3, atol=4e-3)
     assert torch.allclose(k.float(), want_k, rtol=4e-3, atol=4e-3)
+    # a position past the tables (or negative) gives NaN rows for that token
+    # only, and no read outside the tables
+    if tokens > 2:
+        bad = pos.clone()
+        bad[0], bad[2] = 40000, -1
+        q2, k2 = e2e.qk_norm_rope(qkv, s, qw, kw, cos, sin, bad)
+        for t in (0, 2):
+            assert torch.isnan(q2[t]).all() and torch.isnan(k2[t]).all()
+        keep = torch.ones(tokens, dtype=torch.bool, device="cuda")
+        keep[0] = keep[2] = False
+        assert torch.equal(q2[keep], q[keep]) and torch.equal(k2[keep], k[keep])
 
 
 @pytest.mark.parametrize("rows,inter", [(1, 12288), (33, 12288), (100, 1024), (3, 8)])

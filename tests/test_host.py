@@ -427,13 +427,16 @@ def test_e2e_glue_entry_points_refuse_bad_arguments():
                                    None) == -22
     assert b"aligned" in lib.tq_last_error()
     assert lib.tq_e2e_add_rms_norm(None, None, None, None, 0, 4096, 1e-6, None) == 0
-    assert lib.tq_e2e_qk_norm_rope(one, 6144, one, one, one, one, one, 4, 32, 8, 97, 1e-6,
+    assert lib.tq_e2e_qk_norm_rope(one, 6144, one, one, one, one, 100, one, 4, 32, 8, 97, 1e-6,
                                    one, one, None) == -22
     assert b"head_dim" in lib.tq_last_error()
-    assert lib.tq_e2e_qk_norm_rope(one, 1000, one, one, one, one, one, 4, 32, 8, 128, 1e-6,
+    assert lib.tq_e2e_qk_norm_rope(one, 1000, one, one, one, one, 100, one, 4, 32, 8, 128, 1e-6,
                                    one, one, None) == -22
-    assert lib.tq_e2e_qk_norm_rope(one, 6144, one, one, None, one, one, 4, 32, 8, 128, 1e-6,
+    assert lib.tq_e2e_qk_norm_rope(one, 6144, one, one, None, one, 100, one, 4, 32, 8, 128, 1e-6,
                                    one, one, None) == -22
+    assert lib.tq_e2e_qk_norm_rope(one, 6144, one, one, one, one, -1, one, 4, 32, 8, 128, 1e-6,
+                                   one, one, None) == -22
+    assert b"geometry" in lib.tq_last_error()
     assert lib.tq_e2e_silu_mul(one, one, 4, 12, None) == -22
     assert lib.tq_e2e_silu_mul(one, None, 4, 16, None) == -22
     assert lib.tq_e2e_silu_mul(None, None, 0, 16, None) == 0

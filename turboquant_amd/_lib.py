@@ -59,13 +59,13 @@ SIGNATURES = {
                                       _P, _P]),
     "tq_diag_mse_bucketize": (_I32, [_I32]),
     "tq_e2e_add_rms_norm": (_I32, [_P, _P, _P, _P, _I64, _I32, _F32, _P]),
-    "tq_e2e_qk_norm_rope": (_I32, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _F32,
-                                   _P, _P, _P]),
+    "tq_e2e_qk_norm_rope": (_I32, [_P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32,
+                                   _F32, _P, _P, _P]),
     "tq_e2e_silu_mul": (_I32, [_P, _P, _I64, _I32, _P]),
     "tq_last_error": (ctypes.c_char_p, []),
     "tq_abi_version": (_I32, []),
 }
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib = None
 

@@ -80,8 +80,9 @@ template <int D>
 __global__ __launch_bounds__(kGlueThreads) void qk_norm_rope_kernel(
     const _Float16* __restrict__ qkv, int64_t qkv_st, const _Float16* __restrict__ qw,
     const _Float16* __restrict__ kw, const _Float16* __restrict__ cosb,
-    const _Float16* __restrict__ sinb, const int64_t* __restrict__ pos, int64_t tokens,
-    int hq, int hkv, float eps, _Float16* __restrict__ qo, _Float16* __restrict__ ko) {
+    const _Float16* __restrict__ sinb, int64_t trows, const int64_t* __restrict__ pos,
+    int64_t tokens, int hq, int hkv, float eps, _Float16* __restrict__ qo,
+    _Float16* __restrict__ ko) {
   constexpr int V = D / 64;
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * (kGlueThreads / 64) + (threadIdx.x >> 6);
@@ -107,10 +108,15 @@ __global__ __launch_bounds__(kGlueThreads) void qk_norm_rope_kernel(
 #pragma unroll
   for (int e = 0; e < V; e++) pn[e] = __shfl_xor(n[e], 32);
   const int64_t p = pos[t];
-  const _Float16* cr = cosb + p * D + V * lane;
-  const _Float16* sr = sinb + p * D + V * lane;
   _Float16* dst = isq ? qo + (t * hq + hd) * D + V * lane
                       : ko + (t * hkv + (hd - hq)) * D + V * lane;
+  if (p < 0 || p >= trows) {  // no table row: NaN rows, no read past the tables
+#pragma unroll
+    for (int e = 0; e < V; e++) dst[e] = (_Float16)__builtin_nanf("");
+    return;
+  }
+  const _Float16* cr = cosb + p * D + V * lane;
+  const _Float16* sr = sinb + p * D + V * lane;
 #pragma unroll
   for (int e = 0; e < V; e++)
     dst[e] = (_Float16)(__builtin_fmaf(pn[e], (float)sr[e], n[e] * (float)cr[e]));
@@ -121,8 +127,9 @@ __global__ __launch_bounds__(kGlueThreads) void qk_norm_rope_kernel(
 __global__ __launch_bounds__(kGlueThreads) void qk_norm_rope_any_kernel(
     const _Float16* __restrict__ qkv, int64_t qkv_st, const _Float16* __restrict__ qw,
     const _Float16* __restrict__ kw, const _Float16* __restrict__ cosb,
-    const _Float16* __restrict__ sinb, const int64_t* __restrict__ pos, int64_t tokens,
-    int hq, int hkv, int D, float eps, _Float16* __restrict__ qo, _Float16* __restrict__ ko) {
+    const _Float16* __restrict__ sinb, int64_t trows, const int64_t* __restrict__ pos,
+    int64_t tokens, int hq, int hkv, int D, float eps, _Float16* __restrict__ qo,
+    _Float16* __restrict__ ko) {
   constexpr int kMaxV = 4;
   __shared__ float row[kGlueThreads / 64][256];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -154,10 +161,13 @@ __global__ __launch_bounds__(kGlueThreads) void qk_norm_rope_any_kernel(
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const int64_t p = pos[t];
   _Float16* dst = isq ? qo + (t * hq + hd) * D : ko + (t * hkv + (hd - hq)) * D;
+  const bool inside = p >= 0 && p < trows;  // else NaN rows, no read past the tables
 #pragma unroll
   for (int e = 0; e < kMaxV; e++) {
     const int i = lane + 64 * e;
-    if (i < D) {
+    if (i < D && !inside) {
+      dst[i] = (_Float16)__builtin_nanf("");
+    } else if (i < D) {
       const float n = row[w][i], pn = row[w][(i + D / 2) % D];
       dst[i] = (_Float16)(__builtin_fmaf(pn, (float)sinb[p * D + i], n * (float)cosb[p * D + i]));
     }
@@ -220,15 +230,16 @@ extern "C" int tq_e2e_add_rms_norm(void* x, const void* y, const void* w, void* 
 
 extern "C" int tq_e2e_qk_norm_rope(const void* qkv, int64_t qkv_row_stride, const void* q_w,
                                    const void* k_w, const void* cos_table,
-                                   const void* sin_table, const int64_t* positions,
-                                   int64_t tokens, int32_t q_heads, int32_t kv_heads,
+                                   const void* sin_table, int64_t table_rows,
+                                   const int64_t* positions, int64_t tokens, int32_t q_heads,
+                                   int32_t kv_heads,
                                    int32_t head_dim, float eps, void* q_out, void* k_out,
                                    tq_stream_t stream) {
   if (head_dim < 2 || head_dim > 256 || head_dim % 2 != 0) {
     tq::set_error("e2e_qk_norm_rope: head_dim %d unsupported (even, up to 256)", head_dim);
     return tq::kEinval;
   }
-  if (tokens < 0 || q_heads <= 0 || kv_heads <= 0 ||
+  if (tokens < 0 || q_heads <= 0 || kv_heads <= 0 || table_rows < 0 ||
       qkv_row_stride < (int64_t)(q_heads + 2 * kv_heads) * head_dim) {
     tq::set_error("e2e_qk_norm_rope: bad geometry");
     return tq::kEinval;
@@ -250,8 +261,8 @@ extern "C" int tq_e2e_qk_norm_rope(const void* qkv, int64_t qkv_row_stride, cons
                      0, st, static_cast<const _Float16*>(qkv), qkv_row_stride,                   \
                      static_cast<const _Float16*>(q_w), static_cast<const _Float16*>(k_w),       \
                      static_cast<const _Float16*>(cos_table),                                    \
-                     static_cast<const _Float16*>(sin_table), positions, tokens, q_heads,        \
-                     kv_heads, eps, static_cast<_Float16*>(q_out), static_cast<_Float16*>(k_out))
+                     static_cast<const _Float16*>(sin_table), table_rows, positions, tokens,     \
+                     q_heads, kv_heads, eps, static_cast<_Float16*>(q_out), static_cast<_Float16*>(k_out))
   if (head_dim == 64) TQ_QKR(64);
   else if (head_dim == 128) TQ_QKR(128);
   else if (head_dim == 256) TQ_QKR(256);
@@ -260,8 +271,8 @@ extern "C" int tq_e2e_qk_norm_rope(const void* qkv, int64_t qkv_row_stride, cons
                        dim3(tq::kGlueThreads), 0, st, static_cast<const _Float16*>(qkv),
                        qkv_row_stride, static_cast<const _Float16*>(q_w),
                        static_cast<const _Float16*>(k_w), static_cast<const _Float16*>(cos_table),
-                       static_cast<const _Float16*>(sin_table), positions, tokens, q_heads,
-                       kv_heads, head_dim, eps, static_cast<_Float16*>(q_out),
+                       static_cast<const _Float16*>(sin_table), table_rows, positions, tokens,
+                       q_heads, kv_heads, head_dim, eps, static_cast<_Float16*>(q_out),
                        static_cast<_Float16*>(k_out));
 #undef TQ_QKR
   const hipError_t e = hipGetLastError();

@@ -668,7 +668,7 @@ int device_cus() {
 }  // namespace tq
 
 extern "C" const char* tq_last_error(void) { return tq::g_err; }
-extern "C" int32_t tq_abi_version(void) { return 8; }
+extern "C" int32_t tq_abi_version(void) { return 9; }
 
 extern "C" int tq_quantize_write_kv_cache(void* k_slab, void* v_slab, const void* key,
                                           const void* value, int32_t in_dtype,

@@ -136,9 +136,11 @@ def qk_norm_rope(qkv: torch.Tensor, shape: "ModelShape", q_w: torch.Tensor, k_w:
     q = torch.empty((t, s.heads, s.head_dim), dtype=torch.float16, device=qkv.device)
     k = torch.empty((t, s.kv_heads, s.head_dim), dtype=torch.float16, device=qkv.device)
     assert qkv.stride(1) == 1 and pos.dtype == torch.int64 and pos.is_contiguous()
+    assert cos.shape == sin.shape and cos.shape[-1] == s.head_dim
+    assert cos.is_contiguous() and sin.is_contiguous()
     rc = _lib.load().tq_e2e_qk_norm_rope(
         qkv.data_ptr(), qkv.stride(0), q_w.data_ptr(), k_w.data_ptr(), cos.data_ptr(),
-        sin.data_ptr(), pos.data_ptr(), t, s.heads, s.kv_heads, s.head_dim, float(s.eps),
+        sin.data_ptr(), cos.shape[0], pos.data_ptr(), t, s.heads, s.kv_heads, s.head_dim, float(s.eps),
         q.data_ptr(), k.data_ptr(), ops._stream_ptr(qkv.device))
     _lib.check(rc, "e2e_qk_norm_rope")
     return q, k
